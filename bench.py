@@ -1,0 +1,219 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path on one MI355X.
+
+The headline line times BASELINE config 2 -- the bf16 GEMM C[4096,12288] = A[4096,4096] @
+B[4096,12288], fp32 accumulation, bf16 C (Qwen3-8B gate/up projection shape) -- as K back-to-back
+launches over inputs resident in HBM, bracketed by torch.cuda.synchronize().  ``value`` is TFLOP/s
+(2*M*N*K flops per step).  The same JSON line carries, under ``kernels``, each other BASELINE config
+measured the same way (RMSNorm GB/s, fp8 GEMM TFLOP/s, flash-attention TFLOP/s, Qwen3-8B layer
+latency), each with its roofline fraction, and ``cpu_baseline`` times the CPU golden (torch-CPU,
+the oracle's arithmetic) on a bounded sample of the headline workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm_bf16,...]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "pytorchsim-triton-backend_amd"))
+sys.path.insert(0, str(REPO))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed(fn, steps: int, warmup: int):
+    """Run fn() warmup times, then time `steps` launches with HIP events on torch's current stream
+    (the stream every ptb_amd op launches on).  Returns (ms per step, wall ms per step)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return start.elapsed_time(stop) / steps, wall
+
+
+def bench_gemm_bf16(steps, warmup):
+    import torch
+    from ptb_amd import ops
+
+    m, k, n = 4096, 4096, 12288
+    g = torch.Generator().manual_seed(0)
+    a = (torch.randn(m, k, generator=g) / 64.0).to(torch.bfloat16).cuda()
+    b = (torch.randn(k, n, generator=g) / 64.0).to(torch.bfloat16).cuda()
+    c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    ms, wall = timed(lambda: ops.gemm(a, b, out=c), steps, warmup)
+    flops = 2.0 * m * n * k
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "name": "gemm_bf16", "config": "BASELINE config 2: bf16 [4096x4096]@[4096x12288]",
+        "us": ms * 1e3, "wall_us": wall * 1e3, "tflops": tf,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tf / PEAK_BF16_TFLOPS},
+        "flops": flops, "_a": a, "_b": b,
+    }
+
+
+def bench_rmsnorm(steps, warmup):
+    import torch
+    from ptb_amd import ops
+
+    rows, cols = 2048, 4096
+    copies = 16   # 16 x 33.5 MB cycles through > the 256 MB last-level cache: every call reads HBM
+    g = torch.Generator().manual_seed(0)
+    xs = [torch.randn(rows, cols, generator=g).to(torch.bfloat16).cuda() for _ in range(copies)]
+    w = (torch.randn(cols, generator=g) * 0.02 + 1.0).cuda()
+    ys = [torch.empty_like(x) for x in xs]
+    it = [0]
+
+    def step():
+        i = it[0] % copies
+        it[0] += 1
+        ops.rmsnorm(xs[i], w, 1e-6, out=ys[i])
+
+    ms, wall = timed(step, steps * 4, warmup)
+    nbytes = 2 * rows * cols * 2 + cols * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"name": "rmsnorm", "config": "BASELINE config 1: x bf16 [2048x4096], w fp32",
+            "us": ms * 1e3, "wall_us": wall * 1e3, "gbs": gbs,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS}}
+
+
+def bench_gemm_fp8(steps, warmup):
+    import torch
+    from ptb_amd import ops
+
+    m, k, n = 2048, 12288, 4096
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn(k, n, generator=g) * 0.02).cuda()
+    wq_t, sw = ops.quant_weight_e4m3(w)
+    xq, sx = ops.quant_rows_e4m3(x)
+    c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    ms, wall = timed(lambda: ops.gemm_fp8(xq, sx, wq_t, sw, out=c), steps, warmup)
+    qms, _ = timed(lambda: ops.quant_rows_e4m3(x), steps, warmup)
+    flops = 2.0 * m * n * k
+    tf = flops / (ms * 1e-3) / 1e12
+    qbytes = m * k * 2 + m * k + m * 4
+    return {"name": "gemm_fp8", "config": "BASELINE config 4: e4m3 [2048x12288]@[12288x4096] + scales",
+            "us": ms * 1e3, "wall_us": wall * 1e3, "tflops": tf,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / PEAK_FP8_TFLOPS},
+            "quantise_us": qms * 1e3, "quantise_gbs": qbytes / (qms * 1e-3) / 1e9}
+
+
+def cpu_baseline_gemm(a, b, sample_rows=256):
+    """The CPU golden for the headline workload: torch-CPU fp32 matmul of the oracle's arithmetic
+    (bf16 operands upcast, fp32 accumulation, one bf16 rounding), on `sample_rows` rows of A against
+    all of B, scaled to TFLOP/s."""
+    import torch
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    a_s = a[:sample_rows].float().cpu()
+    b_f = b.float().cpu()
+    (a_s[:8] @ b_f).to(torch.bfloat16)   # warm
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        (a_s @ b_f).to(torch.bfloat16)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 50:
+            break
+    sec = (time.perf_counter() - t0) / reps
+    flops = 2.0 * sample_rows * b.shape[0] * b.shape[1]
+    return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{sample_rows} of 4096 rows of A @ full B[4096x12288], torch-CPU fp32, "
+                      f"{reps} reps, {sec * 1e3:.1f} ms each"}
+
+
+BENCHES = {
+    "gemm_bf16": bench_gemm_bf16,
+    "rmsnorm": bench_rmsnorm,
+    "gemm_fp8": bench_gemm_fp8,
+}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default="", help="comma-separated subset of " + ",".join(BENCHES))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU sharding of the path is described in DESIGN.md, not benchmarked.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    from ptb_amd import _lib
+
+    _lib.load()   # fail loudly when the HIP library is missing
+    names = [n for n in (args.only.split(",") if args.only else BENCHES) if n]
+    results = {}
+    for name in names:
+        log(f"[bench] {name} ...")
+        results[name] = BENCHES[name](args.steps, args.warmup)
+        r = results[name]
+        log(f"[bench] {name}: {r['us']:.1f} us/launch, roofline frac {r['roofline']['frac']:.3f}")
+
+    head = results.get("gemm_bf16") or next(iter(results.values()))
+    cpu = None
+    if not args.no_cpu and "gemm_bf16" in results:
+        log("[bench] cpu baseline ...")
+        cpu = cpu_baseline_gemm(head["_a"], head["_b"])
+        log(f"[bench] cpu baseline: {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads")
+    kernels = []
+    for r in results.values():
+        kernels.append({k: v for k, v in r.items() if not k.startswith("_")})
+    line = {
+        "metric": "TFLOP/s or GB/s (% MI355X roofline) per kernel; Qwen3-8B layer latency",
+        "value": head.get("tflops", head.get("gbs")),
+        "unit": "TFLOP/s" if "tflops" in head else "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["us"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded randn, BASELINE.json shapes)",
+        "config": {"workload": "BASELINE config 2: bf16 GEMM C[4096,12288] = A[4096,4096] @ B[4096,12288], "
+                               "fp32 accumulation, bf16 C", "M": 4096, "K": 4096, "N": 12288},
+        "roofline": dict(head["roofline"], traffic=None),
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,122 @@
+// Shared device helpers for the gfx950 kernels: bf16/fp8 bit conversions, wave64 and block
+// reductions, status handling.  Written for CDNA4 only (wave64, MFMA, 160 KB LDS).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ptb_amd.h"
+
+#define PTB_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace ptb {
+
+constexpr int kWave = 64;
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+// 128-bit chunk as a native vector: arrays of these stay in registers (HIP's uint4 is a union
+// struct, and private arrays of it are demoted to scratch or LDS).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+// bf16 bits -> fp32 (exact).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (LLVM fptrunc; v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  __bf16 h = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+}
+
+// NaN-propagating max (triton's tl.maximum(..., PropagateNan.ALL)): NaN if either input is NaN.
+__device__ __forceinline__ float max_nan(float a, float b) {
+  return (a != a) ? a : ((b != b) ? b : fmaxf(a, b));
+}
+
+// fp32 -> OCP e4m3fn bits with round-to-nearest-even, following torch's float8_e4m3fn cast:
+// NaN stays NaN (0x7f), magnitudes that round past 448 become NaN, subnormals down to 2^-9.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;              // NaN
+  if (a > 0x43e80000u) return sign | 0x7fu;              // |x| > 464 rounds past 448 (or is inf)
+  if (a < 0x3c800000u) {                                 // |x| < 2^-6: subnormal range, step 2^-9
+    float m = __builtin_rintf(__uint_as_float(a) * 512.0f);  // exact scaling, RNE to integer
+    return sign | uint32_t(m);                           // m == 8 is the smallest normal, 0x08
+  }
+  // normal: keep 3 mantissa bits, RNE on the 20 dropped bits
+  uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  uint32_t e = (r >> 23) - 120u;                         // rebias 127 -> 7
+  uint32_t m = (r >> 20) & 7u;
+  return sign | (e << 3) | m;
+}
+
+// e4m3fn bits -> fp32 (exact).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  uint32_t sign = (b & 0x80u) << 24;
+  uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
+  if (e == 15u && m == 7u) return __uint_as_float(sign | 0x7fc00000u);
+  float v = (e == 0u) ? float(m) * (1.0f / 512.0f) : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return __uint_as_float(__float_as_uint(v) | sign);
+}
+
+// wave64 reductions through cross-lane shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max_nan(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max_nan(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_absmax(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Block reductions for blocks of NW waves; `red` is NW floats of LDS.  Every thread gets the result.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+template <int NW>
+__device__ __forceinline__ float block_max_nan(float v, float* red) {
+  v = wave_max_nan(v);
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) t = max_nan(t, red[i]);
+  __syncthreads();
+  return t;
+}
+
+__host__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+__host__ __forceinline__ int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PTB_OK : int(e);
+}
+
+}  // namespace ptb

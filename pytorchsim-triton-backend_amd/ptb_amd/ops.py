@@ -1,0 +1,185 @@
+"""Tensor-level entry points over the C ABI.
+
+PyTorch is used only as the owner of device memory and of the current HIP stream: each function
+checks device, dtype, shape and contiguity, allocates its outputs (unless ``out=`` is given) and
+calls the HIP kernel through :mod:`ptb_amd._lib` with raw pointers.  No function has a CPU or
+PyTorch-compute fallback.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+E4M3 = torch.float8_e4m3fn
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(t: torch.Tensor, name: str, dtypes, ndim: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must live on the GPU (got {t.device})")
+    if t.dtype not in (dtypes if isinstance(dtypes, tuple) else (dtypes,)):
+        raise TypeError(f"{name} has dtype {t.dtype}, expected {dtypes}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+
+
+def _out(out, shape, dtype, like: torch.Tensor, name="out") -> torch.Tensor:
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=like.device)
+    _need(out, name, dtype)
+    if tuple(out.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(out.shape)}, expected {tuple(shape)}")
+    return out
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6, out=None) -> torch.Tensor:
+    """y = bf16(x * rsqrt(mean(x^2) + eps) * w) over the last dim of a 2-D bf16 x."""
+    _need(x, "x", BF16, 2)
+    _need(w, "w", (BF16, F32), 1)
+    rows, cols = x.shape
+    if w.numel() != cols:
+        raise ValueError(f"w has {w.numel()} elements, x rows have {cols}")
+    y = _out(out, (rows, cols), BF16, x)
+    wd = _lib.PTB_DTYPE_F32 if w.dtype == F32 else _lib.PTB_DTYPE_BF16
+    _lib.call("ptb_rmsnorm_bf16", x.data_ptr(), w.data_ptr(), wd, y.data_ptr(), rows, cols, float(eps), _stream(x))
+    return y
+
+
+def softmax_rows(x: torch.Tensor, out=None) -> torch.Tensor:
+    _need(x, "x", BF16, 2)
+    y = _out(out, tuple(x.shape), BF16, x)
+    _lib.call("ptb_softmax_rows_bf16", x.data_ptr(), y.data_ptr(), x.shape[0], x.shape[1], _stream(x))
+    return y
+
+
+def silu_mul(gate_up: torch.Tensor, out=None) -> torch.Tensor:
+    """[T, 2I] (gate | up) -> [T, I]: silu(gate) * up."""
+    _need(gate_up, "gate_up", BF16, 2)
+    rows, two_i = gate_up.shape
+    if two_i % 2:
+        raise ValueError("gate_up's last dim must be even (gate | up)")
+    y = _out(out, (rows, two_i // 2), BF16, gate_up)
+    _lib.call("ptb_silu_mul_bf16", gate_up.data_ptr(), y.data_ptr(), rows, two_i // 2, _stream(gate_up))
+    return y
+
+
+def transpose_heads(x: torch.Tensor, out=None) -> torch.Tensor:
+    """[A, B, D] -> [B, A, D] (exact)."""
+    _need(x, "x", BF16, 3)
+    a, b, d = x.shape
+    y = _out(out, (b, a, d), BF16, x)
+    _lib.call("ptb_transpose_heads_bf16", x.data_ptr(), y.data_ptr(), a, b, d, _stream(x))
+    return y
+
+
+def qk_norm_rope(x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float = 1e-6,
+                 out=None) -> torch.Tensor:
+    """x [T, H, D] -> per-head RMSNorm(w) + rotate-half RoPE -> [H, T, D]."""
+    _need(x, "x", BF16, 3)
+    _need(w, "w", BF16, 1)
+    _need(cos, "cos", F32, 2)
+    _need(sin, "sin", F32, 2)
+    t, h, d = x.shape
+    if w.numel() != d or tuple(cos.shape) != (t, d) or tuple(sin.shape) != (t, d):
+        raise ValueError("w must be [D] and cos/sin [T, D]")
+    y = _out(out, (h, t, d), BF16, x)
+    _lib.call("ptb_qk_norm_rope_bf16", x.data_ptr(), w.data_ptr(), cos.data_ptr(), sin.data_ptr(), y.data_ptr(),
+              t, h, d, float(eps), _stream(x))
+    return y
+
+
+def reduce(x: torch.Tensor, op: str = "sum", out=None, workspace=None) -> torch.Tensor:
+    """Whole-tensor sum or max of a bf16 tensor, as one fp32 value (shape [1])."""
+    _need(x, "x", BF16)
+    code = {"sum": _lib.PTB_REDUCE_SUM, "max": _lib.PTB_REDUCE_MAX}[op]
+    y = _out(out, (1,), F32, x)
+    need = _lib.load().ptb_reduce_workspace_bytes(x.numel())
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _lib.call("ptb_reduce_bf16", x.data_ptr(), y.data_ptr(), x.numel(), code, workspace.data_ptr(),
+              workspace.numel() * workspace.element_size(), _stream(x))
+    return y
+
+
+def add_scalar(x: torch.Tensor, s: float, out=None) -> torch.Tensor:
+    _need(x, "x", BF16)
+    y = _out(out, tuple(x.shape), BF16, x)
+    _lib.call("ptb_add_scalar_bf16", x.data_ptr(), y.data_ptr(), x.numel(), float(s), _stream(x))
+    return y
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, residual: torch.Tensor | None = None, out=None) -> torch.Tensor:
+    """C = A[M,K] @ B[K,N] (+ residual[M,N]), bf16 operands, fp32 accumulation, bf16 C."""
+    _need(a, "a", BF16, 2)
+    _need(b, "b", BF16, 2)
+    m, k = a.shape
+    k2, n = b.shape
+    if k != k2:
+        raise ValueError(f"inner dims differ: a is {tuple(a.shape)}, b is {tuple(b.shape)}")
+    rp = 0
+    if residual is not None:
+        _need(residual, "residual", BF16, 2)
+        if tuple(residual.shape) != (m, n):
+            raise ValueError("residual must be [M, N]")
+        rp = residual.data_ptr()
+    c = _out(out, (m, n), BF16, a)
+    _lib.call("ptb_gemm_bf16", a.data_ptr(), b.data_ptr(), rp, c.data_ptr(), m, n, k, _stream(a))
+    return c
+
+
+def quant_rows_e4m3(x: torch.Tensor):
+    """Per-row dynamic e4m3 quantisation: (xq [R,C] float8_e4m3fn, scale [R] fp32)."""
+    _need(x, "x", BF16, 2)
+    rows, cols = x.shape
+    xq = torch.empty((rows, cols), dtype=E4M3, device=x.device)
+    sc = torch.empty((rows,), dtype=F32, device=x.device)
+    _lib.call("ptb_quant_rows_e4m3", x.data_ptr(), xq.data_ptr(), sc.data_ptr(), rows, cols, _stream(x))
+    return xq, sc
+
+
+def quant_weight_e4m3(w: torch.Tensor):
+    """Per-output-channel e4m3 quantisation of fp32 W[K,N]: (wq_t [N,K] float8_e4m3fn, scale [N] fp32)."""
+    _need(w, "w", F32, 2)
+    k, n = w.shape
+    wq = torch.empty((n, k), dtype=E4M3, device=w.device)
+    sc = torch.empty((n,), dtype=F32, device=w.device)
+    _lib.call("ptb_quant_weight_e4m3", w.data_ptr(), wq.data_ptr(), sc.data_ptr(), k, n, _stream(w))
+    return wq, sc
+
+
+def gemm_fp8(aq: torch.Tensor, sa: torch.Tensor, wq_t: torch.Tensor, sw: torch.Tensor, out=None) -> torch.Tensor:
+    """C = bf16((Aq[M,K] @ Wt[N,K]^T) * sa[M] * sw[N]) with e4m3 operands and fp32 accumulation."""
+    _need(aq, "aq", E4M3, 2)
+    _need(wq_t, "wq_t", E4M3, 2)
+    _need(sa, "sa", F32, 1)
+    _need(sw, "sw", F32, 1)
+    m, k = aq.shape
+    n, k2 = wq_t.shape
+    if k != k2 or sa.numel() != m or sw.numel() != n:
+        raise ValueError("shapes: aq [M,K], sa [M], wq_t [N,K], sw [N]")
+    c = _out(out, (m, n), BF16, aq)
+    _lib.call("ptb_gemm_fp8_scaled", aq.data_ptr(), sa.data_ptr(), wq_t.data_ptr(), sw.data_ptr(), c.data_ptr(),
+              m, n, k, _stream(aq))
+    return c
+
+
+def fp8_linear(x: torch.Tensor, wq_t: torch.Tensor, sw: torch.Tensor, out=None) -> torch.Tensor:
+    """Per-token dynamic quantisation of x, then the fp8 GEMM (BASELINE config 4's path)."""
+    xq, sx = quant_rows_e4m3(x)
+    return gemm_fp8(xq, sx, wq_t, sw, out=out)
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,39 @@
+"""Seeded inputs and the tolerance check shared by the parity tests."""
+import torch
+
+
+def randn(shape, seed, dtype=torch.bfloat16, std=1.0, mean=0.0):
+    """torch.Generator().manual_seed(seed) + randn, as the reference's make_inputs draw inputs
+    (validation/pytorchsim/*/..._spec.py:28-36), scaled and cast."""
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std + mean).to(dtype)
+
+
+def assert_close(got, want, rtol, atol, what=""):
+    """allclose(got, want, rtol, atol, equal_nan) with the reference verify's report
+    (tests/runtime/verify.py:28-69) in the failure message."""
+    g = got.detach().float().cpu()
+    w = want.detach().float().cpu()
+    assert g.shape == w.shape, f"{what}: shape {tuple(g.shape)} != {tuple(w.shape)}"
+    ok = torch.allclose(g, w, rtol=rtol, atol=atol, equal_nan=True)
+    if not ok:
+        diff = (g - w).abs().nan_to_num(0.0)
+        rel = diff / w.abs().clamp_min(1e-12)
+        idx = int(diff.reshape(-1).argmax())
+        bad = int((diff > atol + rtol * w.abs()).sum())
+        raise AssertionError(
+            f"{what}: max_abs_err={float(diff.max()):.6g} max_rel_err={float(rel.max()):.6g} "
+            f"worst at {idx}: got={float(g.reshape(-1)[idx])!r} want={float(w.reshape(-1)[idx])!r}; "
+            f"{bad}/{diff.numel()} outside (rtol={rtol}, atol={atol})")
+
+
+def bits_equal(got, want):
+    """Exact equality of the stored bits (bf16/fp8/int tensors)."""
+    a, b = got.detach().cpu().contiguous(), want.detach().cpu().contiguous()
+    if a.dtype != b.dtype or a.shape != b.shape:
+        return False
+    if a.element_size() == 2:
+        return torch.equal(a.view(torch.int16), b.view(torch.int16))
+    if a.element_size() == 1:
+        return torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+    return torch.equal(a, b)

@@ -1,0 +1,104 @@
+"""CPU tests of the C ABI: the library loads, exports every entry point include/ptb_amd.h
+declares, and refuses bad arguments with the documented status codes before touching a GPU."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from ptb_amd import _lib
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "ptb_amd.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ptb_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        from ptb_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "ptb_gemm_bf16" in names and "ptb_rmsnorm_bf16" in names
+    assert len(names) >= 10
+
+
+def test_every_declared_symbol_is_exported(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (ptb_\w+)", out))
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, f"declared in ptb_amd.h but not exported: {missing}"
+    for n in declared_functions():
+        assert hasattr(lib, n)
+
+
+def test_binding_covers_header():
+    assert set(declared_functions()) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_abi_version_and_status_text(lib):
+    assert lib.ptb_abi_version() == 1
+    assert lib.ptb_status_string(0) == b"ok"
+    assert b"NULL" in lib.ptb_status_string(_lib.PTB_ERR_NULL)
+    assert lib.ptb_status_string(-99) == b"unknown status"
+
+
+# Argument checks run before any HIP call, so they are exercised here with host pointers.
+BUF = ctypes.create_string_buffer(1 << 16)
+P = ctypes.addressof(BUF)
+P16 = (P + 15) & ~15
+
+
+def test_null_pointers_refused(lib):
+    assert lib.ptb_rmsnorm_bf16(None, P16, 0, P16, 4, 64, 1e-6, None) == _lib.PTB_ERR_NULL
+    assert lib.ptb_gemm_bf16(P16, None, None, P16, 4, 64, 64, None) == _lib.PTB_ERR_NULL
+    assert lib.ptb_softmax_rows_bf16(P16, None, 4, 64, None) == _lib.PTB_ERR_NULL
+    assert lib.ptb_gemm_fp8_scaled(P16, P16, P16, None, P16, 4, 16, 128, None) == _lib.PTB_ERR_NULL
+
+
+def test_shape_and_alignment_refused(lib):
+    assert lib.ptb_rmsnorm_bf16(P16, P16, 0, P16, -1, 64, 1e-6, None) == _lib.PTB_ERR_SHAPE
+    assert lib.ptb_rmsnorm_bf16(P16, P16, 0, P16, 4, 12, 1e-6, None) == _lib.PTB_ERR_ALIGN
+    assert lib.ptb_rmsnorm_bf16(P16 + 2, P16, 0, P16, 4, 64, 1e-6, None) == _lib.PTB_ERR_ALIGN
+    assert lib.ptb_rmsnorm_bf16(P16, P16, 7, P16, 4, 64, 1e-6, None) == _lib.PTB_ERR_DTYPE
+    assert lib.ptb_gemm_bf16(P16, P16, None, P16, 4, 64, 100, None) == _lib.PTB_ERR_UNSUPPORTED
+    assert lib.ptb_gemm_bf16(P16, P16, None, P16, 4, 60, 64, None) == _lib.PTB_ERR_UNSUPPORTED
+    assert lib.ptb_gemm_bf16(P16, P16, None, P16, -4, 64, 64, None) == _lib.PTB_ERR_SHAPE
+    assert lib.ptb_gemm_fp8_scaled(P16, P16, P16, P16, P16, 4, 16, 64, None) == _lib.PTB_ERR_UNSUPPORTED
+    assert lib.ptb_qk_norm_rope_bf16(P16, P16, P16, P16, P16, 4, 2, 64, 1e-6, None) == _lib.PTB_ERR_UNSUPPORTED
+    assert lib.ptb_transpose_heads_bf16(P16, P16, 2, 3, 4, None) == _lib.PTB_ERR_ALIGN
+    assert lib.ptb_reduce_bf16(P16, P16, 64, 5, P16, 4096, None) == _lib.PTB_ERR_DTYPE
+    assert lib.ptb_reduce_bf16(P16, P16, 64, 0, P16, 4, None) == _lib.PTB_ERR_WORKSPACE
+
+
+def test_empty_work_is_a_no_op(lib):
+    # zero rows / zero-size outputs return OK without launching
+    assert lib.ptb_rmsnorm_bf16(P16, P16, 0, P16, 0, 64, 1e-6, None) == _lib.PTB_OK
+    assert lib.ptb_gemm_bf16(P16, P16, None, P16, 0, 64, 64, None) == _lib.PTB_OK
+    assert lib.ptb_silu_mul_bf16(P16, P16, 0, 64, None) == _lib.PTB_OK
+
+
+def test_error_mapping():
+    with pytest.raises(_lib.ShapeError):
+        _lib.check("f", _lib.PTB_ERR_SHAPE)
+    with pytest.raises(_lib.UnsupportedError):
+        _lib.check("f", _lib.PTB_ERR_UNSUPPORTED)
+    with pytest.raises(_lib.HipError):
+        _lib.check("f", 1)
+    _lib.check("f", 0)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_lib.LibraryMissing):
+        _lib.load(tmp_path / "nope.so")

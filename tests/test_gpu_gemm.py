@@ -1,0 +1,110 @@
+"""Parity of the bf16 and fp8 GEMM kernels with the CPU oracle.
+
+Full-size shapes are checked on sampled rows (one random row from every 256-row tile plus the
+first and last rows): a row of C depends only on that row of A, so the oracle computes exactly
+those rows.  Tolerance: the BASELINE bf16/fp8 bound, rtol = atol = 2e-2 (outputs are O(1) by
+construction), and the quantisers are bit-exact."""
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close, bits_equal, randn
+from ptb_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+RTOL = ATOL = 2e-2
+
+
+def sample_rows(m, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    rows = {0, m - 1}
+    for t0 in range(0, m, 256):
+        rows.add(t0 + int(torch.randint(0, min(256, m - t0), (1,), generator=g)))
+    return torch.tensor(sorted(rows))
+
+
+def run_gemm(m, k, n, seed, std_a, std_b, resid=False):
+    a = randn((m, k), seed, std=std_a)
+    b = randn((k, n), seed + 1, std=std_b)
+    r = randn((m, n), seed + 2) if resid else None
+    c = ops.gemm(a.to(DEV), b.to(DEV), None if r is None else r.to(DEV)).cpu()
+    rows = sample_rows(m, seed) if m > 512 else torch.arange(m)
+    want = oracle.gemm(a[rows], b, None if r is None else r[rows])
+    return c[rows], want
+
+
+@pytest.mark.parametrize("m,k,n,resid", [
+    (4096, 4096, 12288, False),   # BASELINE config 2 (Qwen3-8B gate/up shape)
+    (2048, 4096, 4096, False),    # L2048/01 q_proj
+    (2048, 4096, 1024, False),    # L2048/03 k/v_proj
+    (2048, 4096, 4096, True),     # L2048/08 o_proj + residual
+    (2048, 12288, 4096, True),    # L2048/11 down + residual
+])
+def test_gemm_layer_shapes(m, k, n, resid):
+    std = 1.0 / 64.0
+    got, want = run_gemm(m, k, n, 0, std, std, resid)
+    assert_close(got, want, RTOL, ATOL, f"gemm {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,k,n", [
+    (1, 2048, 768), (8, 768, 2048), (16, 2048, 768), (100, 384, 1152), (300, 768, 128),
+    (1024, 2048, 128), (257, 64, 264), (128, 4096, 4096),
+])
+def test_gemm_ragged(m, k, n):
+    got, want = run_gemm(m, k, n, 3, 1.0, 1.0 / k ** 0.5)
+    assert_close(got, want, RTOL, ATOL, f"gemm {m}x{k}x{n}")
+
+
+def test_gemm_bundle_inputs_exact_products():
+    """bf16 operands from the bundle's make_inputs draw (randn): small enough that the fp32
+    accumulation is exact for small K -> bit-exact output (tests/baselines/tpuv6e.txt:162 records
+    max_abs_err 0 for the reference's bf16 matmul)."""
+    a = torch.randint(-8, 9, (64, 64)).to(torch.bfloat16)
+    b = torch.randint(-8, 9, (64, 256)).to(torch.bfloat16)
+    c = ops.gemm(a.to(DEV), b.to(DEV)).cpu()
+    assert bits_equal(c, oracle.gemm(a, b))
+
+
+def test_gemm_refuses_bad_k():
+    a = torch.zeros((4, 100), dtype=torch.bfloat16, device=DEV)
+    b = torch.zeros((100, 64), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.UnsupportedError):
+        ops.gemm(a, b)
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(2048, 12288, 0), (3, 64, 1), (9, 4096, 2), (2, 8, 3)])
+def test_quant_rows_exact(rows, cols, seed):
+    x = randn((rows, cols), seed)
+    if rows > 2:
+        x[1] = 0.0                                  # all-zero row -> scale 1
+    xq, sc = ops.quant_rows_e4m3(x.to(DEV))
+    wq, wsc = oracle.quant_rows_e4m3(x)
+    assert torch.equal(sc.cpu(), wsc)
+    assert bits_equal(xq, wq)
+
+
+@pytest.mark.parametrize("k,n,seed", [(12288, 4096, 0), (128, 16, 1), (100, 70, 2)])
+def test_quant_weight_exact(k, n, seed):
+    w = randn((k, n), seed, dtype=torch.float32, std=0.02)
+    wq, sc = ops.quant_weight_e4m3(w.to(DEV))
+    owq, osc = oracle.quant_weight_e4m3(w)
+    assert torch.equal(sc.cpu(), osc)
+    assert bits_equal(wq, owq)
+
+
+@pytest.mark.parametrize("m,k,n", [(2048, 12288, 4096), (1, 128, 16), (300, 256, 272), (257, 1024, 512)])
+def test_gemm_fp8(m, k, n):
+    """activations bf16 ~N(0,1) quantised per token, weights from N(0,0.02)
+    quantised per output channel; the GPU GEMM and the oracle see the same quantised operands."""
+    x = randn((m, k), 10)
+    w = randn((k, n), 11, dtype=torch.float32, std=0.02)
+    wq_t, sw = ops.quant_weight_e4m3(w.to(DEV))
+    xq, sx = ops.quant_rows_e4m3(x.to(DEV))
+    c = ops.gemm_fp8(xq, sx, wq_t, sw).cpu()
+    rows = sample_rows(m, 1) if m > 512 else torch.arange(m)
+    want = oracle.gemm_fp8(xq.cpu()[rows], sx.cpu()[rows], wq_t.cpu(), sw.cpu())
+    # outputs are ~N(0, 0.02^2 K): scale the absolute floor with them
+    scale = float(want.float().abs().mean()) + 1e-6
+    assert_close(c[rows], want, RTOL, ATOL * scale, f"gemm_fp8 {m}x{k}x{n}")

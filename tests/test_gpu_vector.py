@@ -1,0 +1,148 @@
+"""Parity of the vector-family HIP kernels with the CPU oracle (bf16 outputs: allclose at the
+BASELINE tolerance rtol=atol=2e-2, plus >= 99% of outputs bit-identical; exact ops: bit-equal)."""
+import math
+
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close, bits_equal, randn
+from ptb_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+RTOL = ATOL = 2e-2
+
+
+def bit_fraction(got, want):
+    a = got.detach().cpu().contiguous().view(torch.int16)
+    b = want.detach().cpu().contiguous().view(torch.int16)
+    return float((a == b).float().mean())
+
+
+def check_bf16(got, want, what, min_exact=0.99):
+    assert_close(got, want, RTOL, ATOL, what)
+    frac = bit_fraction(got, want)
+    assert frac >= min_exact, f"{what}: only {frac:.4%} of outputs bit-identical to the oracle"
+
+
+@pytest.mark.parametrize("rows,cols,wdtype,seed", [
+    (2048, 4096, torch.float32, 0),
+    (2048, 4096, torch.bfloat16, 1),    # L2048/00 (bf16 weight)
+    (3, 128, torch.bfloat16, 2),        # one wave per row, ragged row count
+    (5, 2056, torch.float32, 3),        # block per row, partial last chunk group
+    (7, 16384, torch.bfloat16, 4),      # largest register-resident row
+    (2, 24576, torch.float32, 5),       # long-row two-pass kernel
+])
+def test_rmsnorm(rows, cols, wdtype, seed):
+    x = randn((rows, cols), seed)
+    w = randn((cols,), seed + 100, dtype=wdtype, std=0.02, mean=1.0)
+    got = ops.rmsnorm(x.to(DEV), w.to(DEV), 1e-6)
+    torch.cuda.synchronize()
+    check_bf16(got, oracle.rmsnorm(x, w, 1e-6), f"rmsnorm {rows}x{cols}")
+
+
+def test_rmsnorm_zero_rows_and_empty():
+    x = torch.zeros((4, 256), dtype=torch.bfloat16)
+    w = torch.ones(256, dtype=torch.bfloat16)
+    got = ops.rmsnorm(x.to(DEV), w.to(DEV), 1e-6)
+    assert bits_equal(got, oracle.rmsnorm(x, w, 1e-6))
+    empty = ops.rmsnorm(torch.empty((0, 256), dtype=torch.bfloat16, device=DEV), w.to(DEV))
+    assert empty.shape == (0, 256)
+
+
+@pytest.mark.parametrize("rows,cols,seed", [
+    (2048, 6144, 0),    # vector_softmax_2048x6144_bf16
+    (8, 128, 1), (1, 8192, 2), (1024, 1536, 3), (33, 384, 4),
+    (4, 24576, 5),      # long-row kernel
+])
+def test_softmax(rows, cols, seed):
+    x = randn((rows, cols), seed)
+    got = ops.softmax_rows(x.to(DEV))
+    check_bf16(got, oracle.softmax_rows(x), f"softmax {rows}x{cols}")
+
+
+def test_softmax_nan_and_inf():
+    x = randn((4, 512), 7)
+    x[1, 17] = float("nan")          # NaN-propagating max: whole row NaN
+    x[2, :] = -float("inf")          # all -inf: NaN like the reference's exp(-inf - -inf)
+    x[3, 5] = float("inf")
+    got = ops.softmax_rows(x.to(DEV)).cpu()
+    want = oracle.softmax_rows(x)
+    assert torch.isnan(got[1]).all() and torch.isnan(want[1]).all()
+    assert torch.isnan(got[2]).all() and torch.isnan(want[2]).all()
+    assert torch.equal(torch.isnan(got[3]), torch.isnan(want[3]))
+    check_bf16(got[0:1], want[0:1], "softmax clean row")
+
+
+@pytest.mark.parametrize("rows,inter,seed", [(2048, 12288, 0), (3, 8, 1), (17, 1032, 2)])
+def test_silu_mul(rows, inter, seed):
+    gu = randn((rows, 2 * inter), seed)
+    got = ops.silu_mul(gu.to(DEV))
+    check_bf16(got, oracle.silu_mul(gu), f"silu_mul {rows}x{inter}")
+
+
+@pytest.mark.parametrize("shape", [(2048, 8, 128), (32, 2048, 128), (3, 5, 8), (1, 7, 64)])
+def test_transpose_heads_exact(shape):
+    x = randn(shape, 11)
+    got = ops.transpose_heads(x.to(DEV))
+    assert bits_equal(got, oracle.transpose_heads(x))
+
+
+@pytest.mark.parametrize("tokens,heads,tables,seed", [
+    (2048, 32, "bundle", 0),   # L2048/02: cos/sin drawn by the spec's make_inputs (randn)
+    (2048, 8, "rope", 1),      # L2048/04 with real theta=1e6 tables
+    (5, 3, "rope", 2),
+])
+def test_qk_norm_rope(tokens, heads, tables, seed):
+    x = randn((tokens, heads, 128), seed)
+    w = randn((128,), seed + 1)
+    if tables == "bundle":
+        cos = randn((tokens, 128), seed + 2, dtype=torch.float32)
+        sin = randn((tokens, 128), seed + 3, dtype=torch.float32)
+    else:
+        cos, sin = oracle.rope_tables(tokens, 128, 1.0e6)
+    got = ops.qk_norm_rope(x.to(DEV), w.to(DEV), cos.to(DEV), sin.to(DEV), 1e-6)
+    check_bf16(got, oracle.qk_norm_rope(x, w, cos, sin, 1e-6), f"qk_norm_rope {tokens}x{heads}")
+
+
+@pytest.mark.parametrize("n,seed", [(12288 * 4096, 0), (1024 * 1024, 1), (8 * 128 + 5, 2), (3, 3)])
+def test_reduce(n, seed):
+    x = randn((n,), seed)
+    xd = x.to(DEV)
+    got_max = ops.reduce(xd, "max").cpu()
+    assert torch.equal(got_max, oracle.reduce_max(x))
+    got_sum = ops.reduce(xd, "sum").cpu()
+    want = oracle.reduce_sum(x)
+    # fp32 accumulation in a different order than the exact sum: bound by the summation error scale
+    bound = 1e-6 * float(x.float().abs().sum()) + 1e-6
+    assert abs(float(got_sum) - float(want)) <= bound, (float(got_sum), float(want), bound)
+    # shifted input so the sum is far from zero: relative error within 1e-5
+    xs = (x.float() + 1.0).to(torch.bfloat16)
+    gs, ws = float(ops.reduce(xs.to(DEV), "sum")), float(oracle.reduce_sum(xs))
+    assert abs(gs - ws) <= 1e-5 * abs(ws), (gs, ws)
+
+
+def test_reduce_max_nan():
+    x = randn((4096,), 9)
+    x[1234] = float("nan")
+    assert math.isnan(float(ops.reduce(x.to(DEV), "max")))
+
+
+@pytest.mark.parametrize("n", [1024 * 1024, 8 * 128, 37])
+def test_add_scalar_exact(n):
+    x = randn((n,), 5)
+    got = ops.add_scalar(x.to(DEV), 1.0)
+    assert bits_equal(got, oracle.add_scalar(x, 1.0))
+
+
+def test_error_paths_on_device():
+    x = torch.zeros((4, 12), dtype=torch.bfloat16, device=DEV)   # 12 % 8 != 0
+    w = torch.ones(12, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.AlignmentError):
+        ops.rmsnorm(x, w)
+    xh = torch.zeros((4, 3, 64), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.UnsupportedError):
+        ops.qk_norm_rope(xh, torch.ones(64, dtype=torch.bfloat16, device=DEV),
+                         torch.ones((4, 64), device=DEV), torch.zeros((4, 64), device=DEV))
