@@ -122,6 +122,45 @@ def bench_gemm_fp8(steps, warmup):
             "quantise_us": qms * 1e3, "quantise_gbs": qbytes / (qms * 1e-3) / 1e9}
 
 
+def bench_attention(steps, warmup):
+    import torch
+    from ptb_amd import ops
+
+    hq, hkv, s, d = 32, 8, 4096, 128
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(hq, s, d, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(hkv, s, d, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(hkv, s, d, generator=g).to(torch.bfloat16).cuda()
+    o = torch.empty_like(q)
+    ms, wall = timed(lambda: ops.flash_attention(q, k, v, hq, hkv, True, out=o), steps, warmup)
+    flops = 4.0 * hq * d * s * (s + 1) / 2
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"name": "flash_attention", "config": "BASELINE config 3: causal GQA 32/8 heads, S 4096, D 128",
+            "us": ms * 1e3, "wall_us": wall * 1e3, "tflops": tf,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / PEAK_BF16_TFLOPS}}
+
+
+def bench_layer(steps, warmup):
+    import torch
+    from ptb_amd import qwen3
+
+    t = 2048
+    layer = qwen3.Qwen3Layer(qwen3.random_weights(device="cuda"))
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(t, 4096, generator=g).to(torch.bfloat16).cuda()
+    y = torch.empty_like(x)
+    ms, wall = timed(lambda: layer.forward(x, out=y), max(5, steps // 5), max(2, warmup // 5))
+    work = qwen3.layer_work(t)
+    roof_us = sum(max(f / (PEAK_BF16_TFLOPS * 1e12), b / (PEAK_HBM_GBS * 1e9)) for _, f, b in work) * 1e6
+    flops = sum(f for _, f, _ in work)
+    return {"name": "qwen3_8b_layer", "config": "BASELINE config 5: Qwen3-8B decoder layer prefill T=S=2048",
+            "us": ms * 1e3, "wall_us": wall * 1e3, "tflops": flops / (ms * 1e-3) / 1e12,
+            "roofline": {"bound": "mixed", "achieved": roof_us, "peak": ms * 1e3, "unit": "us (roofline / measured)",
+                         "frac": roof_us / (ms * 1e3)},
+            "launches": len(work)}
+
+
 def cpu_baseline_gemm(a, b, sample_rows=256):
     """The CPU golden for the headline workload: torch-CPU fp32 matmul of the oracle's arithmetic
     (bf16 operands upcast, fp32 accumulation, one bf16 rounding), on `sample_rows` rows of A against
@@ -151,6 +190,8 @@ BENCHES = {
     "gemm_bf16": bench_gemm_bf16,
     "rmsnorm": bench_rmsnorm,
     "gemm_fp8": bench_gemm_fp8,
+    "flash_attention": bench_attention,
+    "qwen3_8b_layer": bench_layer,
 }
 
 

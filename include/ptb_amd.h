@@ -116,6 +116,15 @@ int ptb_quant_weight_e4m3(const float* w, void* wq_t, float* scale, int64_t k, i
 int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* wq_t, const float* sw, void* c,
                         int64_t m, int64_t n, int64_t k, void* stream);
 
+/* Flash-attention forward, head-major layout: q/o [batch*hq, seq, head_dim], k/v [batch*hkv, seq,
+ * head_dim]; q head h reads kv head h / (hq / hkv).  Online softmax in fp32 with P rounded to bf16
+ * before P.V; causal masks key > query.  head_dim must be 128 and seq a multiple of 128.
+ * Replaces: validation/pytorchsim/attention_prefill_32x8x4096_bf16/00__prefill_kernel/
+ *           _prefill_kernel_triton.py:4-44 (and qwen3_8b_layer_prefill_2048x2048_bf16/06__prefill_kernel). */
+int ptb_flash_attn_fwd_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
+                            int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale,
+                            int causal, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

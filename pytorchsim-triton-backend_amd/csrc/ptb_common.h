@@ -112,6 +112,20 @@ __device__ __forceinline__ float block_max_nan(float v, float* red) {
   return t;
 }
 
+// Column C of an 8x8 block of 16-bit values held as 8 row vectors (row p = 8 values): the 8
+// values of column C, one from each row, packed in row order.  Used to transpose 8x8 tiles in
+// registers before a K-contiguous LDS store (v_perm / v_and_or per dword).
+template <int C>
+__device__ __forceinline__ u32x4 column8x8(const u32x4 (&r)[8]) {
+  u32x4 o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t lo = r[2 * q][C / 2], hi = r[2 * q + 1][C / 2];
+    o[q] = (C % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+  }
+  return o;
+}
+
 __host__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 __host__ __forceinline__ int launch_status() {

@@ -85,6 +85,8 @@ SIGNATURES = {
     "ptb_quant_rows_e4m3": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp]),
     "ptb_quant_weight_e4m3": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp]),
     "ptb_gemm_fp8_scaled": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
+    "ptb_flash_attn_fwd_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32,
+                                         _c_int, _vp]),
 }
 
 _lock = threading.Lock()

@@ -183,3 +183,21 @@ def fp8_linear(x: torch.Tensor, wq_t: torch.Tensor, sw: torch.Tensor, out=None) 
 
 def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, hq: int, hkv: int, causal: bool = True,
+                    scale: float | None = None, out=None) -> torch.Tensor:
+    """Flash-attention forward over head-major q [B*hq, S, D], k/v [B*hkv, S, D] -> o like q."""
+    for t, name in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, name, BF16, 3)
+    bhq, s, d = q.shape
+    if hq <= 0 or hkv <= 0 or hq % hkv or bhq % hq:
+        raise ValueError(f"bad head counts hq={hq}, hkv={hkv} for q of shape {tuple(q.shape)}")
+    batch = bhq // hq
+    if tuple(k.shape) != (batch * hkv, s, d) or tuple(v.shape) != (batch * hkv, s, d):
+        raise ValueError("k and v must be [B*hkv, S, D] matching q")
+    o = _out(out, tuple(q.shape), BF16, q)
+    sc = default_scale(d) if scale is None else float(scale)
+    _lib.call("ptb_flash_attn_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), batch, hq, hkv, s,
+              d, sc, 1 if causal else 0, _stream(q))
+    return o

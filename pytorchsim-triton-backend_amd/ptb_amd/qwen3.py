@@ -1,0 +1,163 @@
+"""Qwen3-8B decoder layer (prefill) composed from the HIP kernels.
+
+The launch sequence is the reference bundle's: validation/pytorchsim/qwen3_8b_layer_prefill_2048x2048_bf16/
+manifest.json lists 14 launches of 12 kernels, 00,01,02,03,04,03,05,06,07,08,00,09,10,11, and
+:meth:`Qwen3Layer.forward` issues them in that order on the current HIP stream:
+
+  K00 rmsnorm(x, w_in)            K01 q = xn Wq          K02 q-norm + RoPE -> [32,T,128]
+  K03 k = xn Wk                   K04 k-norm + RoPE      K03 v = xn Wv      K05 v -> [8,T,128]
+  K06 causal GQA attention        K07 o -> [T,32,128]    K08 h = o Wo + x
+  K00 rmsnorm(h, w_post)          K09 gu = hn Wgu        K10 a = silu(g) * u
+  K11 y = a Wd + h
+
+(The data flow is read from each kernel's index arithmetic; the reference times these kernels
+separately and never runs the layer end to end, validation/gemm/simulate_shapes.py:279-302.)
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+
+BF16 = torch.bfloat16
+
+
+@dataclass(frozen=True)
+class Qwen3Config:
+    hidden: int = 4096
+    intermediate: int = 12288
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    rope_theta: float = 1.0e6
+    eps: float = 1e-6
+
+
+QWEN3_8B = Qwen3Config()
+
+LAUNCH_ORDER = ("00", "01", "02", "03", "04", "03", "05", "06", "07", "08", "00", "09", "10", "11")
+
+
+def rope_tables(tokens: int, head_dim: int = 128, theta: float = 1.0e6, device="cpu"):
+    """cos/sin [T, D] fp32 for rotate-half RoPE (angle t / theta^(2i/D), both halves alike),
+    computed in fp64 on the host once per sequence length, like the model's cached tables."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim))
+    ang = torch.arange(tokens, dtype=torch.float64)[:, None] * inv[None, :]
+    emb = torch.cat([ang, ang], dim=-1)
+    return emb.cos().float().to(device), emb.sin().float().to(device)
+
+
+def random_weights(cfg: Qwen3Config = QWEN3_8B, seed: int = 0, std: float = 0.02, norm_mean: float = 1.0,
+                   device="cpu") -> dict:
+    """Random-init bf16 weights: projections ~N(0, std); the RMSNorm weights ~N(norm_mean, std)
+    (norm_mean=1 keeps activations O(1) through the layer).  Drawn in a fixed order from one
+    seeded generator.  Wgu is [hidden, 2*intermediate] = gate | up."""
+    g = torch.Generator().manual_seed(seed)
+    h, i, hd = cfg.hidden, cfg.intermediate, cfg.head_dim
+
+    def draw(*shape, mean=0.0):
+        return (torch.randn(*shape, generator=g) * std + mean).to(BF16).to(device)
+
+    return {
+        "w_in": draw(h, mean=norm_mean),
+        "wq": draw(h, cfg.heads * hd),
+        "wk": draw(h, cfg.kv_heads * hd),
+        "wv": draw(h, cfg.kv_heads * hd),
+        "w_qn": draw(hd, mean=norm_mean),
+        "w_kn": draw(hd, mean=norm_mean),
+        "wo": draw(cfg.heads * hd, h),
+        "w_post": draw(h, mean=norm_mean),
+        "wgu": draw(h, 2 * i),
+        "wd": draw(i, h),
+    }
+
+
+class Qwen3Layer:
+    """One decoder layer on the GPU; weights are device bf16 tensors as from :func:`random_weights`."""
+
+    def __init__(self, weights: dict, cfg: Qwen3Config = QWEN3_8B):
+        self.w = weights
+        self.cfg = cfg
+        self._tables = {}
+        self._bufs = {}
+
+    def tables(self, tokens: int, device):
+        key = (tokens, str(device))
+        if key not in self._tables:
+            self._tables[key] = rope_tables(tokens, self.cfg.head_dim, self.cfg.rope_theta, device)
+        return self._tables[key]
+
+    def buffers(self, tokens: int, device) -> dict:
+        """Activation buffers for one forward at this length, allocated once and reused."""
+        key = (tokens, str(device))
+        if key not in self._bufs:
+            c = self.cfg
+            qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+
+            def e(*shape):
+                return torch.empty(*shape, dtype=BF16, device=device)
+
+            self._bufs[key] = {
+                "xn": e(tokens, c.hidden), "q": e(tokens, qd), "k": e(tokens, kd), "v": e(tokens, kd),
+                "qh": e(c.heads, tokens, c.head_dim), "kh": e(c.kv_heads, tokens, c.head_dim),
+                "vh": e(c.kv_heads, tokens, c.head_dim), "oh": e(c.heads, tokens, c.head_dim),
+                "o": e(tokens, c.heads, c.head_dim), "h": e(tokens, c.hidden), "hn": e(tokens, c.hidden),
+                "gu": e(tokens, 2 * c.intermediate), "a": e(tokens, c.intermediate), "y": e(tokens, c.hidden),
+            }
+        return self._bufs[key]
+
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        c, w = self.cfg, self.w
+        t = x.shape[0]
+        cos, sin = self.tables(t, x.device)
+        b = self.buffers(t, x.device)
+        y = b["y"] if out is None else out
+        ops.rmsnorm(x, w["w_in"], c.eps, out=b["xn"])                                       # K00
+        ops.gemm(b["xn"], w["wq"], out=b["q"])                                              # K01
+        ops.qk_norm_rope(b["q"].view(t, c.heads, c.head_dim), w["w_qn"], cos, sin, c.eps, out=b["qh"])   # K02
+        ops.gemm(b["xn"], w["wk"], out=b["k"])                                              # K03
+        ops.qk_norm_rope(b["k"].view(t, c.kv_heads, c.head_dim), w["w_kn"], cos, sin, c.eps, out=b["kh"])  # K04
+        ops.gemm(b["xn"], w["wv"], out=b["v"])                                              # K03
+        ops.transpose_heads(b["v"].view(t, c.kv_heads, c.head_dim), out=b["vh"])           # K05
+        ops.flash_attention(b["qh"], b["kh"], b["vh"], c.heads, c.kv_heads, True,
+                            1.0 / math.sqrt(c.head_dim), out=b["oh"])                       # K06
+        ops.transpose_heads(b["oh"], out=b["o"])                                            # K07
+        ops.gemm(b["o"].view(t, c.heads * c.head_dim), w["wo"], residual=x, out=b["h"])     # K08
+        ops.rmsnorm(b["h"], w["w_post"], c.eps, out=b["hn"])                                # K00
+        ops.gemm(b["hn"], w["wgu"], out=b["gu"])                                            # K09
+        ops.silu_mul(b["gu"], out=b["a"])                                                   # K10
+        ops.gemm(b["a"], w["wd"], residual=b["h"], out=y)                                   # K11
+        return y
+
+    __call__ = forward
+
+
+def layer_work(tokens: int, cfg: Qwen3Config = QWEN3_8B) -> list:
+    """(name, flops, hbm bytes) of each launch at this length: the roofline model of the layer
+    (flop conventions as the reference reports: 2*M*N*K per GEMM, 4*H*D*S(S+1)/2 causal attention;
+    bytes = each operand read once plus each output written once)."""
+    c = cfg
+    t, hd, i = tokens, c.hidden, c.intermediate
+    qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+
+    def mm(m, k, n, resid=False):
+        return 2.0 * m * n * k, 2.0 * (m * k + k * n + m * n + (m * n if resid else 0))
+
+    work = [("K00 rmsnorm", 4.0 * t * hd, 2.0 * (2 * t * hd + hd))]
+    work.append(("K01 q_proj",) + mm(t, hd, qd))
+    work.append(("K02 q_norm_rope", 10.0 * t * qd, 2.0 * 2 * t * qd + 8.0 * t * c.head_dim))
+    work.append(("K03 k_proj",) + mm(t, hd, kd))
+    work.append(("K04 k_norm_rope", 10.0 * t * kd, 2.0 * 2 * t * kd + 8.0 * t * c.head_dim))
+    work.append(("K03 v_proj",) + mm(t, hd, kd))
+    work.append(("K05 v_transpose", 0.0, 2.0 * 2 * t * kd))
+    work.append(("K06 attention", 4.0 * c.heads * c.head_dim * t * (t + 1) / 2, 2.0 * (2 * t * qd + 2 * t * kd)))
+    work.append(("K07 o_transpose", 0.0, 2.0 * 2 * t * qd))
+    work.append(("K08 o_proj+res",) + mm(t, qd, hd, True))
+    work.append(("K00 rmsnorm", 4.0 * t * hd, 2.0 * (2 * t * hd + hd)))
+    work.append(("K09 gate_up",) + mm(t, hd, 2 * i))
+    work.append(("K10 silu_mul", 5.0 * t * i, 2.0 * 3 * t * i))
+    work.append(("K11 down+res",) + mm(t, i, hd, True))
+    return work

@@ -1,0 +1,69 @@
+"""Parity of the flash-attention kernel with the oracle's restatement of the reference's
+_prefill_kernel (P rounded to bf16 before P.V).  The kernel blocks keys by 64 where the reference
+blocks by 1024, so the bf16 rounding points of P differ: bf16 tolerance rtol = atol = 2e-2 (O is
+O(1)), and the exact invariants (row 0 = V[0]) are checked bit-for-bit."""
+import math
+
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close, bits_equal, randn
+from ptb_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+RTOL = ATOL = 2e-2
+
+
+def inputs(batch, hq, hkv, s, seed):
+    q = randn((batch * hq, s, 128), seed)
+    k = randn((batch * hkv, s, 128), seed + 1)
+    v = randn((batch * hkv, s, 128), seed + 2)
+    return q, k, v
+
+
+@pytest.mark.parametrize("batch,hq,hkv,s,causal", [
+    (1, 32, 8, 4096, True),     # BASELINE config 3 / attention_prefill_32x8x4096_bf16
+    (1, 32, 8, 2048, True),     # L2048/06 (the Qwen3-8B layer's attention)
+    (1, 16, 8, 1024, True),
+    (1, 24, 8, 512, True),      # G = 3
+    (1, 64, 8, 256, True),      # G = 8
+    (2, 4, 2, 384, True),       # batch > 1, S not a multiple of 256
+    (1, 8, 8, 128, True),       # MHA, a single tile
+    (1, 8, 2, 512, False),      # non-causal path
+])
+def test_flash_attention(batch, hq, hkv, s, causal):
+    q, k, v = inputs(batch, hq, hkv, s, 0)
+    o = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hq, hkv, causal).cpu()
+    # the oracle is the reference's own blocking (1024, or S when shorter); check a subset of
+    # heads at the largest sizes to keep the CPU side to seconds
+    heads = torch.arange(batch * hq)
+    if s >= 2048:
+        heads = torch.tensor([0, 5, 13, 31])
+    want = oracle.flash_attention(q, k, v, hq, hkv, causal, 1.0 / math.sqrt(128))
+    assert_close(o[heads], want[heads], RTOL, ATOL, f"flash {batch}x{hq}x{hkv}x{s} causal={causal}")
+    if causal:
+        # row 0 attends only to key 0: p = 1 exactly, so O[h, 0] = V[kv(h), 0] bit for bit
+        g = hq // hkv
+        for bh in range(batch * hq):
+            b, h = divmod(bh, hq)
+            assert bits_equal(o[bh, 0], v[b * hkv + h // g, 0])
+
+
+def test_flash_constant_v():
+    """V = const c: every output is c * sum(bf16(p)) / sum(p), i.e. c within bf16 rounding."""
+    q, k, _ = inputs(1, 8, 2, 512, 3)
+    v = torch.full((2, 512, 128), 0.75, dtype=torch.bfloat16)
+    o = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), 8, 2, True).cpu().float()
+    assert (o - 0.75).abs().max() <= 0.75 * 2 ** -7
+
+
+def test_flash_refuses_bad_shapes():
+    q = torch.zeros((4, 100, 128), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.UnsupportedError):
+        ops.flash_attention(q, q[:2].contiguous(), q[:2].contiguous(), 4, 2)
+    q64 = torch.zeros((4, 128, 64), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.UnsupportedError):
+        ops.flash_attention(q64, q64[:2].contiguous(), q64[:2].contiguous(), 4, 2)
