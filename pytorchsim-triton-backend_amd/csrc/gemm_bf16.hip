@@ -1,79 +1,88 @@
 // bf16 GEMM on gfx950 matrix cores: C[M,N] = A[M,K] * B[K,N] (+ R[M,N]), all row-major, fp32
 // accumulation, one bf16 rounding at the store.
 //
-// Workgroup tile 256x256, K step 64, 4 waves in a 2x2 arrangement, each wave owning a 128x128
+// Workgroup tile 256x256, K step 32, 4 waves in a 2x2 arrangement, each wave owning a 128x128
 // sub-tile as 4x4 v_mfma_f32_32x32x16_bf16 accumulators (256 fp32 per lane, held in AGPRs).
-// Both operands are staged through LDS, double-buffered (2 x 72 KB of the 160 KB), with one barrier
-// per K step: while the matrix cores work on stage s, the next K slice is already in flight from
-// HBM into registers and is written to stage s^1 afterwards.
 //
-// MFMA wants every lane to hold 8 consecutive K values of one row (A) or one column (B).  A rows
-// are K-contiguous already; B is N-contiguous, so each thread loads an 8(K) x 8(N) block of B with
-// eight 128-bit loads and transposes it in registers (v_perm) before the 128-bit LDS stores.  LDS
-// rows are padded to 72 elements (144 B), which makes both the fragment reads and the stores
-// bank-conflict free.
+// Operands move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging) into a ring of four
+// 32 KB LDS stages, three K steps ahead of the matrix cores, so two to three microseconds of memory
+// latency stay hidden behind MFMA work.  Each stage holds the A tile [256 rows][32 k] and the B tile
+// [32 k][256 n] in their global layouts, with 16-byte chunks XOR-swizzled per row so that every LDS
+// read below is bank-conflict free:
+//   A fragments (8 consecutive k of one row per lane) are plain 128-bit LDS reads;
+//   B fragments (8 consecutive k of one column per lane, while B is N-contiguous) come from two
+//   ds_read_b64_tr_b16 transposing reads: within each 16-lane group, lane 4j+q supplies row k+j,
+//   columns n+4q..n+4q+3, and lane i receives rows k..k+3 of column n+i.
+// Swizzles: A row m keeps chunk c in slot c ^ ((m >> 2) & 3); B row k keeps chunk c in slot
+// c ^ (4 * (k & 3)), so the 4 rows x 4 chunks a half-wave reads land in 16 distinct bank groups.
+// The fragments of the next 16-wide K slice are always read while the MFMAs of the current one
+// run (the last slice of a step reads the first slice of the next stage, behind the barrier that
+// publishes it), so LDS latency stays off the matrix cores' critical path.
+// The MFMA is issued with B as its first operand, so each accumulator holds a 32x32 block of C^T:
+// a lane's four consecutive registers are four consecutive columns of one row of C, stored (with
+// the residual read) as one 8-byte access.
 //
 // Tile order is XCD-aware: hardware hands workgroup i to XCD i % 8, so ids are remapped to give
-// each XCD a contiguous range of tiles, walked in groups of 8 tile-rows for L2 reuse of B panels.
+// each XCD a contiguous range of tiles, walked in groups of 8 tile-rows for L2 reuse.
 #include "ptb_common.h"
 
 using namespace ptb;
 
+#pragma clang diagnostic ignored "-Winline-asm"
+
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int LDK = BK + 8;                  // padded LDS row, bf16 elements
+constexpr int BM = 256, BN = 256, BK = 32;
 constexpr int kThreads = 256;
-constexpr int kStageElems = (BM + BN) * LDK;  // one stage: A tile then transposed B tile
+constexpr int kStages = 4;
+constexpr int kABytes = BM * BK * 2;           // 16 KB: 256 rows x 64 B
+constexpr int kBBytes = BK * BN * 2;           // 16 KB: 32 rows x 512 B
+constexpr int kStageBytes = kABytes + kBBytes;  // 32 KB
 constexpr int kGroupM = 8;
+constexpr int kDmaPerStage = 8;                // buffer_load ... lds per wave per stage
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-// Column C of an 8x8 bf16 block held as 8 row vectors: 8 K-consecutive values of one column.
-template <int C>
-__device__ __forceinline__ u32x4 column(const u32x4 (&r)[8]) {
-  u32x4 o;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t lo = r[2 * q][C / 2], hi = r[2 * q + 1][C / 2];
-    o[q] = (C % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
-  }
-  return o;
+// 16 bytes per lane from global (buffer resource, byte offsets) straight into LDS at
+// lds_base + 16 * lane; lds_base is wave-uniform.  The compiler does not see the LDS write, so the
+// caller orders it with explicit s_waitcnt vmcnt + barrier.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
 }
 
-template <int C>
-__device__ __forceinline__ void store_columns(uint16_t* bs, const u32x4 (&r)[8]) {
-  *reinterpret_cast<u32x4*>(bs + C * LDK) = column<C>(r);
-  if constexpr (C + 1 < 8) store_columns<C + 1>(bs, r);
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
 
-// One K slice of this thread's share: 8 A chunks (8 rows) and an 8x8 block of B.
-struct Slice {
-  u32x4 a[8];
-  u32x4 b[8];
-};
-
-__device__ __forceinline__ Slice gload(const uint16_t* const (&a_src)[8], const uint16_t* b_src, int N,
-                                       int k0) {
-  Slice s;
-#pragma unroll
-  for (int p = 0; p < 8; ++p) s.a[p] = *reinterpret_cast<const u32x4*>(a_src[p] + k0);
-#pragma unroll
-  for (int p = 0; p < 8; ++p) s.b[p] = *reinterpret_cast<const u32x4*>(b_src + int64_t(k0 + p) * N);
-  return s;
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = int(uint32_t(a));
+  r[1] = int(uint32_t(a >> 32) & 0xffffu);  // stride 0
+  r[2] = int(bytes);                        // num_records: reads past it return 0
+  r[3] = 0x00020000;                        // dword data format (gfx9 family)
+  return r;
 }
 
-__device__ __forceinline__ void sstore(const Slice& s, uint16_t* a_dst, uint16_t* b_dst, int st) {
+// acc[i][j] += (B^T A^T) block: C^T rows = N (j tile), C^T cols = M (i tile)
+__device__ __forceinline__ void mfma_slice(f32x16 (&acc)[4][4], const bf16x8 (&fa)[4], const bf16x8 (&fb)[4]) {
 #pragma unroll
-  for (int p = 0; p < 8; ++p) *reinterpret_cast<u32x4*>(a_dst + st * kStageElems + p * 32 * LDK) = s.a[p];
-  store_columns<0>(b_dst + st * kStageElems, s.b);
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
 }
 
 template <bool RESID>
-__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const uint16_t* __restrict__ R,
     uint16_t* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * kStageElems];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStageBytes];
 
   // ---- tile selection
   const int ntiles = tiles_m * tiles_n;
@@ -90,17 +99,34 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // ---- global -> register loaders (rows/cols past the edge are clamped; their results are
-  //      never stored)
-  const int a_chunk = tid & 7, a_row = tid >> 3;  // A: 8 chunks of 8 per 64-wide K row, 32 rows/pass
-  const uint16_t* a_src[8];
+  // ---- loaders: A tile rows past M read as zero (num_records); B columns past N are read from
+  //      the next row or as zero, and only feed columns of C that are never stored
+  const i32x4 rsrc_a = make_rsrc(A + int64_t(m0) * K, uint32_t(min(BM, M - m0)) * uint32_t(K) * 2u);
+  const i32x4 rsrc_b = make_rsrc(B + n0, uint32_t((int64_t(K) * N - n0) * 2));
+  // A: instruction t of this wave covers rows (4*wave+t)*16 .. +16; lane -> row l/4, slot l%4
+  uint32_t a_voff[4], b_voff[4];
 #pragma unroll
-  for (int p = 0; p < 8; ++p) a_src[p] = A + int64_t(min(m0 + p * 32 + a_row, M - 1)) * K + a_chunk * 8;
-  const int b_kb = tid & 7, b_nb = tid >> 3;      // B: 8x8 block (k-block b_kb, n-block b_nb)
-  const int b_n = min(n0 + b_nb * 8, N - 8);
-  const uint16_t* b_src = B + int64_t(b_kb * 8) * N + b_n;
-  uint16_t* const a_dst = smem + a_row * LDK + a_chunk * 8;
-  uint16_t* const b_dst = smem + BM * LDK + (b_nb * 8) * LDK + b_kb * 8;
+  for (int t = 0; t < 4; ++t) {
+    const int row = (wave * 4 + t) * 16 + (lane >> 2);
+    const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+    a_voff[t] = uint32_t(row * K + chunk * 8) * 2u;
+    // B: instruction t covers k rows 2*(4*wave+t) + lane/32; lane -> slot lane%32
+    const int k = 2 * (wave * 4 + t) + (lane >> 5);
+    const int bchunk = (lane & 31) ^ (4 * (k & 3));
+    b_voff[t] = uint32_t(k * N + bchunk * 8) * 2u;
+  }
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
+  auto issue_stage = [&](int kt) {
+    const uint32_t st = lds0 + uint32_t(kt % kStages) * kStageBytes;
+    const uint32_t a_soff = uint32_t(kt * BK) * 2u;
+    const uint32_t b_soff = uint32_t(kt * BK) * uint32_t(N) * 2u;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      dma16(rsrc_a, __builtin_amdgcn_readfirstlane(st + (wave * 4 + t) * 1024), a_voff[t], a_soff);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      dma16(rsrc_b, __builtin_amdgcn_readfirstlane(st + kABytes + (wave * 4 + t) * 1024), b_voff[t], b_soff);
+  };
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -110,61 +136,91 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // fragment addressing: lane -> row/col (lane % 32), K half (lane / 32)
-  const int fr = lane & 31, fk = (lane >> 5) * 8;
-  const int a_off = (wm * 128 + fr) * LDK + fk;
-  const int b_off = BM * LDK + (wn * 128 + fr) * LDK + fk;
-
-  const int nk = K / BK;
-  sstore(gload(a_src, b_src, N, 0), a_dst, b_dst, 0);
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const uint16_t* st = smem + (kt & 1) * kStageElems;
-    const bool more = kt + 1 < nk;
-    Slice nxt;
-    if (more) nxt = gload(a_src, b_src, N, (kt + 1) * BK);
-    bf16x8 fa[2][4], fb[2][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      fa[0][i] = *reinterpret_cast<const bf16x8*>(st + a_off + i * 32 * LDK);
-      fb[0][i] = *reinterpret_cast<const bf16x8*>(st + b_off + i * 32 * LDK);
-    }
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int cb = ks & 1;
-      if (ks + 1 < BK / 16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          fa[cb ^ 1][i] = *reinterpret_cast<const bf16x8*>(st + a_off + i * 32 * LDK + (ks + 1) * 16);
-          fb[cb ^ 1][i] = *reinterpret_cast<const bf16x8*>(st + b_off + i * 32 * LDK + (ks + 1) * 16);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][i], fb[cb][j], acc[i][j], 0, 0, 0);
-    }
-    if (more) sstore(nxt, a_dst, b_dst, (kt + 1) & 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: accumulator (i, j, r) of lane -> row 8*(r/4) + 4*(lane/32) + r%4, col lane%32
+  // ---- fragment addressing
+  const int fr = lane & 31, h = lane >> 5;
+  // A: row m (this lane's), chunk 2*ks + h, swizzled by (m >> 2) & 3
+  int a_row_off[4], a_sw[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    const int m = wm * 128 + i * 32 + fr;
+    a_row_off[i] = m * 64;
+    a_sw[i] = (m >> 2) & 3;
+  }
+  // B (transposing reads): group g = lane/16 -> k half g/2, column half 16*(g%2); in-group lane
+  // 4*jj + q supplies row 8h + 4r + jj (+16 ks), columns +4q..+4q+3
+  const int g16 = (lane >> 4) & 1, l16 = lane & 15, jj = l16 >> 2, q = l16 & 3;
+  int b_off[4][2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = wn * 128 + j * 32 + 16 * g16 + 4 * q;
+    const int chunk = n >> 3;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int k = 8 * h + 4 * r + jj;  // + 16*ks, which keeps k & 3
+      b_off[j][r] = kABytes + k * 512 + ((chunk ^ (4 * (k & 3))) << 4) + (q & 1) * 8;
+    }
+  }
+
+  auto load_frags = [&](const uint8_t* st, int ks, bf16x8 (&fa)[4], bf16x8 (&fb)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[i] = *reinterpret_cast<const bf16x8*>(st + a_row_off[i] + (((2 * ks + h) ^ a_sw[i]) << 4));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int col = n0 + wn * 128 + j * 32 + fr;
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(st + b_off[j][0] + ks * 16 * 512));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(st + b_off[j][1] + ks * 16 * 512));
+      fb[j] = __builtin_bit_cast(bf16x8, i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+    }
+  };
+
+  const int nk = K / BK;
+  for (int s = 0; s < kStages - 1 && s < nk; ++s) issue_stage(s);
+  // stage 0 published; first slice's fragments in registers
+  if (nk > 2) wait_vmcnt<2 * kDmaPerStage>();
+  else if (nk > 1) wait_vmcnt<kDmaPerStage>();
+  else wait_vmcnt<0>();
+  __syncthreads();
+  bf16x8 fa0[4], fb0[4], fa1[4], fb1[4];
+  load_frags(smem, 0, fa0, fb0);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint8_t* st = smem + (kt % kStages) * kStageBytes;
+    load_frags(st, 1, fa1, fb1);
+    mfma_slice(acc, fa0, fb0);
+    if (kt + 1 < nk) {
+      // publish stage kt+1 (this wave's DMA of it landed, then everyone's); past this barrier no
+      // wave reads stage kt-1's slot any more, so stage kt+3 can be issued into it
+      if (kt + 2 < nk) wait_vmcnt<kDmaPerStage>();
+      else wait_vmcnt<0>();
+      __syncthreads();
+      if (kt + kStages - 1 < nk) issue_stage(kt + kStages - 1);
+      load_frags(smem + ((kt + 1) % kStages) * kStageBytes, 0, fa0, fb0);
+    }
+    mfma_slice(acc, fa1, fb1);
+  }
+
+  // ---- epilogue: accumulator (i, j, r) of lane -> C row m0 + wm*128 + i*32 + lane%32,
+  //      column n0 + wn*128 + j*32 + 8*(r/4) + 4*(lane/32) + r%4: 4 consecutive columns per r/4
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < M && col < N) {
-          const int64_t o = int64_t(row) * N + col;
-          float v = acc[i][j][r];
-          if constexpr (RESID) v = v + bf16_to_f32(R[o]);
-          C[o] = f32_to_bf16(v);
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + wm * 128 + i * 32 + fr;
+    if (row >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = n0 + wn * 128 + j * 32 + 8 * g + 4 * h;
+        if (col >= N) continue;  // N % 8 == 0: a 4-column group is all in or all out
+        const int64_t o = int64_t(row) * N + col;
+        float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1], v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
+        if constexpr (RESID) {
+          const u32x2 rr = *reinterpret_cast<const u32x2*>(R + o);
+          v0 += bf16_lo(rr[0]);
+          v1 += bf16_hi(rr[0]);
+          v2 += bf16_lo(rr[1]);
+          v3 += bf16_hi(rr[1]);
         }
+        *reinterpret_cast<u32x2*>(C + o) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
       }
     }
   }
@@ -179,7 +235,9 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
   if (!a || !b || !c) return PTB_ERR_NULL;
   if (k == 0) return PTB_ERR_UNSUPPORTED;
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
-  if (k % BK || n % 8) return PTB_ERR_UNSUPPORTED;
+  if (k % 64 || n % 8) return PTB_ERR_UNSUPPORTED;
+  // buffer offsets are 32-bit: B and one 256-row panel of A must each stay under 4 GB
+  if (k * n * 2 >= (int64_t(1) << 32) || int64_t(BM) * k * 2 >= (int64_t(1) << 32)) return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
   const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
