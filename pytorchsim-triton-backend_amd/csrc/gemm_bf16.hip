@@ -28,13 +28,17 @@
 
 using namespace ptb;
 
-#pragma clang diagnostic ignored "-Winline-asm"
+
 
 namespace {
 
 constexpr int BM = 256, BN = 256, BK = 32;
 constexpr int kThreads = 256;
-constexpr int kStages = 4;
+#ifndef PTB_GEMM_STAGES
+#define PTB_GEMM_STAGES 4
+#endif
+constexpr int kStages = PTB_GEMM_STAGES;  // LDS ring depth, 3..5 (32 KB each of the 160 KB)
+static_assert(kStages >= 3 && kStages <= 5, "LDS ring of 3 to 5 stages");
 constexpr int kABytes = BM * BK * 2;           // 16 KB: 256 rows x 64 B
 constexpr int kBBytes = BK * BN * 2;           // 16 KB: 32 rows x 512 B
 constexpr int kStageBytes = kABytes + kBBytes;  // 32 KB
@@ -44,39 +48,7 @@ constexpr int kDmaPerStage = 8;                // buffer_load ... lds per wave p
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
-// 16 bytes per lane from global (buffer resource, byte offsets) straight into LDS at
-// lds_base + 16 * lane; lds_base is wave-uniform.  The compiler does not see the LDS write, so the
-// caller orders it with explicit s_waitcnt vmcnt + barrier.
-__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :: "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
-}
-
-__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  i32x4 r;
-  r[0] = int(uint32_t(a));
-  r[1] = int(uint32_t(a >> 32) & 0xffffu);  // stride 0
-  r[2] = int(bytes);                        // num_records: reads past it return 0
-  r[3] = 0x00020000;                        // dword data format (gfx9 family)
-  return r;
-}
-
-// acc[i][j] += (B^T A^T) block: C^T rows = N (j tile), C^T cols = M (i tile)
-__device__ __forceinline__ void mfma_slice(f32x16 (&acc)[4][4], const bf16x8 (&fa)[4], const bf16x8 (&fb)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-}
 
 template <bool RESID>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_bf16_kernel(
@@ -161,43 +133,72 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
   }
 
-  auto load_frags = [&](const uint8_t* st, int ks, bf16x8 (&fa)[4], bf16x8 (&fb)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      fa[i] = *reinterpret_cast<const bf16x8*>(st + a_row_off[i] + (((2 * ks + h) ^ a_sw[i]) << 4));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(st + b_off[j][0] + ks * 16 * 512));
-      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(st + b_off[j][1] + ks * 16 * 512));
-      fb[j] = __builtin_bit_cast(bf16x8, i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+  // One K slice's fragments, read in 12 pieces (4 A reads, 8 B half-reads) so that the reads can
+  // be spread between MFMAs.
+  struct Slice {
+    bf16x8 a[4];
+    bf16x8 b[4];
+    i16x4 blo[4];
+  };
+  auto read_piece = [&](const uint8_t* st, int ks, int p, Slice& f) {
+    if (p < 4) {
+      f.a[p] = *reinterpret_cast<const bf16x8*>(st + a_row_off[p] + (((2 * ks + h) ^ a_sw[p]) << 4));
+    } else {
+      const int j = (p - 4) >> 1, r = (p - 4) & 1;
+      const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(st + b_off[j][r] + ks * 16 * 512));
+      if (r == 0) f.blo[j] = v;
+      else f.b[j] = __builtin_bit_cast(bf16x8, i16x8{f.blo[j][0], f.blo[j][1], f.blo[j][2], f.blo[j][3], v[0], v[1], v[2], v[3]});
     }
   };
+  auto mfma_one = [&](const Slice& f, int u) {
+    const int i = u >> 2, j = u & 3;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
+  };
+  // t-th of this wave's 8 DMA instructions of stage kt (4 for A, then 4 for B)
+  auto dma_one = [&](int kt, int t) {
+    const uint32_t st = lds0 + uint32_t(kt % kStages) * kStageBytes;
+    if (t < 4)
+      dma16(rsrc_a, __builtin_amdgcn_readfirstlane(st + (wave * 4 + t) * 1024), a_voff[t], uint32_t(kt * BK) * 2u);
+    else
+      dma16(rsrc_b, __builtin_amdgcn_readfirstlane(st + kABytes + (wave * 4 + t - 4) * 1024), b_voff[t - 4],
+            uint32_t(kt * BK) * uint32_t(N) * 2u);
+  };
 
+  // The DMA stream runs kStages-1 stages ahead of the MFMAs and does not stop at the last K step:
+  // stages past the end read zeros (num_records) into slots nobody reads any more, which keeps the
+  // loop free of branches; everything is drained before the epilogue.
   const int nk = K / BK;
-  for (int s = 0; s < kStages - 1 && s < nk; ++s) issue_stage(s);
-  // stage 0 published; first slice's fragments in registers
-  if (nk > 2) wait_vmcnt<2 * kDmaPerStage>();
-  else if (nk > 1) wait_vmcnt<kDmaPerStage>();
-  else wait_vmcnt<0>();
-  __syncthreads();
-  bf16x8 fa0[4], fb0[4], fa1[4], fb1[4];
-  load_frags(smem, 0, fa0, fb0);
+  for (int s = 0; s < kStages - 1; ++s) issue_stage(s);
+  wait_vmcnt<(kStages - 2) * kDmaPerStage>();  // stage 0 landed (this wave's part)
+  __syncthreads();                              // ... and everyone's
+  Slice s0, s1;
+#pragma unroll
+  for (int p = 0; p < 12; ++p) read_piece(smem, 0, p, s0);
 
+  // Each K step: slice 0's MFMAs with slice 1's reads folded in; the barrier publishing stage kt+1;
+  // slice 1's MFMAs with the DMA of stage kt+3 and the reads of stage kt+1's slice 0 folded in.
+  // sched_barrier(0) pins that interleave, so the matrix core is fed between memory instructions.
   for (int kt = 0; kt < nk; ++kt) {
     const uint8_t* st = smem + (kt % kStages) * kStageBytes;
-    load_frags(st, 1, fa1, fb1);
-    mfma_slice(acc, fa0, fb0);
-    if (kt + 1 < nk) {
-      // publish stage kt+1 (this wave's DMA of it landed, then everyone's); past this barrier no
-      // wave reads stage kt-1's slot any more, so stage kt+3 can be issued into it
-      if (kt + 2 < nk) wait_vmcnt<kDmaPerStage>();
-      else wait_vmcnt<0>();
-      __syncthreads();
-      if (kt + kStages - 1 < nk) issue_stage(kt + kStages - 1);
-      load_frags(smem + ((kt + 1) % kStages) * kStageBytes, 0, fa0, fb0);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      mfma_one(s0, u);
+      if (u < 12) read_piece(st, 1, u, s1);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    mfma_slice(acc, fa1, fb1);
+    // stage kt+1 landed; past this barrier no wave reads stage kt-1's slot, which takes kt+3
+    wait_vmcnt<(kStages - 3) * kDmaPerStage>();
+    __syncthreads();
+    const uint8_t* nst = smem + ((kt + 1) % kStages) * kStageBytes;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      mfma_one(s1, u);
+      if (u < 8) dma_one(kt + kStages - 1, u);
+      if (u >= 1 && u < 13) read_piece(nst, 0, u - 1, s0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
+  wait_vmcnt<0>();
 
   // ---- epilogue: accumulator (i, j, r) of lane -> C row m0 + wm*128 + i*32 + lane%32,
   //      column n0 + wn*128 + j*32 + 8*(r/4) + 4*(lane/32) + r%4: 4 consecutive columns per r/4

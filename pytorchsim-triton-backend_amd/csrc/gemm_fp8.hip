@@ -6,52 +6,44 @@
 //   gemm_fp8     : C[m,n] = bf16( (sum_k Aq[m,k] * Wt[n,k]) * sa[m] * sw[n] ), fp32 accumulation
 //
 // The GEMM uses v_mfma_f32_32x32x64_f8f6f4 (both operands e4m3, no block scales): a 256x256
-// workgroup tile, K step 128, 4 waves of 128x128 (4x4 accumulators of 32x32).  Both operands are
-// K-contiguous rows, so each stage is a plain copy into LDS (rows padded 128 -> 144 B, conflict-free
-// 2 x 128-bit fragment reads); stages are double-buffered with one barrier per K step.
+// workgroup tile, K step 64, 4 waves of 128x128 (4x4 accumulators of 32x32).  Both operands are
+// K-contiguous rows of 64 bytes per K step; they move HBM -> LDS with buffer_load_dwordx4 ... lds
+// into a ring of four 32 KB stages, three K steps ahead of the matrix cores.  Within a row the four
+// 16-byte chunks are XOR-swizzled by (row >> 2) & 3, so the two 128-bit fragment reads per lane are
+// bank-conflict free.  The fragments of stage k+1 are read (behind the barrier that publishes it)
+// while the MFMAs of stage k run.  MFMAs take W as the first operand, so accumulators hold C^T
+// blocks and each lane stores 4 consecutive columns of a row of C at once.
 #include "ptb_common.h"
 
 using namespace ptb;
 
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 128;  // BK in bytes (= fp8 elements)
-constexpr int LDB = BK + 16;                 // padded LDS row, bytes
+constexpr int BM = 256, BN = 256, BK = 64;     // BK in bytes (= fp8 elements)
 constexpr int kThreads = 256;
-constexpr int kStageBytes = (BM + BN) * LDB;
+constexpr int kStages = 4;
+constexpr int kOpBytes = BM * BK;              // 16 KB per operand per stage
+constexpr int kStageBytes = 2 * kOpBytes;
 constexpr int kGroupM = 8;
+constexpr int kDmaPerStage = 8;
 
-struct Slice {
-  u32x4 a[8];
-  u32x4 w[8];
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+struct Frags {
+  i32x8 a[4];
+  i32x8 w[4];
 };
 
-__device__ __forceinline__ Slice gload(const uint8_t* const (&a_src)[8], const uint8_t* const (&w_src)[8], int k0) {
-  Slice s;
-#pragma unroll
-  for (int p = 0; p < 8; ++p) s.a[p] = *reinterpret_cast<const u32x4*>(a_src[p] + k0);
-#pragma unroll
-  for (int p = 0; p < 8; ++p) s.w[p] = *reinterpret_cast<const u32x4*>(w_src[p] + k0);
-  return s;
-}
-
-__device__ __forceinline__ void sstore(const Slice& s, uint8_t* a_dst, uint8_t* w_dst, int st) {
-#pragma unroll
-  for (int p = 0; p < 8; ++p) *reinterpret_cast<u32x4*>(a_dst + st * kStageBytes + p * 32 * LDB) = s.a[p];
-#pragma unroll
-  for (int p = 0; p < 8; ++p) *reinterpret_cast<u32x4*>(w_dst + st * kStageBytes + p * 32 * LDB) = s.w[p];
-}
-
-__device__ __forceinline__ i32x8 frag(const uint8_t* p) {
-  const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
-  const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 16);
+__device__ __forceinline__ i32x8 frag32(const uint8_t* row, int c0, int sw) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(row + ((c0 ^ sw) << 4));
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(row + (((c0 + 1) ^ sw) << 4));
   return i32x8{int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
 }
 
-__global__ __launch_bounds__(kThreads, 1) void gemm_fp8_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_fp8_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ W,
     const float* __restrict__ SW, uint16_t* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStageBytes];
 
   const int ntiles = tiles_m * tiles_n;
   int pid = blockIdx.x;
@@ -67,16 +59,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_kernel(
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  const int chunk = tid & 7, lrow = tid >> 3;
-  const uint8_t* a_src[8];
-  const uint8_t* w_src[8];
+  // loaders: rows past M (A) or N (W) read as zero through num_records
+  const i32x4 rsrc_a = make_rsrc(A + int64_t(m0) * K, uint32_t(min(BM, M - m0)) * uint32_t(K));
+  const i32x4 rsrc_w = make_rsrc(W + int64_t(n0) * K, uint32_t(min(BN, N - n0)) * uint32_t(K));
+  // instruction t of this wave covers rows (4*wave+t)*16 .. +16; lane -> row lane/4, slot lane%4
+  uint32_t voff[4];
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    a_src[p] = A + int64_t(min(m0 + p * 32 + lrow, M - 1)) * K + chunk * 16;
-    w_src[p] = W + int64_t(min(n0 + p * 32 + lrow, N - 1)) * K + chunk * 16;
+  for (int t = 0; t < 4; ++t) {
+    const int row = (wave * 4 + t) * 16 + (lane >> 2);
+    voff[t] = uint32_t(row * K + (((lane & 3) ^ ((row >> 2) & 3)) << 4));
   }
-  uint8_t* const a_dst = smem + lrow * LDB + chunk * 16;
-  uint8_t* const w_dst = smem + BM * LDB + lrow * LDB + chunk * 16;
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
+  auto issue_stage = [&](int kt) {
+    const uint32_t st = lds0 + uint32_t(kt % kStages) * kStageBytes;
+    const uint32_t soff = uint32_t(kt * BK);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) dma16(rsrc_a, __builtin_amdgcn_readfirstlane(st + (wave * 4 + t) * 1024), voff[t], soff);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      dma16(rsrc_w, __builtin_amdgcn_readfirstlane(st + kOpBytes + (wave * 4 + t) * 1024), voff[t], soff);
+  };
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -86,48 +88,70 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // lane -> row/col lane % 32, K half (32 bytes) lane / 32
-  const int fr = lane & 31, fk = (lane >> 5) * 32;
-  const int a_off = (wm * 128 + fr) * LDB + fk;
-  const int w_off = BM * LDB + (wn * 128 + fr) * LDB + fk;
-
-  const int nk = K / BK;
-  sstore(gload(a_src, w_src, 0), a_dst, w_dst, 0);
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const uint8_t* st = smem + (kt & 1) * kStageBytes;
-    const bool more = kt + 1 < nk;
-    Slice nxt;
-    if (more) nxt = gload(a_src, w_src, (kt + 1) * BK);
+  // lane -> row (or column) lane % 32, K half (32 bytes = chunks 2h, 2h+1) lane / 32
+  const int fr = lane & 31, h = lane >> 5;
+  int a_row[4], w_row[4], a_sw[4], w_sw[4];
 #pragma unroll
-    for (int ks = 0; ks < BK / 64; ++ks) {
-      i32x8 fa[4], fw[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        fa[i] = frag(st + a_off + i * 32 * LDB + ks * 64);
-        fw[i] = frag(st + w_off + i * 32 * LDB + ks * 64);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fw[j], acc[i][j], 0, 0, 0, 0, 0, 0);
-    }
-    if (more) sstore(nxt, a_dst, w_dst, (kt + 1) & 1);
-    __syncthreads();
+  for (int i = 0; i < 4; ++i) {
+    const int m = wm * 128 + i * 32 + fr, n = wn * 128 + i * 32 + fr;
+    a_row[i] = m * BK;
+    w_row[i] = kOpBytes + n * BK;
+    a_sw[i] = (m >> 2) & 3;
+    w_sw[i] = (n >> 2) & 3;
   }
-
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = n0 + wn * 128 + j * 32 + fr;
-    const float sw = SW[min(col, N - 1)];
+  auto load_frags = [&](const uint8_t* st) {
+    Frags f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      f.a[i] = frag32(st + a_row[i], 2 * h, a_sw[i]);
+      f.w[i] = frag32(st + w_row[i], 2 * h, w_sw[i]);
+    }
+    return f;
+  };
+
+  const int nk = K / BK;
+  for (int s = 0; s < kStages - 1 && s < nk; ++s) issue_stage(s);
+  if (nk > 2) wait_vmcnt<2 * kDmaPerStage>();
+  else if (nk > 1) wait_vmcnt<kDmaPerStage>();
+  else wait_vmcnt<0>();
+  __syncthreads();
+  Frags cur = load_frags(smem);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    Frags nxt;
+    if (kt + 1 < nk) {
+      // publish stage kt+1; past this barrier stage kt-1's slot is free for stage kt+3
+      if (kt + 2 < nk) wait_vmcnt<kDmaPerStage>();
+      else wait_vmcnt<0>();
+      __syncthreads();
+      if (kt + kStages - 1 < nk) issue_stage(kt + kStages - 1);
+      nxt = load_frags(smem + ((kt + 1) % kStages) * kStageBytes);
+    }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < M && col < N) C[int64_t(row) * N + col] = f32_to_bf16((acc[i][j][r] * SA[row]) * sw);
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.w[j], cur.a[i], acc[i][j], 0, 0, 0, 0, 0, 0);
+    cur = nxt;
+  }
+
+  // accumulator (i, j, r) of lane -> C row m0 + wm*128 + i*32 + lane%32, columns
+  // n0 + wn*128 + j*32 + 8*(r/4) + 4*(lane/32) + r%4
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + wm * 128 + i * 32 + fr;
+    if (row >= M) continue;
+    const float sa = SA[row];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = n0 + wn * 128 + j * 32 + 8 * g + 4 * h;
+        if (col >= N) continue;  // N % 16 == 0: a 4-column group is all in or all out
+        const f32x4v sw = *reinterpret_cast<const f32x4v*>(SW + col);
+        const float v0 = (acc[i][j][4 * g] * sa) * sw[0], v1 = (acc[i][j][4 * g + 1] * sa) * sw[1];
+        const float v2 = (acc[i][j][4 * g + 2] * sa) * sw[2], v3 = (acc[i][j][4 * g + 3] * sa) * sw[3];
+        *reinterpret_cast<u32x2*>(C + int64_t(row) * N + col) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
       }
     }
   }
@@ -298,8 +322,10 @@ PTB_EXPORT int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* 
   if (!aq || !sa || !wq_t || !sw || !c) return PTB_ERR_NULL;
   if (k == 0) return PTB_ERR_UNSUPPORTED;
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
-  if (k % BK || n % 16) return PTB_ERR_UNSUPPORTED;
-  if (!aligned16(aq) || !aligned16(wq_t) || (reinterpret_cast<uintptr_t>(c) & 1u)) return PTB_ERR_ALIGN;
+  if (k % 128 || n % 16) return PTB_ERR_UNSUPPORTED;
+  if (int64_t(BM) * k >= (int64_t(1) << 32)) return PTB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
+  if (!aligned16(aq) || !aligned16(wq_t) || !aligned16(sw) || (reinterpret_cast<uintptr_t>(c) & 7u))
+    return PTB_ERR_ALIGN;
   const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
   gemm_fp8_kernel<<<dim3(unsigned(tm * tn)), dim3(kThreads), 0, static_cast<hipStream_t>(stream)>>>(

@@ -7,6 +7,9 @@
 
 #include "ptb_amd.h"
 
+// dma16 below clobbers m0 on purpose (its LDS base register); nothing else here uses m0.
+#pragma clang diagnostic ignored "-Winline-asm"
+
 #define PTB_EXPORT extern "C" __attribute__((visibility("default")))
 
 namespace ptb {
@@ -124,6 +127,32 @@ __device__ __forceinline__ u32x4 column8x8(const u32x4 (&r)[8]) {
     o[q] = (C % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
   }
   return o;
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource for raw byte-offset loads: reads at offsets >= bytes return 0.
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = int(uint32_t(a));
+  r[1] = int(uint32_t(a >> 32) & 0xffffu);  // stride 0
+  r[2] = int(bytes);                        // num_records
+  r[3] = 0x00020000;                        // dword data format (gfx9 family)
+  return r;
+}
+
+// 16 bytes per lane from global (buffer resource, byte offsets voff + soff) straight into LDS at
+// lds_base + 16 * lane (buffer_load_dwordx4 ... lds, no VGPR staging); lds_base is wave-uniform.
+// The compiler does not see the LDS write: callers order it with wait_vmcnt + a barrier.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
 
 __host__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
