@@ -238,7 +238,8 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
   if (k % 64 || n % 8) return PTB_ERR_UNSUPPORTED;
   // buffer offsets are 32-bit: B and one 256-row panel of A must each stay under 4 GB
-  if (k * n * 2 >= (int64_t(1) << 32) || int64_t(BM) * k * 2 >= (int64_t(1) << 32)) return PTB_ERR_UNSUPPORTED;
+  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || int64_t(BM) * k * 2 >= (int64_t(1) << 32))
+    return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
   const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;

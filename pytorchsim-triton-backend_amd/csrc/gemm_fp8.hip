@@ -5,45 +5,55 @@
 //                  Wt[N,K] (K contiguous), which is how the GEMM streams it
 //   gemm_fp8     : C[m,n] = bf16( (sum_k Aq[m,k] * Wt[n,k]) * sa[m] * sw[n] ), fp32 accumulation
 //
-// The GEMM uses v_mfma_f32_32x32x64_f8f6f4 (both operands e4m3, no block scales): a 256x256
-// workgroup tile, K step 64, 4 waves of 128x128 (4x4 accumulators of 32x32).  Both operands are
-// K-contiguous rows of 64 bytes per K step; they move HBM -> LDS with buffer_load_dwordx4 ... lds
-// into a ring of four 32 KB stages, three K steps ahead of the matrix cores.  Within a row the four
-// 16-byte chunks are XOR-swizzled by (row >> 2) & 3, so the two 128-bit fragment reads per lane are
-// bank-conflict free.  The fragments of stage k+1 are read (behind the barrier that publishes it)
-// while the MFMAs of stage k run.  MFMAs take W as the first operand, so accumulators hold C^T
-// blocks and each lane stores 4 consecutive columns of a row of C at once.
+// The GEMM uses v_mfma_f32_32x32x64_f8f6f4 (both operands e4m3, no block scales): a 256xBN
+// workgroup tile (BN = 256, or 128 when 256x256 tiles would leave CUs idle), K step 64, 4 waves in
+// a 2x2 arrangement, each wave 128 x BN/2 as 32x32 accumulators.  Both operands are K-contiguous
+// rows of 64 bytes per K step; they move HBM -> LDS with buffer_load_dwordx4 ... lds into a ring of
+// four stages, three K steps ahead of the matrix cores.  Within a row the four 16-byte chunks are
+// XOR-swizzled by (row >> 2) & 3, so the two 128-bit fragment reads per lane are bank-conflict
+// free.  Each K step issues half of its MFMAs, passes the barrier that publishes the next stage,
+// then issues the other half with the next stage's DMA and fragment reads folded in between them.
+// MFMAs take W as the first operand, so accumulators hold C^T blocks and each lane stores 4
+// consecutive columns of a row of C at once.
 #include "ptb_common.h"
 
 using namespace ptb;
 
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64;     // BK in bytes (= fp8 elements)
+constexpr int BM = 256, BK = 64;   // BK in bytes (= fp8 elements)
 constexpr int kThreads = 256;
 constexpr int kStages = 4;
-constexpr int kOpBytes = BM * BK;              // 16 KB per operand per stage
-constexpr int kStageBytes = 2 * kOpBytes;
 constexpr int kGroupM = 8;
-constexpr int kDmaPerStage = 8;
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-struct Frags {
-  i32x8 a[4];
-  i32x8 w[4];
+template <int BN>
+struct Cfg {
+  static constexpr int WNT = BN / 64;                  // 32-wide column tiles per wave
+  static constexpr int kABytes = BM * BK;              // 16 KB
+  static constexpr int kWBytes = BN * BK;
+  static constexpr int kStageBytes = kABytes + kWBytes;
+  static constexpr int kDmaA = BM / 16 / 4;            // per wave per stage
+  static constexpr int kDmaW = BN / 16 / 4;
+  static constexpr int kDma = kDmaA + kDmaW;
+  static constexpr int kPieces = 2 * (4 + WNT);        // 128-bit fragment reads per stage
+  static constexpr int kMfma = 4 * WNT;
 };
 
-__device__ __forceinline__ i32x8 frag32(const uint8_t* row, int c0, int sw) {
-  const u32x4 lo = *reinterpret_cast<const u32x4*>(row + ((c0 ^ sw) << 4));
-  const u32x4 hi = *reinterpret_cast<const u32x4*>(row + (((c0 + 1) ^ sw) << 4));
-  return i32x8{int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
-}
+template <int BN>
+struct Frags {
+  i32x8 a[4];
+  i32x8 w[Cfg<BN>::WNT];
+  u32x4 lo[4 + Cfg<BN>::WNT];
+};
 
+template <int BN>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_fp8_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ W,
     const float* __restrict__ SW, uint16_t* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStageBytes];
+  using G = Cfg<BN>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * G::kStageBytes];
 
   const int ntiles = tiles_m * tiles_n;
   int pid = blockIdx.x;
@@ -59,94 +69,119 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // loaders: rows past M (A) or N (W) read as zero through num_records
+  // loaders: rows past M (A) or N (W) read as zero through num_records; stages past K read
+  // zeros too (the DMA stream runs ahead without a branch)
   const i32x4 rsrc_a = make_rsrc(A + int64_t(m0) * K, uint32_t(min(BM, M - m0)) * uint32_t(K));
   const i32x4 rsrc_w = make_rsrc(W + int64_t(n0) * K, uint32_t(min(BN, N - n0)) * uint32_t(K));
-  // instruction t of this wave covers rows (4*wave+t)*16 .. +16; lane -> row lane/4, slot lane%4
-  uint32_t voff[4];
+  // DMA instruction d of this wave covers rows 16*(kDma_op*wave + d) .. +16; lane -> row lane/4,
+  // slot lane%4 holding chunk (lane%4) ^ ((row >> 2) & 3)
+  auto voff_of = [&](int row) { return uint32_t(row * K + (((lane & 3) ^ ((row >> 2) & 3)) << 4)); };
+  uint32_t a_voff[G::kDmaA], w_voff[G::kDmaW];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int row = (wave * 4 + t) * 16 + (lane >> 2);
-    voff[t] = uint32_t(row * K + (((lane & 3) ^ ((row >> 2) & 3)) << 4));
-  }
+  for (int t = 0; t < G::kDmaA; ++t) a_voff[t] = voff_of((wave * G::kDmaA + t) * 16 + (lane >> 2));
+#pragma unroll
+  for (int t = 0; t < G::kDmaW; ++t) w_voff[t] = voff_of((wave * G::kDmaW + t) * 16 + (lane >> 2));
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
-  auto issue_stage = [&](int kt) {
-    const uint32_t st = lds0 + uint32_t(kt % kStages) * kStageBytes;
+  auto dma_one = [&](int kt, int d) {
+    const uint32_t st = lds0 + uint32_t(kt % kStages) * G::kStageBytes;
     const uint32_t soff = uint32_t(kt * BK);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) dma16(rsrc_a, __builtin_amdgcn_readfirstlane(st + (wave * 4 + t) * 1024), voff[t], soff);
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      dma16(rsrc_w, __builtin_amdgcn_readfirstlane(st + kOpBytes + (wave * 4 + t) * 1024), voff[t], soff);
+    if (d < G::kDmaA)
+      dma16(rsrc_a, __builtin_amdgcn_readfirstlane(st + (wave * G::kDmaA + d) * 1024), a_voff[d], soff);
+    else
+      dma16(rsrc_w, __builtin_amdgcn_readfirstlane(st + G::kABytes + (wave * G::kDmaW + d - G::kDmaA) * 1024),
+            w_voff[d - G::kDmaA], soff);
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][G::WNT];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < G::WNT; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   // lane -> row (or column) lane % 32, K half (32 bytes = chunks 2h, 2h+1) lane / 32
   const int fr = lane & 31, h = lane >> 5;
-  int a_row[4], w_row[4], a_sw[4], w_sw[4];
+  int row_off[4 + G::WNT], row_sw[4 + G::WNT];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int m = wm * 128 + i * 32 + fr, n = wn * 128 + i * 32 + fr;
-    a_row[i] = m * BK;
-    w_row[i] = kOpBytes + n * BK;
-    a_sw[i] = (m >> 2) & 3;
-    w_sw[i] = (n >> 2) & 3;
+    const int m = wm * 128 + i * 32 + fr;
+    row_off[i] = m * BK;
+    row_sw[i] = (m >> 2) & 3;
   }
-  auto load_frags = [&](const uint8_t* st) {
-    Frags f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f.a[i] = frag32(st + a_row[i], 2 * h, a_sw[i]);
-      f.w[i] = frag32(st + w_row[i], 2 * h, w_sw[i]);
+  for (int j = 0; j < G::WNT; ++j) {
+    const int n = wn * (BN / 2) + j * 32 + fr;
+    row_off[4 + j] = G::kABytes + n * BK;
+    row_sw[4 + j] = (n >> 2) & 3;
+  }
+  // piece p: operand row t = p / 2, half c = p % 2 (chunk 2h + c)
+  auto read_piece = [&](const uint8_t* st, int p, Frags<BN>& f) {
+    const int t = p >> 1, c = p & 1;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(st + row_off[t] + (((2 * h + c) ^ row_sw[t]) << 4));
+    if (c == 0) {
+      f.lo[t] = v;
+    } else {
+      const i32x8 x = i32x8{int(f.lo[t][0]), int(f.lo[t][1]), int(f.lo[t][2]), int(f.lo[t][3]),
+                            int(v[0]), int(v[1]), int(v[2]), int(v[3])};
+      if (t < 4) f.a[t] = x;
+      else f.w[t - 4] = x;
     }
-    return f;
+  };
+  auto mfma_one = [&](const Frags<BN>& f, int u) {
+    const int i = u / G::WNT, j = u % G::WNT;
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[j], f.a[i], acc[i][j], 0, 0, 0, 0, 0, 0);
   };
 
   const int nk = K / BK;
-  for (int s = 0; s < kStages - 1 && s < nk; ++s) issue_stage(s);
-  if (nk > 2) wait_vmcnt<2 * kDmaPerStage>();
-  else if (nk > 1) wait_vmcnt<kDmaPerStage>();
-  else wait_vmcnt<0>();
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s)
+#pragma unroll
+    for (int d = 0; d < G::kDma; ++d) dma_one(s, d);
+  wait_vmcnt<(kStages - 2) * G::kDma>();
   __syncthreads();
-  Frags cur = load_frags(smem);
+  Frags<BN> cur, nxt;
+#pragma unroll
+  for (int p = 0; p < G::kPieces; ++p) read_piece(smem, p, cur);
 
+  constexpr int kHalf = G::kMfma / 2;
   for (int kt = 0; kt < nk; ++kt) {
-    Frags nxt;
-    if (kt + 1 < nk) {
-      // publish stage kt+1; past this barrier stage kt-1's slot is free for stage kt+3
-      if (kt + 2 < nk) wait_vmcnt<kDmaPerStage>();
-      else wait_vmcnt<0>();
-      __syncthreads();
-      if (kt + kStages - 1 < nk) issue_stage(kt + kStages - 1);
-      nxt = load_frags(smem + ((kt + 1) % kStages) * kStageBytes);
+#pragma unroll
+    for (int u = 0; u < kHalf; ++u) mfma_one(cur, u);
+    __builtin_amdgcn_sched_barrier(0);
+    // stage kt+1 landed; past this barrier stage kt-1's slot is free for stage kt+3
+    wait_vmcnt<(kStages - 3) * G::kDma>();
+    __syncthreads();
+    const uint8_t* nst = smem + ((kt + 1) % kStages) * G::kStageBytes;
+    // the second half of the MFMAs, with the DMA of stage kt+3 and the reads of stage kt+1 between
+    constexpr int kSlots = (G::kDma + G::kPieces + kHalf - 1) / kHalf;
+#pragma unroll
+    for (int u = 0; u < kHalf; ++u) {
+      mfma_one(cur, kHalf + u);
+#pragma unroll
+      for (int q = 0; q < kSlots; ++q) {
+        const int e = u * kSlots + q;
+        if (e < G::kDma) dma_one(kt + kStages - 1, e);
+        else if (e < G::kDma + G::kPieces) read_piece(nst, e - G::kDma, nxt);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.w[j], cur.a[i], acc[i][j], 0, 0, 0, 0, 0, 0);
     cur = nxt;
   }
+  wait_vmcnt<0>();
 
   // accumulator (i, j, r) of lane -> C row m0 + wm*128 + i*32 + lane%32, columns
-  // n0 + wn*128 + j*32 + 8*(r/4) + 4*(lane/32) + r%4
+  // n0 + wn*BN/2 + j*32 + 8*(r/4) + 4*(lane/32) + r%4
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = m0 + wm * 128 + i * 32 + fr;
     if (row >= M) continue;
     const float sa = SA[row];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < G::WNT; ++j) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int col = n0 + wn * 128 + j * 32 + 8 * g + 4 * h;
+        const int col = n0 + wn * (BN / 2) + j * 32 + 8 * g + 4 * h;
         if (col >= N) continue;  // N % 16 == 0: a 4-column group is all in or all out
         const f32x4v sw = *reinterpret_cast<const f32x4v*>(SW + col);
         const float v0 = (acc[i][j][4 * g] * sa) * sw[0], v1 = (acc[i][j][4 * g + 1] * sa) * sw[1];
@@ -326,10 +361,21 @@ PTB_EXPORT int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* 
   if (int64_t(BM) * k >= (int64_t(1) << 32)) return PTB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   if (!aligned16(aq) || !aligned16(wq_t) || !aligned16(sw) || (reinterpret_cast<uintptr_t>(c) & 7u))
     return PTB_ERR_ALIGN;
-  const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
+  // 256x256 tiles unless that leaves CUs idle, then 256x128
+  const int64_t tm = (m + BM - 1) / BM;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const bool wide = tm * ((n + 255) / 256) >= cus;
+  const int bn = wide ? 256 : 128;
+  const int64_t tn = (n + bn - 1) / bn;
   if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
-  gemm_fp8_kernel<<<dim3(unsigned(tm * tn)), dim3(kThreads), 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint8_t*>(aq), sa, static_cast<const uint8_t*>(wq_t), sw, static_cast<uint16_t*>(c),
-      int(m), int(n), int(k), int(tm), int(tn));
+  const dim3 grid(unsigned(tm * tn)), block(kThreads);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (wide)
+    gemm_fp8_kernel<256><<<grid, block, 0, s>>>(static_cast<const uint8_t*>(aq), sa, static_cast<const uint8_t*>(wq_t),
+                                                 sw, static_cast<uint16_t*>(c), int(m), int(n), int(k), int(tm), int(tn));
+  else
+    gemm_fp8_kernel<128><<<grid, block, 0, s>>>(static_cast<const uint8_t*>(aq), sa, static_cast<const uint8_t*>(wq_t),
+                                                 sw, static_cast<uint16_t*>(c), int(m), int(n), int(k), int(tm), int(tn));
   return launch_status();
 }
