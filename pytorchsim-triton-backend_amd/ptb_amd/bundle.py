@@ -1,0 +1,131 @@
+"""Read the reference's kernel bundle (``validation/pytorchsim/``) without running any of its code.
+
+Each workload directory holds ``manifest.json`` -- ``{workload, suite, <keys>..., launches: [{kernel,
+dir}], externs}`` -- and per launched kernel a ``<kernel>_spec.py`` (a ``KernelSpec(...)`` call with
+literal arguments) beside ``<kernel>_triton.py`` (validation/gemm/simulate_shapes.py:363-405 loads
+the same files).  The spec is parsed with :mod:`ast` (its keyword values are literals and ``Arg``
+calls), never imported, so no reference module and no ``pytorchsim_triton_compiler`` is needed.
+The Triton source is kept as text: the kernel families that need index facts read them from it.
+"""
+from __future__ import annotations
+
+import ast
+import json
+import os
+from dataclasses import dataclass, field
+
+from .contract import Arg, KernelSpec
+
+SUITE_KEYS = {
+    # validation/{vector,gemm,attention,layer,qwen3_8b}/simulate_shapes.py KEYS
+    "vector": ("program", "R", "C"),
+    "gemm": ("M", "K", "N"),
+    "attention": ("kind", "Hq", "Hkv", "S"),
+    "layer": ("section", "name", "T", "S"),
+    "qwen3_8b": ("section", "name", "T", "S"),
+}
+
+
+@dataclass
+class BundleKernel:
+    dir: str
+    spec: KernelSpec
+    source: str          # the Triton kernel's text ("" when absent)
+    launches: int = 1    # how many times the workload launches it
+
+
+@dataclass
+class Workload:
+    name: str
+    suite: str
+    keys: dict
+    kernels: list = field(default_factory=list)   # BundleKernel, in first-launch order
+    order: list = field(default_factory=list)     # kernel dirs in launch order (repeats kept)
+    path: str = ""
+
+
+def _literal(node):
+    if isinstance(node, ast.Call) and getattr(node.func, "id", None) == "Arg":
+        vals = [ast.literal_eval(a) for a in node.args]
+        kw = {k.arg: ast.literal_eval(k.value) for k in node.keywords}
+        return Arg(*vals, **kw)
+    if isinstance(node, (ast.List, ast.Tuple)):
+        items = [_literal(e) for e in node.elts]
+        return items if isinstance(node, ast.List) else tuple(items)
+    return ast.literal_eval(node)
+
+
+_SPEC_FIELDS = ("name", "signature", "constexprs", "args", "grid", "rtol", "atol", "parallel_axes", "extra",
+                "graph_prefetch")
+
+
+def parse_spec_text(text: str, where: str = "<spec>") -> KernelSpec:
+    """The KernelSpec a reference kernel file declares as ``SPEC = KernelSpec(...)``, read from its
+    text.  Keyword arguments that are not literals (kernel, reference, make_inputs) are skipped."""
+    tree = ast.parse(text, where)
+    for node in tree.body:
+        if (isinstance(node, ast.Assign) and any(getattr(t, "id", None) == "SPEC" for t in node.targets)
+                and isinstance(node.value, ast.Call)):
+            kw = {}
+            for k in node.value.keywords:
+                if k.arg in _SPEC_FIELDS:
+                    kw[k.arg] = _literal(k.value)
+            kw.setdefault("constexprs", {})
+            kw.setdefault("signature", {})
+            return KernelSpec(**kw)
+    raise ValueError(f"{where}: no SPEC = KernelSpec(...) assignment")
+
+
+def load_kernel_dir(path: str) -> tuple:
+    """(spec, triton source text) of one bundle kernel directory."""
+    specs = sorted(f for f in os.listdir(path) if f.endswith("_spec.py"))
+    if len(specs) != 1:
+        raise ValueError(f"{path}: expected one *_spec.py, found {specs}")
+    with open(os.path.join(path, specs[0])) as fh:
+        spec = parse_spec_text(fh.read(), specs[0])
+    src = ""
+    tri = specs[0][: -len("_spec.py")] + "_triton.py"
+    if os.path.exists(os.path.join(path, tri)):
+        with open(os.path.join(path, tri)) as fh:
+            src = fh.read()
+    return spec, src
+
+
+def load_workload(path: str) -> Workload:
+    with open(os.path.join(path, "manifest.json")) as fh:
+        man = json.load(fh)
+    suite = man.get("suite", "")
+    keys = {k: man[k] for k in SUITE_KEYS.get(suite, ()) if k in man}
+    w = Workload(name=man["workload"], suite=suite, keys=keys, path=path)
+    seen = {}
+    for launch in man["launches"]:
+        d = launch["dir"]
+        w.order.append(d)
+        if d in seen:
+            seen[d].launches += 1
+            continue
+        spec, src = load_kernel_dir(os.path.join(path, d))
+        bk = BundleKernel(dir=d, spec=spec, source=src)
+        seen[d] = bk
+        w.kernels.append(bk)
+    return w
+
+
+def load_bundle(bundle_dir: str, suite: str | None = None, where=None) -> list:
+    """Every workload under `bundle_dir` (optionally of one suite, and matching `where`, a dict of
+    key -> value or a callable), sorted by name."""
+    out = []
+    for name in sorted(os.listdir(bundle_dir)):
+        p = os.path.join(bundle_dir, name)
+        if not os.path.isfile(os.path.join(p, "manifest.json")):
+            continue
+        with open(os.path.join(p, "manifest.json")) as fh:
+            man = json.load(fh)
+        if suite and man.get("suite") != suite:
+            continue
+        if isinstance(where, dict) and any(str(man.get(k)) != str(v) for k, v in where.items()):
+            continue
+        if callable(where) and not where(man):
+            continue
+        out.append(load_workload(p))
+    return out

@@ -1,0 +1,149 @@
+"""The operator contract of the reference's kernel files, restated for the HIP path.
+
+A kernel file declares a ``KernelSpec``: name, Triton signature, constexprs, the memory-backed
+arguments (``Arg(name, role, dtype, shape)`` with flat shapes), the launch grid, scalars
+(``extra["scalar_values"]``), seeded ``make_inputs`` and tolerances
+(reference: pytorchsim_triton_compiler/contract/kernel_spec.py:24-139).  A compiled kernel is
+described by a manifest with the same facts (contract/kernel_object.py:333-359).  This module
+keeps those shapes of data so that a caller of the reference's boundary can hand its specs,
+manifests and tensors to the MI355X path unchanged; it holds no compiler state.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Callable
+
+IN = "in"
+OUT = "out"
+INOUT = "inout"
+ROLES = (IN, OUT, INOUT)
+
+# dtype name -> numpy carrier and byte size: bf16 travels as uint16 bits and fp8 as uint8 bits, as in
+# the reference's kernel objects (contract/kernel_object.py:43-56); the table is the same mapping.
+NP_DTYPE = {
+    "float64": "float64", "float32": "float32", "float16": "float16",
+    "bfloat16": "uint16", "float8_e5m2": "uint8", "float8_e4m3fn": "uint8",
+    "int64": "int64", "int32": "int32", "int16": "int16", "int8": "int8",
+    "uint64": "uint64", "uint32": "uint32", "uint16": "uint16", "uint8": "uint8",
+    "bool": "int8",
+}
+ITEMSIZE = {
+    "float64": 8, "float32": 4, "float16": 2, "bfloat16": 2, "float8_e5m2": 1, "float8_e4m3fn": 1,
+    "int64": 8, "int32": 4, "int16": 2, "int8": 1,
+    "uint64": 8, "uint32": 4, "uint16": 2, "uint8": 1,
+    "bool": 1,
+}
+# Triton pointer tokens of a signature -> dtype names
+TRITON_DTYPE = {"fp64": "float64", "fp32": "float32", "fp16": "float16", "bf16": "bfloat16", "i64": "int64",
+                "i32": "int32", "i16": "int16", "i8": "int8", "i1": "bool", "fp8e4nv": "float8_e4m3fn",
+                "fp8e5": "float8_e5m2"}
+
+
+def is_read(arg) -> bool:
+    return arg.role in (IN, INOUT)
+
+
+def is_written(arg) -> bool:
+    return arg.role in (OUT, INOUT)
+
+
+@dataclass
+class Arg:
+    """One memory-backed kernel argument (contract/kernel_spec.py:24-38)."""
+    name: str
+    role: str
+    dtype: str
+    shape: tuple
+
+    def __post_init__(self):
+        if self.role not in ROLES:
+            raise ValueError(f"Arg {self.name}: role must be one of {ROLES}, not {self.role!r}")
+        if self.dtype not in ITEMSIZE:
+            raise ValueError(f"Arg {self.name}: unknown dtype {self.dtype!r}")
+        self.shape = tuple(int(s) for s in self.shape)
+
+    @property
+    def numel(self) -> int:
+        return math.prod(self.shape)
+
+    @property
+    def nbytes(self) -> int:
+        return self.numel * ITEMSIZE[self.dtype]
+
+
+@dataclass
+class KernelSpec:
+    """What a kernel file declares (contract/kernel_spec.py:41-139), minus the compiler-only fields
+    (expected IR, scratchpad placement, prefetch plan)."""
+    name: str
+    signature: dict
+    constexprs: dict
+    args: list
+    grid: tuple
+    kernel: Callable | None = None
+    reference: Callable | None = None
+    make_inputs: Callable | None = None
+    rtol: float = 1e-4
+    atol: float = 1e-4
+    parallel_axes: tuple = ()
+    extra: dict = field(default_factory=dict)
+    graph_prefetch: object = None
+
+    def __post_init__(self):
+        self.grid = tuple(int(g) for g in self.grid)
+        if not self.parallel_axes:
+            self.parallel_axes = ("x", "y", "z")[:max(1, len(self.grid))]
+        names = [a.name for a in self.args]
+        if len(set(names)) != len(names):
+            raise ValueError(f"{self.name}: argument names repeat: {names}")
+
+    def inputs(self):
+        return [a for a in self.args if is_read(a)]
+
+    def outputs(self):
+        return [a for a in self.args if is_written(a)]
+
+    def arg(self, name: str) -> Arg:
+        for a in self.args:
+            if a.name == name:
+                return a
+        raise KeyError(f"{self.name} has no argument {name!r}")
+
+    @property
+    def scalar_values(self) -> dict:
+        return dict((self.extra or {}).get("scalar_values", {}))
+
+    def manifest(self) -> dict:
+        """The facts a compiled kernel's manifest states (contract/kernel_object.py:333-359) that a
+        device needs to run it: name, grid, args, scalars, constexprs."""
+        scalars = [{"name": n, "ctype": c, "default": self.scalar_values.get(n)}
+                   for n, c in (self.extra or {}).get("scalar_args", [])]
+        return {"name": self.name, "grid": list(self.grid),
+                "args": [{"name": a.name, "role": a.role, "dtype": a.dtype, "shape": list(a.shape)}
+                         for a in self.args],
+                "scalars": scalars, "constexprs": dict(self.constexprs)}
+
+
+def spec_from_manifest(manifest: dict) -> KernelSpec:
+    """A KernelSpec from a manifest dict (the kernel.json facts, or :meth:`KernelSpec.manifest`)."""
+    args = [Arg(a["name"], a["role"], a["dtype"], tuple(a["shape"])) for a in manifest["args"]]
+    scalars = manifest.get("scalars", [])
+    extra = dict(manifest.get("extra", {}))
+    extra.update({"scalar_args": [(s["name"], s.get("ctype", "int32_t")) for s in scalars],
+                  "scalar_values": {s["name"]: s.get("default") for s in scalars if s.get("default") is not None}})
+    return KernelSpec(name=manifest["name"], signature=manifest.get("signature", {}),
+                      constexprs=dict(manifest.get("constexprs", {})), args=args,
+                      grid=tuple(manifest.get("grid", (1,))), extra=extra)
+
+
+def seeded_inputs(spec: KernelSpec, torch, seed: int = 0) -> dict:
+    """The inputs the reference's generated specs draw (validation/pytorchsim/*/..._spec.py:28-36):
+    one generator seeded once, then ``torch.randn(numel, generator=g).to(dtype)`` for every read
+    argument in argument order.  CPU tensors, flat, as the specs make them."""
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for a in spec.inputs():
+        dt = getattr(torch, a.dtype)
+        out[a.name] = torch.randn(a.numel, generator=g).to(dt)
+    return out

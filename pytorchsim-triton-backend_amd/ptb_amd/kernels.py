@@ -1,0 +1,306 @@
+"""Map a reference kernel (its spec or manifest, plus the Triton source when at hand) to the HIP
+kernel family that executes it, and run it over flat device tensors.
+
+The reference compiles each Inductor-generated Triton kernel to its own ELF; here every kernel of
+the hot path is one of a few hand-written HIP families, chosen from what the spec states:
+
+  attention   ``_prefill_kernel`` with constexprs HQ, G, S, D, CAUSAL, SCALE
+              (attention_prefill_*/00__prefill_kernel/_prefill_kernel_triton.py:4-44)
+  gemm        args arg_A, arg_B, out_ptr0 (+ a leading in_ptr0 residual): the ``mm`` and RESIDENT
+              templates (qwen3_8b_layer_prefill_*/01, 03, 08, 09, 11; gemm_<M>x<K>x<N>_bf16)
+  rmsnorm     x, w, out with a mean/rsqrt reduction over w's length (.../00_..._gwdq6qer)
+  qk_norm_rope x, w[D], cos, sin (fp32), out head-major (.../02, 04)
+  transpose   one bf16 in, one bf16 out, an affine permutation of [A, B, D] -> [B, A, D]
+              (.../05, 07), read from the kernel's index expressions
+  silu_mul    in [T, 2I] -> out [T, I] (.../10); I from the kernel's index expressions
+  softmax     ``softmax`` kernels with scalars xnumel (rows), r0_numel (cols) (vector_softmax_*)
+  reduce      whole-tensor ``sum`` / ``max`` into one fp32 (vector_sum_*, vector_max_*)
+  add_scalar  ``fused_add``: bf16(x + c) (vector_add1_*)
+
+Anything else raises :class:`UnsupportedKernel` -- there is no fallback execution.
+"""
+from __future__ import annotations
+
+import math
+import re
+from dataclasses import dataclass, field
+
+from .contract import KernelSpec
+
+
+class UnsupportedKernel(ValueError):
+    pass
+
+
+@dataclass
+class Plan:
+    family: str
+    params: dict = field(default_factory=dict)
+
+
+# ---------------------------------------------------------------- Triton source helpers
+_DECOMP = re.compile(r"^\s*(x\d+)\s*=\s*(.+?)\s*$", re.M)
+
+
+def _index_terms(expr: str) -> dict:
+    """'x0 + 128*x2 + 1024*x1' -> {'x0': 1, 'x2': 128, 'x1': 1024} (affine, positive strides)."""
+    out = {}
+    for term in expr.replace(" ", "").split("+"):
+        if not term:
+            continue
+        m = re.fullmatch(r"(?:(\d+)\*)?\(?([a-z]\w*)\)?(?:\*(\d+))?", term)
+        if not m:
+            m2 = re.fullmatch(r"\(?(\d+)\)?", term)
+            if m2:
+                out["const"] = out.get("const", 0) + int(m2.group(1))
+                continue
+            raise UnsupportedKernel(f"index term {term!r} is not affine")
+        coef = int(m.group(1) or m.group(3) or 1)
+        out[m.group(2)] = out.get(m.group(2), 0) + coef
+    return out
+
+
+def _decomposition(src: str) -> dict:
+    """x-variable definitions of a pointwise Inductor kernel: name -> (divisor, modulus or None)."""
+    out = {}
+    for name, rhs in _DECOMP.findall(src):
+        r = rhs.replace(" ", "")
+        m = re.fullmatch(r"\(*xindex(?://(\d+))?\)*(?:%(\d+))?\)*", r)
+        if m:
+            out[name] = (int(m.group(1) or 1), int(m.group(2)) if m.group(2) else None)
+    return out
+
+
+def _load_index(src: str, ptr: str) -> str:
+    m = re.search(r"tl\.load\(\s*" + re.escape(ptr) + r"\s*\+\s*\((.*?)\)\s*,", src)
+    if not m:
+        raise UnsupportedKernel(f"no affine load of {ptr} in the kernel source")
+    return m.group(1)
+
+
+def _permutation_from_source(src: str, numel: int):
+    """For a [A, B, D] -> [B, A, D] copy kernel: (A, B, D) from its index expressions."""
+    dec = _decomposition(src)
+    terms = _index_terms(_load_index(src, "in_ptr0"))
+    # output dims from the decomposition: innermost x (divisor 1, modulus D), middle (divisor D,
+    # modulus n1), outer (divisor D*n1)
+    inner = [v for v, (d, mod) in dec.items() if d == 1 and mod]
+    if len(inner) != 1:
+        raise UnsupportedKernel("cannot find the innermost index of the copy kernel")
+    xi = inner[0]
+    d = dec[xi][1]
+    mid = [v for v, (dv, mod) in dec.items() if dv == d and mod]
+    outer = [v for v, (dv, mod) in dec.items() if dv > d and mod is None]
+    if len(mid) != 1 or len(outer) != 1:
+        raise UnsupportedKernel("copy kernel is not a 3-D permutation")
+    xm, xo = mid[0], outer[0]
+    n_mid = dec[xm][1]
+    n_out = numel // (d * n_mid)
+    # input strides: inner must be 1; y[o, m, i] = x[...]; the transpose family needs x = [m][o][i]
+    if terms.get(xi) != 1 or terms.get(xo) != d or terms.get(xm) != d * n_out or terms.get("const"):
+        raise UnsupportedKernel(f"copy kernel's input strides {terms} are not a head transpose")
+    return n_mid, n_out, d   # x is [n_mid, n_out, d], y is [n_out, n_mid, d]
+
+
+def _row_length_from_source(src: str) -> int:
+    """silu_mul: the gate row length I from 'x0 = (xindex % I)'."""
+    for _, (dv, mod) in _decomposition(src).items():
+        if dv == 1 and mod:
+            return mod
+    raise UnsupportedKernel("cannot read the gate width from the silu_mul kernel")
+
+
+def _float_constant(src: str, default: float) -> float:
+    m = re.search(r"tl\.full\(\[1\],\s*([-0-9.e]+),\s*tl\.float32\)", src or "")
+    return float(m.group(1)) if m else default
+
+
+# ---------------------------------------------------------------- resolution
+def _names(spec):
+    return [a.name for a in spec.args]
+
+
+def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
+    """The HIP family and its parameters for one reference kernel."""
+    names = _names(spec)
+    ce = spec.constexprs or {}
+    sv = spec.scalar_values
+    # index facts a manifest may carry instead of the Triton source (see kernel_hints)
+    hints = (spec.extra or {}).get("hints", {})
+    name = spec.name
+    if {"HQ", "G", "S", "D"} <= set(ce):
+        q = spec.args[0]
+        hq, g, s, d = int(ce["HQ"]), int(ce["G"]), int(ce["S"]), int(ce["D"])
+        if "decode" in name:
+            raise UnsupportedKernel(f"{name}: decode attention is not on the HIP path yet")
+        if len(spec.args) != 4:
+            raise UnsupportedKernel(f"{name}: attention takes q, k, v, o")
+        return Plan("attention", dict(batch=q.numel // (hq * s * d), hq=hq, hkv=hq // g, seq=s, head_dim=d,
+                                      causal=bool(ce.get("CAUSAL", True)),
+                                      scale=float(ce.get("SCALE", 1.0 / math.sqrt(d))),
+                                      q=names[0], k=names[1], v=names[2], o=names[3]))
+    if "arg_A" in names and "arg_B" in names:
+        a, b = spec.arg("arg_A"), spec.arg("arg_B")
+        outs = spec.outputs()
+        if len(outs) != 1:
+            raise UnsupportedKernel(f"{name}: a GEMM with {len(outs)} outputs")
+        c = outs[0]
+        m2 = a.numel * c.numel / b.numel
+        m = int(round(math.sqrt(m2)))
+        if m <= 0 or m * m != int(round(m2)):
+            raise UnsupportedKernel(f"{name}: operand sizes {a.numel}, {b.numel}, {c.numel} are not a GEMM")
+        k, n = a.numel // m, c.numel // m
+        resid = [x for x in spec.inputs() if x.name not in ("arg_A", "arg_B")]
+        return Plan("gemm", dict(m=m, k=k, n=n, residual=resid[0].name if resid else None, a="arg_A", b="arg_B",
+                                 c=c.name))
+    ins, outs = spec.inputs(), spec.outputs()
+
+    def sizes(key):  # a size the kernel pins as a runtime scalar or as a constexpr
+        v = sv.get(key, ce.get(key))
+        return int(v) if v is not None else None
+
+    if "softmax" in name and len(ins) == 1 and len(outs) == 1:
+        cols = sizes("r0_numel")
+        if not cols or ins[0].numel % cols:
+            raise UnsupportedKernel(f"{name}: softmax needs its row length r0_numel")
+        return Plan("softmax", dict(rows=ins[0].numel // cols, cols=cols, x=ins[0].name, y=outs[0].name))
+    if "_mm_" in name and len(ins) == 2 and len(outs) == 1 and sizes("r0_numel") and sizes("xnumel"):
+        # the M = 1 template: out[n] = sum_k in0[k] * in1[k * N + n] (gemm_1x<K>x<N>_bf16)
+        k, n = sizes("r0_numel"), sizes("xnumel")
+        a, b = ins
+        if source:
+            terms = _index_terms(_load_index(source, b.name))
+            if terms != {"x0": 1, "r0_1": n}:
+                raise UnsupportedKernel(f"{name}: the M = 1 template reads B as {terms}, not row-major [K, N]")
+        if a.numel == k and b.numel == k * n and outs[0].numel == n:
+            return Plan("gemm", dict(m=1, k=k, n=n, residual=None, a=a.name, b=b.name, c=outs[0].name))
+    if len(ins) == 1 and len(outs) == 1 and outs[0].numel == 1 and outs[0].dtype == "float32":
+        if "slice" in name:
+            raise UnsupportedKernel(f"{name}: the single-element slice kernel has no HIP family")
+        if "_sum_" in name or name.endswith("sum"):
+            return Plan("reduce", dict(op="sum", n=ins[0].numel, x=ins[0].name, y=outs[0].name))
+        if "_max_" in name or name.endswith("max"):
+            return Plan("reduce", dict(op="max", n=ins[0].numel, x=ins[0].name, y=outs[0].name))
+    if "rsqrt" in name and "mean" in name:
+        if len(ins) == 2 and len(outs) == 1:
+            x, w = ins
+            return Plan("rmsnorm", dict(rows=x.numel // w.numel, cols=w.numel, eps=1e-6, x=x.name, w=w.name,
+                                        y=outs[0].name))
+        if len(ins) == 4 and len(outs) == 1:
+            x, w, cs, sn = ins
+            d = w.numel
+            t = cs.numel // d
+            return Plan("qk_norm_rope", dict(tokens=t, heads=x.numel // (t * d), head_dim=d, eps=1e-6, x=x.name,
+                                             w=w.name, cos=cs.name, sin=sn.name, y=outs[0].name))
+    if len(ins) == 1 and len(outs) == 1 and ins[0].dtype == outs[0].dtype == "bfloat16":
+        x, y = ins[0], outs[0]
+        if "silu" in name and x.numel == 2 * y.numel:
+            if "inter" in hints:
+                inter = int(hints["inter"])
+            elif source is not None:
+                inter = _row_length_from_source(source)
+            else:
+                raise UnsupportedKernel(f"{name}: silu_mul needs the kernel source (or an 'inter' hint)")
+            return Plan("silu_mul", dict(rows=y.numel // inter, inter=inter, x=x.name, y=y.name))
+        if "transpose" in name and x.numel == y.numel:
+            if {"d0", "d1", "inner"} <= set(hints):
+                d0, d1, inner = int(hints["d0"]), int(hints["d1"]), int(hints["inner"])
+            elif source is not None:
+                d0, d1, inner = _permutation_from_source(source, x.numel)
+            else:
+                raise UnsupportedKernel(f"{name}: a transpose needs the kernel source (or d0/d1/inner hints)")
+            if d0 * d1 * inner != x.numel:
+                raise UnsupportedKernel(f"{name}: transpose dims {d0}x{d1}x{inner} do not cover {x.numel} elements")
+            return Plan("transpose", dict(d0=d0, d1=d1, inner=inner, x=x.name, y=y.name))
+        if "fused_add" in name and x.numel == y.numel:
+            return Plan("add_scalar", dict(s=_float_constant(source, 1.0), n=x.numel, x=x.name, y=y.name))
+    raise UnsupportedKernel(f"{name}: no HIP kernel family matches this kernel")
+
+
+def kernel_hints(plan: Plan) -> dict:
+    """The index facts of a plan that :func:`resolve` otherwise reads from the Triton source, for a
+    manifest to carry under ``extra["hints"]`` when the source does not travel with it."""
+    if plan.family == "transpose":
+        return {k: plan.params[k] for k in ("d0", "d1", "inner")}
+    if plan.family == "silu_mul":
+        return {"inter": plan.params["inter"]}
+    return {}
+
+
+# ---------------------------------------------------------------- execution
+def run(plan: Plan, tensors: dict) -> None:
+    """Launch `plan` on the current stream over flat device tensors keyed by argument name."""
+    from . import ops
+
+    p, t = plan.params, tensors
+    f = plan.family
+    if f == "gemm":
+        m, k, n = p["m"], p["k"], p["n"]
+        r = t[p["residual"]].view(m, n) if p["residual"] else None
+        ops.gemm(t[p["a"]].view(m, k), t[p["b"]].view(k, n), r, out=t[p["c"]].view(m, n))
+    elif f == "attention":
+        bh, s, d = p["batch"] * p["hq"], p["seq"], p["head_dim"]
+        q, k, v, o = t[p["q"]], t[p["k"]], t[p["v"]], t[p["o"]]
+        kv = p["batch"] * p["hkv"]
+        ops.flash_attention(q.view(bh, s, d), k.view(kv, s, d), v.view(kv, s, d), p["hq"], p["hkv"], p["causal"],
+                            p["scale"], out=o.view(bh, s, d))
+    elif f == "rmsnorm":
+        ops.rmsnorm(t[p["x"]].view(p["rows"], p["cols"]), t[p["w"]], p["eps"], out=t[p["y"]].view(p["rows"], p["cols"]))
+    elif f == "qk_norm_rope":
+        tk, h, d = p["tokens"], p["heads"], p["head_dim"]
+        ops.qk_norm_rope(t[p["x"]].view(tk, h, d), t[p["w"]], t[p["cos"]].view(tk, d), t[p["sin"]].view(tk, d),
+                         p["eps"], out=t[p["y"]].view(h, tk, d))
+    elif f == "transpose":
+        ops.transpose_heads(t[p["x"]].view(p["d0"], p["d1"], p["inner"]), out=t[p["y"]].view(p["d1"], p["d0"], p["inner"]))
+    elif f == "silu_mul":
+        ops.silu_mul(t[p["x"]].view(p["rows"], 2 * p["inter"]), out=t[p["y"]].view(p["rows"], p["inter"]))
+    elif f == "softmax":
+        ops.softmax_rows(t[p["x"]].view(p["rows"], p["cols"]), out=t[p["y"]].view(p["rows"], p["cols"]))
+    elif f == "reduce":
+        ops.reduce(t[p["x"]], p["op"], out=t[p["y"]])
+    elif f == "add_scalar":
+        ops.add_scalar(t[p["x"]], p["s"], out=t[p["y"]])
+    else:
+        raise UnsupportedKernel(f"unknown family {f}")
+
+
+def launch(spec: KernelSpec, tensors: dict, source: str | None = None) -> Plan:
+    """Resolve and run one kernel; returns the plan it ran."""
+    plan = resolve(spec, source)
+    run(plan, tensors)
+    return plan
+
+
+def work_of(plan: Plan) -> tuple:
+    """(flops, algorithmic HBM bytes) of one launch -- each operand read once, each output written
+    once; flop conventions as the reference's reports use them (2MNK per GEMM, 4*H*D*S(S+1)/2 for
+    causal attention, validation/attention/emit_report.py:295; vector ops by element,
+    validation/vector/emit_report.py:20-39)."""
+    p, f = plan.params, plan.family
+    if f == "gemm":
+        m, k, n = p["m"], p["k"], p["n"]
+        return 2.0 * m * n * k, 2.0 * (m * k + k * n + m * n * (2 if p["residual"] else 1))
+    if f == "attention":
+        h, d, s = p["batch"] * p["hq"], p["head_dim"], p["seq"]
+        pairs = s * (s + 1) / 2 if p["causal"] else s * s
+        return 4.0 * h * d * pairs, 2.0 * d * s * (2 * h + 2 * p["batch"] * p["hkv"])
+    if f == "rmsnorm":
+        r, c = p["rows"], p["cols"]
+        return 4.0 * r * c, 2.0 * (2 * r * c + c)
+    if f == "qk_norm_rope":
+        n = p["tokens"] * p["heads"] * p["head_dim"]
+        return 10.0 * n, 4.0 * n + 8.0 * p["tokens"] * p["head_dim"]
+    if f == "transpose":
+        n = p["d0"] * p["d1"] * p["inner"]
+        return 0.0, 4.0 * n
+    if f == "silu_mul":
+        n = p["rows"] * p["inter"]
+        return 5.0 * n, 6.0 * n
+    if f == "softmax":
+        n = p["rows"] * p["cols"]
+        return 5.0 * n, 4.0 * n
+    if f == "reduce":
+        return float(p["n"]), 2.0 * p["n"] + 4.0
+    if f == "add_scalar":
+        return float(p["n"]), 4.0 * p["n"]
+    raise UnsupportedKernel(f"unknown family {f}")

@@ -1,0 +1,142 @@
+"""Validation-suite entry points on the GPU: time the bundle's workloads with the HIP kernels.
+
+Mirrors the reference's runners, ``validation/{vector,gemm,attention,layer,qwen3_8b}/
+simulate_shapes.py`` (shared runner validation/gemm/simulate_shapes.py:265-319, 426-502): the same
+suite KEYS name a workload, every distinct kernel of a workload runs once per launch count, and
+``results.json`` -- rewritten after every workload -- holds per workload the keys, ``kernel`` (the
+workload name), ``rc``, ``failed_step``, ``us`` and per kernel its launches.  Where the reference
+reads TOGSim cycles, this runner reads hipEvent time of back-to-back launches on inputs drawn by
+the specs' seeded ``make_inputs`` convention, and adds TFLOP/s, GB/s and the MI355X roofline
+fraction per kernel.  ``--shard K/N`` and ``--merge`` split and join runs as the reference's do.
+
+    python -m ptb_amd.validation qwen3_8b --bundle <reference>/validation/pytorchsim --out results.json
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+from . import bundle, contract, kernels
+
+MI355X = {"name": "MI355X (gfx950)", "peak_bf16_tflops": 2500.0, "peak_fp8_tflops": 5000.0, "hbm_gbs": 8000.0}
+SUITES = tuple(bundle.SUITE_KEYS)
+
+
+def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0) -> dict:
+    """Run one bundle kernel on the GPU and time it; returns its record."""
+    import torch
+
+    plan = kernels.resolve(bk.spec, bk.source)
+    host = contract.seeded_inputs(bk.spec, torch, seed)
+    tensors = {}
+    for a in bk.spec.args:
+        if a.name in host:
+            tensors[a.name] = host[a.name].to("cuda")
+        else:
+            tensors[a.name] = torch.empty(a.numel, dtype=getattr(torch, a.dtype), device="cuda")
+    for _ in range(warmup):
+        kernels.run(plan, tensors)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        kernels.run(plan, tensors)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    flops, nbytes = kernels.work_of(plan)
+    tflops = flops / (us * 1e-6) / 1e12
+    gbs = nbytes / (us * 1e-6) / 1e9
+    roof_us = max(flops / (MI355X["peak_bf16_tflops"] * 1e12), nbytes / (MI355X["hbm_gbs"] * 1e9)) * 1e6
+    return {"dir": bk.dir, "name": bk.spec.name, "launches": bk.launches, "family": plan.family, "us": us,
+            "tflops": tflops, "gbs": gbs, "roofline_us": roof_us, "roofline_frac": roof_us / us if us else None}
+
+
+def run_workload(w, reps: int = 20, warmup: int = 3) -> dict:
+    got = dict(w.keys, kernel=w.name, rc=0, failed_step=None, kernels=[])
+    t0 = time.monotonic()
+    step = "resolve"
+    try:
+        for bk in w.kernels:
+            step = bk.dir
+            got["kernels"].append(time_kernel(bk, reps, warmup))
+        got["us"] = sum(k["us"] * k["launches"] for k in got["kernels"])
+        got["roofline_us"] = sum(k["roofline_us"] * k["launches"] for k in got["kernels"])
+    except Exception as e:  # noqa: BLE001 - a workload's failure is recorded, never lost
+        got.update(rc=f"{type(e).__name__}: {e}", failed_step=step)
+    got["wall_s"] = round(time.monotonic() - t0, 1)
+    return got
+
+
+def write_results(path, suite, done, total, part=None) -> None:
+    keys = bundle.SUITE_KEYS[suite]
+    shapes = sorted(done, key=lambda r: tuple(str(r.get(k)) for k in keys))
+    res = {"machine": MI355X, "suite": suite, "expected": total, "shapes": shapes}
+    if part:
+        res["shard"] = part
+    tmp = path + ".tmp"
+    with open(tmp, "w") as fh:
+        json.dump(res, fh, indent=1)
+    os.replace(tmp, path)
+
+
+def merge(paths, out) -> int:
+    parts = [json.load(open(p)) for p in paths]
+    suite = parts[0]["suite"]
+    if any(p["suite"] != suite or p["machine"] != parts[0]["machine"] for p in parts):
+        raise ValueError("shards of different suites or machines")
+    shapes = [s for p in parts for s in p["shapes"]]
+    write_results(out, suite, shapes, parts[0]["expected"])
+    return 0 if len(shapes) == parts[0]["expected"] else 1
+
+
+def parse_where(items):
+    out = {}
+    for it in items or ():
+        k, _, v = it.partition("=")
+        out[k] = v
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="time a validation suite's bundle workloads on the GPU")
+    ap.add_argument("suite", choices=SUITES)
+    ap.add_argument("--bundle", required=False, help="the reference's validation/pytorchsim directory")
+    ap.add_argument("--out", default="results.json")
+    ap.add_argument("--where", action="append", help="key=value filter on the workload's keys (repeatable)")
+    ap.add_argument("--only", action="append", help="workload name (repeatable)")
+    ap.add_argument("--shard", help="K/N: run the K-th of N interleaved parts")
+    ap.add_argument("--merge", nargs="+", help="join shard results.json files into --out")
+    ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    args = ap.parse_args(argv)
+    if args.merge:
+        return merge(args.merge, args.out)
+    if not args.bundle:
+        ap.error("--bundle is required unless --merge")
+    from . import _lib
+
+    _lib.load()
+    ws = bundle.load_bundle(args.bundle, args.suite, parse_where(args.where) or None)
+    if args.only:
+        ws = [w for w in ws if w.name in set(args.only)]
+    part = None
+    if args.shard:
+        k, n = (int(x) for x in args.shard.split("/"))
+        ws = ws[k - 1::n]
+        part = args.shard
+    done = []
+    write_results(args.out, args.suite, done, len(ws), part)
+    for w in ws:
+        r = run_workload(w, args.reps, args.warmup)
+        done.append(r)
+        write_results(args.out, args.suite, done, len(ws), part)
+        print(f"{w.name}: rc={r['rc']} us={r.get('us', float('nan')):.1f}", flush=True)
+    return 0 if all(r["rc"] == 0 for r in done) else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,181 @@
+"""The reference's boundary on the GPU: bundle kernels (as manifests) run through
+ptb_amd.launcher / the set_launcher-compatible hook / HipDevice over .raw files, on the inputs the
+specs' make_inputs draw, checked against the oracle (bf16 tolerance 2e-2; exact families
+bit-equal; full-size GEMMs and attention on sampled rows / heads)."""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close, bits_equal
+from ptb_amd import contract, device, kernels, launcher, verify
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+MANIFESTS = json.loads((GOLDEN / "bundle_manifests.json").read_text())
+CASES = [(w, i) for w in sorted(MANIFESTS) for i in range(len(MANIFESTS[w]["kernels"]))]
+
+
+def sample(n, k=8, seed=0):
+    if n <= k:
+        return torch.arange(n)
+    g = torch.Generator().manual_seed(seed)
+    return torch.unique(torch.cat([torch.tensor([0, n - 1]), torch.randint(0, n, (k,), generator=g)]))
+
+
+def check_against_oracle(plan, host, got):
+    """got: name -> CPU tensor (flat) from the GPU; host: the CPU inputs."""
+    p, f = plan.params, plan.family
+    if f == "gemm":
+        m, k, n = p["m"], p["k"], p["n"]
+        rows = sample(m, 16)
+        a = host[p["a"]].view(m, k)[rows]
+        r = host[p["residual"]].view(m, n)[rows] if p["residual"] else None
+        want = oracle.gemm(a, host[p["b"]].view(k, n), r)
+        scale = float(want.float().abs().mean()) + 1e-6
+        assert_close(got[p["c"]].view(m, n)[rows], want, 2e-2, 2e-2 * scale, "gemm")
+    elif f == "attention":
+        bh, s, d, hkv = p["batch"] * p["hq"], p["seq"], p["head_dim"], p["batch"] * p["hkv"]
+        q = host[p["q"]].view(bh, s, d)
+        heads = sample(bh, 2)
+        k = host[p["k"]].view(hkv, s, d)
+        v = host[p["v"]].view(hkv, s, d)
+        g = p["hq"] // p["hkv"]
+        kv_of = [(h // p["hq"]) * p["hkv"] + (h % p["hq"]) // g for h in heads.tolist()]
+        want = oracle.flash_attention(q[heads], k[kv_of], v[kv_of], len(kv_of), len(kv_of), p["causal"], p["scale"])
+        assert_close(got[p["o"]].view(bh, s, d)[heads], want, 2e-2, 2e-2, "attention")
+    elif f == "rmsnorm":
+        want = oracle.rmsnorm(host[p["x"]].view(p["rows"], p["cols"]), host[p["w"]], p["eps"])
+        assert_close(got[p["y"]].view(p["rows"], p["cols"]), want, 2e-2, 2e-2, "rmsnorm")
+    elif f == "qk_norm_rope":
+        t, h, d = p["tokens"], p["heads"], p["head_dim"]
+        want = oracle.qk_norm_rope(host[p["x"]].view(t, h, d), host[p["w"]], host[p["cos"]].view(t, d),
+                                   host[p["sin"]].view(t, d), p["eps"])
+        assert_close(got[p["y"]].view(h, t, d), want, 2e-2, 2e-2, "qk_norm_rope")
+    elif f == "transpose":
+        want = oracle.transpose_heads(host[p["x"]].view(p["d0"], p["d1"], p["inner"]))
+        assert bits_equal(got[p["y"]].view(p["d1"], p["d0"], p["inner"]), want)
+    elif f == "silu_mul":
+        want = oracle.silu_mul(host[p["x"]].view(p["rows"], 2 * p["inter"]))
+        assert_close(got[p["y"]].view(p["rows"], p["inter"]), want, 2e-2, 2e-2, "silu_mul")
+    elif f == "softmax":
+        want = oracle.softmax_rows(host[p["x"]].view(p["rows"], p["cols"]))
+        assert_close(got[p["y"]].view(p["rows"], p["cols"]), want, 2e-2, 2e-2, "softmax")
+    elif f == "reduce":
+        x = host[p["x"]]
+        if p["op"] == "max":
+            assert torch.equal(got[p["y"]], oracle.reduce_max(x))
+        else:
+            bound = 1e-6 * float(x.float().abs().sum()) + 1e-6
+            assert abs(float(got[p["y"]]) - float(oracle.reduce_sum(x))) <= bound
+    elif f == "add_scalar":
+        assert bits_equal(got[p["y"]], oracle.add_scalar(host[p["x"]], p["s"]))
+    else:
+        raise AssertionError(f"no oracle for {f}")
+
+
+@pytest.mark.parametrize("workload,index", CASES)
+def test_bundle_kernel_through_launcher(workload, index):
+    man = MANIFESTS[workload]["kernels"][index]
+    spec = contract.spec_from_manifest(man)
+    host = contract.seeded_inputs(spec, torch, seed=0)
+    dev = {a.name: (host[a.name].cuda() if a.name in host
+                    else torch.empty(a.numel, dtype=getattr(torch, a.dtype), device="cuda")) for a in spec.args}
+    plan = launcher.launch(spec, dev, grid=tuple(man["grid"]))
+    torch.cuda.synchronize()
+    got = {a.name: dev[a.name].cpu() for a in spec.outputs()}
+    check_against_oracle(plan, host, got)
+
+
+def test_hip_launcher_hook_takes_kernel_json():
+    man = MANIFESTS["qwen3_8b_layer_prefill_512x512_bf16"]["kernels"][0]   # rmsnorm
+    spec = contract.spec_from_manifest(man)
+    host = contract.seeded_inputs(spec, torch, seed=3)
+    args = [host[a.name].cuda() if a.name in host else torch.empty(a.numel, dtype=torch.bfloat16, device="cuda")
+            for a in spec.args]
+    launcher.set_launcher(launcher.hip_launcher)
+    try:
+        fn = launcher.registered_launcher()
+        fn(b"", json.dumps(man), tuple(man["grid"]), args + [2048, 4096])
+    finally:
+        launcher.set_launcher(None)
+    torch.cuda.synchronize()
+    p = kernels.resolve(spec).params
+    want = oracle.rmsnorm(host["in_ptr0"].view(p["rows"], p["cols"]), host["in_ptr1"], 1e-6)
+    assert_close(args[2].cpu().view(p["rows"], p["cols"]), want, 2e-2, 2e-2, "hook rmsnorm")
+
+
+def test_hip_device_over_raw_files(tmp_path):
+    """HipDevice reads .raw inputs, poisons outputs, runs, writes .raw outputs; the result equals
+    the launcher's bit for bit and passes verify against the oracle."""
+    man = MANIFESTS["qwen3_8b_layer_prefill_512x512_bf16"]["kernels"][5]   # k/v projection GEMM
+    spec = contract.spec_from_manifest(man)
+    host = contract.seeded_inputs(spec, torch, seed=0)
+    paths = {a.name: str(tmp_path / f"{a.name}.raw") for a in spec.args}
+    for a in spec.inputs():
+        verify.write_raw(paths[a.name], a, host[a.name].view(torch.int16).numpy().view(np.uint16))
+    device.get("hip").launch(device.Launch(str(tmp_path), man, raw_paths=paths, grid=tuple(man["grid"])))
+    out = spec.outputs()[0]
+    raw = verify.read_raw(paths[out.name], out)
+    got = torch.from_numpy(raw.view(np.int16).copy()).view(torch.bfloat16)
+    dev = {a.name: (host[a.name].cuda() if a.name in host else torch.empty(a.numel, dtype=torch.bfloat16,
+                                                                             device="cuda")) for a in spec.args}
+    plan = launcher.launch(spec, dev)
+    torch.cuda.synchronize()
+    assert bits_equal(got, dev[out.name].cpu())
+    check_against_oracle(plan, host, {out.name: got})
+
+
+def test_qwen3_layer_from_bundle_manifests_matches_composed_oracle():
+    """The 14 launches of qwen3_8b_layer_prefill_512x512_bf16, chained the way the layer's data flows
+    (K00 -> K01/K03 -> K02/K04/K05 -> K06 -> K07 -> K08 -> K00 -> K09 -> K10 -> K11), against the
+    oracle's Qwen3 layer on the same weights."""
+    w = MANIFESTS["qwen3_8b_layer_prefill_512x512_bf16"]
+    specs = {m["dir"][:2]: contract.spec_from_manifest(m) for m in w["kernels"]}
+    t, hidden, hq, hkv, d, inter = 512, 4096, 32, 8, 128, 12288
+    g = torch.Generator().manual_seed(5)
+
+    def rnd(*shape, std=0.02, mean=0.0):
+        return (torch.randn(*shape, generator=g) * std + mean).to(torch.bfloat16)
+
+    x = rnd(t, hidden, std=1.0)
+    wts = {"w_in": rnd(hidden, mean=1.0), "wq": rnd(hidden, hq * d), "wk": rnd(hidden, hkv * d),
+           "wv": rnd(hidden, hkv * d), "w_qn": rnd(d, mean=1.0), "w_kn": rnd(d, mean=1.0), "wo": rnd(hq * d, hidden),
+           "w_post": rnd(hidden, mean=1.0), "wgu": rnd(hidden, 2 * inter), "wd": rnd(inter, hidden)}
+    cos, sin = oracle.rope_tables(t, d, 1.0e6)
+    cu = {k: v.cuda().reshape(-1) for k, v in wts.items()}
+
+    def run(key, **named):
+        spec = specs[key]
+        tens = {}
+        for a in spec.args:
+            tens[a.name] = named[a.name] if a.name in named else torch.empty(
+                a.numel, dtype=getattr(torch, a.dtype), device="cuda")
+        launcher.launch(spec, tens)
+        return tens[spec.outputs()[0].name]
+
+    xc = x.cuda().reshape(-1)
+    xn = run("00", in_ptr0=xc, in_ptr1=cu["w_in"])
+    q = run("01", arg_A=xn, arg_B=cu["wq"])
+    k = run("03", arg_A=xn, arg_B=cu["wk"])
+    v = run("03", arg_A=xn, arg_B=cu["wv"])
+    qh = run("02", in_ptr0=q, in_ptr1=cu["w_qn"], in_ptr2=cos.cuda().reshape(-1), in_ptr3=sin.cuda().reshape(-1))
+    kh = run("04", in_ptr0=k, in_ptr1=cu["w_kn"], in_ptr2=cos.cuda().reshape(-1), in_ptr3=sin.cuda().reshape(-1))
+    vh = run("05", in_ptr0=v)
+    oh = run("06", q_ptr=qh, k_ptr=kh, v_ptr=vh, o_ptr=torch.empty_like(qh))
+    o = run("07", in_ptr0=oh)
+    h = run("08", in_ptr0=xc, arg_A=o, arg_B=cu["wo"])
+    hn = run("00", in_ptr0=h, in_ptr1=cu["w_post"])
+    gu = run("09", arg_A=hn, arg_B=cu["wgu"])
+    a = run("10", in_ptr0=gu)
+    y = run("11", in_ptr0=h, arg_A=a, arg_B=cu["wd"])
+    torch.cuda.synchronize()
+    want = oracle.qwen3_layer(x, wts, cos, sin, hq, hkv, d, 1e-6, bq=512)
+    rms = float(want.float().pow(2).mean().sqrt())
+    assert_close(y.cpu().view(t, hidden), want, 2e-2, 2e-2 * max(1.0, rms), "qwen3 layer from manifests")
+    assert math.isfinite(rms)

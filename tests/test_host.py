@@ -1,0 +1,156 @@
+"""CPU tests of the host-side boundary: spec/manifest round trips, the seeded-input convention,
+kernel-family resolution of the bundle's kernels, verify semantics, the launcher registry and the
+device's error paths.  No GPU is touched."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from ptb_amd import contract, device, kernels, launcher, verify
+from ptb_amd.contract import Arg, KernelSpec
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+MANIFESTS = json.loads((GOLDEN / "bundle_manifests.json").read_text())
+
+
+def spec_of(workload, i):
+    return contract.spec_from_manifest(MANIFESTS[workload]["kernels"][i])
+
+
+def test_arg_and_spec_basics():
+    a = Arg("x", "in", "bfloat16", (4, 8))
+    assert a.numel == 32 and a.nbytes == 64
+    with pytest.raises(ValueError):
+        Arg("x", "sideways", "bfloat16", (1,))
+    with pytest.raises(ValueError):
+        Arg("x", "in", "bfloat17", (1,))
+    s = KernelSpec(name="k", signature={}, constexprs={}, grid=(2,),
+                   args=[Arg("x", "in", "bfloat16", (8,)), Arg("y", "inout", "float32", (8,)),
+                         Arg("z", "out", "float32", (8,))])
+    assert [a.name for a in s.inputs()] == ["x", "y"]
+    assert [a.name for a in s.outputs()] == ["y", "z"]
+    assert s.parallel_axes == ("x",)
+    with pytest.raises(ValueError):
+        KernelSpec(name="k", signature={}, constexprs={}, grid=(1,),
+                   args=[Arg("x", "in", "bfloat16", (8,)), Arg("x", "out", "bfloat16", (8,))])
+
+
+def test_manifest_round_trip_keeps_scalars_and_hints():
+    man = MANIFESTS["qwen3_8b_layer_prefill_2048x2048_bf16"]["kernels"][0]
+    spec = contract.spec_from_manifest(man)
+    again = spec.manifest()
+    assert again["name"] == man["name"] and again["args"] == man["args"] and again["grid"] == man["grid"]
+    assert spec.scalar_values == {"xnumel": 2048, "r0_numel": 4096}
+
+
+def test_seeded_inputs_follow_the_spec_convention():
+    """One generator, randn per read argument in order, cast (validation/pytorchsim/*/_spec.py:28-36)."""
+    spec = spec_of("attention_prefill_24x8x1024_bf16", 0)
+    got = contract.seeded_inputs(spec, torch, seed=0)
+    g = torch.Generator().manual_seed(0)
+    for a in spec.inputs():
+        want = torch.randn(a.numel, generator=g).to(torch.bfloat16)
+        assert torch.equal(got[a.name], want), a.name
+    assert list(got) == [a.name for a in spec.inputs()]   # o_ptr is inout: drawn too
+
+
+@pytest.mark.parametrize("workload", sorted(MANIFESTS))
+def test_every_fixture_kernel_resolves_to_its_recorded_family(workload):
+    for man in MANIFESTS[workload]["kernels"]:
+        plan = kernels.resolve(contract.spec_from_manifest(man))
+        assert plan.family == man["family"], man["name"]
+        flops, nbytes = kernels.work_of(plan)
+        assert nbytes > 0
+
+
+def test_qwen3_layer_plans_match_the_model_shapes():
+    fams = {m["dir"][:2]: kernels.resolve(contract.spec_from_manifest(m))
+            for m in MANIFESTS["qwen3_8b_layer_prefill_2048x2048_bf16"]["kernels"]}
+    assert fams["00"].params == dict(rows=2048, cols=4096, eps=1e-6, x="in_ptr0", w="in_ptr1", y="out_ptr1")
+    assert (fams["01"].params["m"], fams["01"].params["k"], fams["01"].params["n"]) == (2048, 4096, 4096)
+    assert (fams["09"].params["n"], fams["11"].params["k"]) == (24576, 12288)
+    assert fams["08"].params["residual"] == "in_ptr0" and fams["11"].params["residual"] == "in_ptr0"
+    assert fams["02"].params["heads"] == 32 and fams["04"].params["heads"] == 8
+    assert (fams["05"].params["d0"], fams["05"].params["d1"]) == (2048, 8)      # [T,8,D] -> [8,T,D]
+    assert (fams["07"].params["d0"], fams["07"].params["d1"]) == (32, 2048)     # [32,T,D] -> [T,32,D]
+    assert fams["06"].params["hkv"] == 8 and fams["06"].params["causal"]
+    assert fams["10"].params["inter"] == 12288
+    order = MANIFESTS["qwen3_8b_layer_prefill_2048x2048_bf16"]["order"]
+    assert [d[:2] for d in order] == ["00", "01", "02", "03", "04", "03", "05", "06", "07", "08", "00", "09",
+                                      "10", "11"]
+
+
+def test_index_expression_parser():
+    src = ("    x0 = (xindex % 128)\n    x1 = ((xindex // 128) % 2048)\n    x2 = xindex // 262144\n"
+           "    x3 = xindex\n    tmp0 = tl.load(in_ptr0 + (x0 + 128*x2 + 1024*x1), None)\n")
+    assert kernels._permutation_from_source(src, 2048 * 8 * 128) == (2048, 8, 128)
+    bad = src.replace("1024*x1", "1000*x1")
+    with pytest.raises(kernels.UnsupportedKernel):
+        kernels._permutation_from_source(bad, 2048 * 8 * 128)
+    assert kernels._row_length_from_source("    x0 = (xindex % 12288)\n") == 12288
+
+
+def test_unsupported_kernels_fail_loudly():
+    s = KernelSpec(name="mystery", signature={}, constexprs={}, grid=(1,),
+                   args=[Arg("a", "in", "int32", (8,)), Arg("b", "out", "int32", (8,))])
+    with pytest.raises(kernels.UnsupportedKernel):
+        kernels.resolve(s)
+    dec = KernelSpec(name="_decode_kernel", signature={}, grid=(8,),
+                     constexprs={"HQ": 32, "G": 4, "S": 128, "D": 128},
+                     args=[Arg(n, "in", "bfloat16", (8,)) for n in ("q", "k", "v")] + [Arg("o", "out", "bfloat16", (8,))])
+    with pytest.raises(kernels.UnsupportedKernel):
+        kernels.resolve(dec)
+
+
+def test_verify_report_matches_reference_semantics():
+    want = np.array([1.0, 2.0, 3.0, np.nan])
+    ok, lines = verify.compare_arrays("o", want.copy(), want, 1e-4, 1e-4)
+    assert ok and "PASS" in lines[0]
+    got = want.copy()
+    got[1] = 2.5
+    ok, lines = verify.compare_arrays("o", got, want, 1e-4, 1e-4)
+    assert not ok
+    assert "max_abs_err = 0.5" in lines[1] and "worst at flat index 1" in lines[2]
+    assert lines[3].strip().startswith("1/4")
+
+
+def test_verify_compare_decodes_bf16_bits(tmp_path):
+    spec = KernelSpec(name="k", signature={}, constexprs={}, grid=(1,),
+                      args=[Arg("x", "in", "bfloat16", (4,)), Arg("y", "out", "bfloat16", (4,))])
+    y = torch.tensor([1.0, -2.0, 0.5, 3.0]).to(torch.bfloat16)
+    path = tmp_path / "y.raw"
+    verify.write_raw(path, spec.arg("y"), y.view(torch.int16).numpy().view(np.uint16))
+    back = verify.read_raw(path, spec.arg("y"))
+    assert back.dtype == np.uint16
+    ok, _ = verify.compare(spec, {"y": back}, {"y": y}, torch)
+    assert ok
+    with pytest.raises(ValueError):
+        verify.read_raw(path, Arg("y", "out", "bfloat16", (8,)))
+
+
+def test_launcher_registry_and_grid_check():
+    launcher.set_launcher(None)
+    with pytest.raises(RuntimeError):
+        launcher.registered_launcher()
+    launcher.set_launcher(launcher.hip_launcher)
+    assert launcher.registered_launcher() is launcher.hip_launcher
+    launcher.set_launcher(None)
+    spec = spec_of("vector_add1_1024x1024_bf16", 0)
+    with pytest.raises(launcher.GridMismatch):
+        launcher.launch(spec, {}, grid=(7, 1, 1))
+    with pytest.raises(ValueError):   # CPU tensors are refused before any launch
+        launcher.launch(spec, {"in_ptr0": torch.zeros(1048576, dtype=torch.bfloat16),
+                               "out_ptr0": torch.zeros(1048576, dtype=torch.bfloat16)})
+
+
+def test_device_registry_and_missing_inputs(tmp_path):
+    dev = device.get("hip")
+    assert dev.name == "hip"
+    with pytest.raises(device.DeviceError):
+        device.get("spike")
+    man = MANIFESTS["vector_add1_1024x1024_bf16"]["kernels"][0]
+    req = device.Launch(str(tmp_path), man, raw_paths={})
+    with pytest.raises(device.DeviceError):
+        dev.launch(req)
