@@ -6,5 +6,7 @@ launcher hook (:mod:`ptb_amd.launcher`), verify semantics (:mod:`ptb_amd.verify`
 layer (:mod:`ptb_amd.qwen3`) and the validation-suite entry points (:mod:`ptb_amd.validation`).
 """
 from . import _lib  # noqa: F401
+from ._lib import (AlignmentError, GridError, HipError, LibraryMissing, PtbError,  # noqa: F401
+                   ShapeError, UnsupportedError)
 
 __version__ = "0.1.0"
