@@ -33,11 +33,21 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+SETTLE_S = 0.3   # untimed run-in before the warmup steps (set from --settle)
+
+
 def timed(fn, steps: int, warmup: int):
-    """Run fn() warmup times, then time `steps` launches with HIP events on torch's current stream
-    (the stream every ptb_amd op launches on).  Returns (ms per step, wall ms per step)."""
+    """Run fn() back to back for SETTLE_S seconds (the GPU raises its clock over the first ~50 ms of
+    sustained load; the timed steps should see the sustained clock, not the ramp), then warmup
+    times, then time `steps` launches with HIP events on torch's current stream (the stream every
+    ptb_amd op launches on).  Returns (ms per step, wall ms per step)."""
     import torch
 
+    t_end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -257,7 +267,10 @@ def main(argv=None):
     ap.add_argument("--only", default="", help="comma-separated subset of " + ",".join(BENCHES))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-driver", help="run one kernel 5x plus a 256 MiB copy (for rocprofv3 --pmc) and exit")
+    ap.add_argument("--settle", type=float, default=SETTLE_S,
+                    help="seconds of untimed back-to-back launches before the warmup steps")
     args = ap.parse_args(argv)
+    globals()["SETTLE_S"] = max(0.0, args.settle)
     if args.pmc_driver:
         pmc_driver(args.pmc_driver)
         return 0
@@ -304,9 +317,12 @@ def main(argv=None):
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded randn, BASELINE.json shapes)",
-        "config": {"workload": "BASELINE config 2: bf16 GEMM C[4096,12288] = A[4096,4096] @ B[4096,12288], "
-                               "fp32 accumulation, bf16 C", "M": 4096, "K": 4096, "N": 12288},
-        "roofline": dict(head["roofline"], traffic=profiled_traffic("gemm_bf16_4096x4096x12288")),
+        "config": ({"workload": "BASELINE config 2: bf16 GEMM C[4096,12288] = A[4096,4096] @ B[4096,12288], "
+                                "fp32 accumulation, bf16 C", "M": 4096, "K": 4096, "N": 12288,
+                    "settle_s": SETTLE_S}
+                   if "gemm_bf16" in results else {"workload": head["config"], "settle_s": SETTLE_S}),
+        "roofline": (dict(head["roofline"], traffic=profiled_traffic("gemm_bf16_4096x4096x12288"))
+                     if "gemm_bf16" in results else dict(head["roofline"], traffic=None)),
         "cpu_baseline": cpu,
         "kernels": kernels,
     }

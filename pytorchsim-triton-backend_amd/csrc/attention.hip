@@ -3,17 +3,36 @@
 // Layout (the reference's): q, o [B*HQ, S, 128]; k, v [B*HKV, S, 128]; query head h of batch b reads
 // kv head b*HKV + h / (HQ/HKV).
 //
-// Workgroup = 4 waves = 128 query rows of one head (32 per wave); K/V blocks of 64 keys are staged
-// in LDS, double-buffered (K as [key][d], V transposed to [d][key]).  Each wave computes the
-// transposed score tile S^T = K Q^T (keys on the MFMA's M side, its 32 queries on the lanes), so a
-// query's scores sit in one lane pair (lane, lane^32) and its softmax statistics need one cross-lane
-// exchange per block.  The exponentials, rounded to bf16, are already laid out as the B operand of
-// O^T += V^T P^T, so P never goes through LDS.  Online softmax follows the reference step by step:
-// s = (q.k) * scale, masked entries -1e30, m_new = max(m, rowmax), alpha = exp(m - m_new),
-// p = exp(s - m_new), l = l * alpha + rowsum(p), acc = acc * alpha + bf16(p) V, out = acc / l.
+// Workgroup = 8 waves = 256 query rows of one head (32 per wave); one workgroup per CU, two waves
+// per SIMD.  Blocks of 64 keys move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging)
+// into two 32 KB stages, one block ahead, shared by all 256 rows.  Both tiles keep their global
+// [key][d] layout with the 16-byte chunks of each 256-byte row XOR-swizzled, so every LDS read is
+// bank-conflict free:
+//   K: chunk c of key row r sits in slot c ^ (r & 15); the 16 lanes of a 128-bit read take 16 keys.
+//   V: chunk c of key row r sits in slot c ^ (4 * (r & 3)); V^T fragments come from
+//      ds_read_b64_tr_b16 (within each 16-lane group lane 4j+q supplies key k+j, d n+4q..n+4q+3 and
+//      lane i receives keys k..k+3 of d n+i), whose half-wave reads cover 4 keys x 4 chunks.
+// Each wave computes the transposed score tile S^T = K Q^T (keys on the MFMA's M side, its 32
+// queries on the lanes), so a query's 64 scores sit in one lane pair (lane, lane^32); the softmax
+// statistics need one cross-lane exchange per block.  The K fragments of a block are read ahead of
+// its MFMAs (four in flight), so LDS latency does not serialise the score MFMAs.  The exponentials,
+// rounded to bf16, are already laid out as the B operand of O^T += V^T P^T, so P never goes
+// through LDS.
+//
+// Online softmax, as the reference defines it (s = (q.k) * scale, masked entries excluded,
+// p = exp(s - m), l sums the fp32 p, acc += bf16(p) V, out = acc / l), computed in base 2 with the
+// scale folded in: t = (q.k) * scale*log2(e), p = 2^(t - m), one FMA and one v_exp_f32 per score.
+// The running maximum m is raised only when a row's block maximum exceeds it by more than 2^8
+// (any row of the wave: then acc and l are rescaled by 2^(m_old - m_new)); otherwise p <= 256 and
+// acc, l carry the same factor, which cancels in acc / l.  The causal mask is applied only in the
+// one 64-key block that straddles a wave's diagonal; blocks above it are skipped.
 //
 // Work order: q tiles heaviest-first (causal), and workgroup ids are spread so that each XCD serves
 // one kv head group at a time (its K/V stay in that XCD's L2 while the group's query heads use them).
+// When S is not a multiple of 256 the last tile's waves past S only keep the loads and barriers
+// going (keys past S read as zero through the buffer range).
+#include <cmath>
+
 #include "ptb_common.h"
 
 using namespace ptb;
@@ -21,69 +40,129 @@ using namespace ptb;
 namespace {
 
 constexpr int D = 128;
-constexpr int BQ = 128;            // query rows per workgroup
+constexpr int BQ = 256;            // query rows per workgroup
 constexpr int BKV = 64;            // keys per block
-constexpr int kThreads = 256;
-constexpr int LDK = D + 8;         // K tile row (key) stride, elements: 272 B, conflict-free b128 reads
-constexpr int LDV = BKV + 4;       // V^T tile row (d) stride, elements: 136 B, conflict-free b64 reads
-constexpr int kKElems = BKV * LDK;
-constexpr int kVElems = D * LDV;
-constexpr int kStageElems = kKElems + kVElems;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTileBytes = BKV * D * 2;        // 16 KB: 64 key rows x 256 B
+constexpr int kStageBytes = 2 * kTileBytes;    // K tile, then V tile
+constexpr int kKPrefetch = 4;                  // K fragment reads kept ahead of the score MFMAs
+constexpr float kRescaleLog2 = 8.f;            // raise m only when a block max exceeds it by 2^8
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 
-struct KV {
-  u32x4 r[8];
+__device__ __forceinline__ bf16x8 lds_read_b128(uint32_t addr) {
+  return *reinterpret_cast<const lds_bf16x8*>(size_t(addr));
+}
+
+__device__ __forceinline__ i16x4 lds_read_tr(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(size_t(addr)));
+}
+
+__device__ __forceinline__ bf16x8 join(i16x4 lo, i16x4 hi) {
+  return __builtin_bit_cast(bf16x8, i16x8(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)));
+}
+
+// A wave's online-softmax state for its 32 queries.
+struct WaveState {
+  f32x16 acc[4];   // O^T: d = 32*dt + 8*(r/4) + 4*h + r%4, query = lane%32
+  float m;         // running maximum, log2 units (t = q.k * c)
+  float l;         // this lane's partial row sum (the lane pair's two halves add up at the end)
 };
 
-// Threads 0..127 load an 8(key) x 8(d) block of V; threads 128..255 load 8 chunks of K.
-__device__ __forceinline__ KV load_block(const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp, int key0,
-                                         int tid) {
-  KV x;
-  if (tid < 128) {
-    const int kb8 = tid & 7, db = tid >> 3;
-    const uint16_t* src = vp + int64_t(key0 + kb8 * 8) * D + db * 8;
+// S^T (64 keys x 32 queries) = K Q^T for one wave: the lane holds query lane%32 and keys
+// 32*t2 + 8*(e/4) + 4*(lane/32) + e%4 of the block.  All 16 K fragments are requested before the
+// MFMAs that use them; the scheduling groups keep kKPrefetch reads in flight.
+__device__ __forceinline__ void qk_step(f32x16 (&sacc)[2], const bf16x8 (&qf)[8], uint32_t k_tile,
+                                        const uint32_t (&koff)[8]) {
 #pragma unroll
-    for (int p = 0; p < 8; ++p) x.r[p] = *reinterpret_cast<const u32x4*>(src + p * D);
-  } else {
-    const int t = tid - 128;
+  for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = t + 128 * i;
-      x.r[i] = *reinterpret_cast<const u32x4*>(kp + int64_t(key0 + (c >> 4)) * D + (c & 15) * 8);
-    }
-  }
-  return x;
-}
-
-template <int C>
-__device__ __forceinline__ void store_vt(uint16_t* vt, const u32x4 (&r)[8]) {
-  const u32x4 col = column8x8<C>(r);
-  *reinterpret_cast<u32x2*>(vt + C * LDV) = u32x2{col[0], col[1]};
-  *reinterpret_cast<u32x2*>(vt + C * LDV + 4) = u32x2{col[2], col[3]};
-  if constexpr (C + 1 < 8) store_vt<C + 1>(vt, r);
-}
-
-__device__ __forceinline__ void store_block(uint16_t* stage, const KV& x, int tid) {
-  if (tid < 128) {
-    const int kb8 = tid & 7, db = tid >> 3;
-    store_vt<0>(stage + kKElems + (db * 8) * LDV + kb8 * 8, x.r);
-  } else {
-    const int t = tid - 128;
+    for (int e = 0; e < 16; ++e) sacc[t2][e] = 0.f;
+  bf16x8 kf[2][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = t + 128 * i;
-      *reinterpret_cast<u32x4*>(stage + (c >> 4) * LDK + (c & 15) * 8) = x.r[i];
-    }
+  for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) kf[t2][kk] = lds_read_b128(k_tile + koff[kk] + t2 * 32 * 256);
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+      sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t2][kk], qf[kk], sacc[t2], 0, 0, 0);
+  __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);   // LDS reads
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // the next read
   }
 }
 
-__device__ __forceinline__ float exp_e(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+// Online-softmax update from one S^T block; lim = query - key0 - 4*(lane/32) for the diagonal block.
+template <bool MASK>
+__device__ __forceinline__ void softmax_step(WaveState& w, f32x16 (&sacc)[2], bf16x8 (&pf)[2][2], float c,
+                                             int lim) {
+  if constexpr (MASK) {
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (32 * t2 + 8 * (e >> 2) + (e & 3) > lim) sacc[t2][e] = -INFINITY;
+  }
+  float mx = sacc[0][0];
+#pragma unroll
+  for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[t2][e]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  const float mt = mx * c;
+  if (__builtin_amdgcn_ballot_w64(mt > w.m + kRescaleLog2)) {
+    const float m_new = fmaxf(w.m, mt);
+    const float alpha = __builtin_amdgcn_exp2f(w.m - m_new);
+    w.l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) w.acc[i][e] *= alpha;
+    w.m = m_new;
+  }
+  const float nm = -w.m;
+  float lsum = 0.f;
+#pragma unroll
+  for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t2][e], c, nm));
+      lsum += p;
+      pf[t2][e >> 3][e & 7] = (__bf16)p;
+    }
+  w.l += lsum;
+}
 
-__global__ __launch_bounds__(kThreads, 2) void flash_fwd_kernel(
+// O^T[d][q] += V^T[d][key] P^T[key][q]; K-step (t2, k16) covers keys 32*t2 + 16*k16 .. +16, lane
+// half h holding keys +4h..+4h+3 and +8+4h..+8+4h+3 (the score tile's own layout).
+__device__ __forceinline__ void pv_step(WaveState& w, const bf16x8 (&pf)[2][2], uint32_t v_tile,
+                                        const uint32_t (&voff)[4]) {
+#pragma unroll
+  for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+    for (int k16 = 0; k16 < 2; ++k16)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint32_t a = v_tile + voff[dt] + (32 * t2 + 16 * k16) * 256;
+        const i16x4 lo = lds_read_tr(a);
+        const i16x4 hi = lds_read_tr(a + 8 * 256);
+        w.acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(join(lo, hi), pf[t2][k16], w.acc[dt], 0, 0, 0);
+      }
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-    uint16_t* __restrict__ O, int S, int hq, int hkv, int nkv, int nt, float scale, int causal) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * kStageElems];
+    uint16_t* __restrict__ O, int S, int hq, int hkv, int nkv, int nt, float c, int negate, int causal) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
 
   // ---- work decode: r enumerates (q tile heaviest-first, kv head); g = query head within group
   const int G = hq / hkv;
@@ -111,114 +190,110 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_kernel(
   const int h = lane >> 5, fr = lane & 31;
   const int q0 = tile * BQ;
   const int qw0 = q0 + wave * 32;
-  const int qi = qw0 + fr;  // this lane's query
+  const int qi = qw0 + fr;             // this lane's query
+  const bool active = qw0 < S;         // S is a multiple of 32: a wave's rows are all in or all out
 
-  // Q fragments (B operand of S^T = K Q^T): 8 K-steps of 16 over d
-  bf16x8 qf[8];
-  {
-    const uint16_t* src = qp + int64_t(qi) * D + h * 8;
+  // ---- K/V loaders: instruction t of this wave fills key rows 4*(2*wave + t) .. +3 of a tile;
+  //      lane L writes row L/16, slot L%16, so it fetches the chunk that belongs in that slot
+  const uint32_t kv_bytes = uint32_t(S) * D * 2u;
+  const i32x4 rsrc_k = make_rsrc(kp, kv_bytes);
+  const i32x4 rsrc_v = make_rsrc(vp, kv_bytes);
+  uint32_t k_voff[2], v_voff[2];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(src + kk * 16));
+  for (int t = 0; t < 2; ++t) {
+    const int key = 4 * (2 * wave + t) + (lane >> 4);
+    const int slot = lane & 15;
+    k_voff[t] = uint32_t(key * D + ((slot ^ (key & 15)) * 8)) * 2u;
+    v_voff[t] = uint32_t(key * D + ((slot ^ (4 * (key & 3))) * 8)) * 2u;
+  }
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
+  auto issue_block = [&](int kb) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + uint32_t(kb & 1) * kStageBytes;
+    const uint32_t soff = uint32_t(kb) * uint32_t(kTileBytes);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      dma16(rsrc_k, __builtin_amdgcn_readfirstlane(st + (wave * 2 + t) * 1024), k_voff[t], soff);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      dma16(rsrc_v, __builtin_amdgcn_readfirstlane(st + kTileBytes + (wave * 2 + t) * 1024), v_voff[t], soff);
+  };
+
+  // ---- fragment addressing
+  // K (A operand of S^T): key row 32*t2 + fr, chunk 2*kk + h in slot (2*kk + h) ^ (fr & 15)
+  uint32_t koff[8];
+  {
+    const int s = h ^ (fr & 15);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) koff[kk] = uint32_t(fr * 256 + (((2 * kk) ^ s) << 4));
+  }
+  // V^T (A operand of O^T): 16-lane group -> d half 16*g16; in-group lane 4*jj + q supplies key
+  // base + 4h + jj, d 32*dt + 16*g16 + 4q .. +3 (chunk 4dt + 2g16 + q/2, byte 8*(q&1) within it)
+  uint32_t voff[4];
+  {
+    const int g16 = (lane >> 4) & 1, l16 = lane & 15, jj = l16 >> 2, q = l16 & 3;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int chunk = 4 * dt + 2 * g16 + (q >> 1);
+      voff[dt] = uint32_t((4 * h + jj) * 256 + ((chunk ^ (4 * jj)) << 4) + (q & 1) * 8);
+    }
   }
 
-  f32x16 acc[4];
+  // ---- Q fragments (B operand of S^T = K Q^T): 8 K-steps of 16 over d; a negative scale is
+  //      carried by Q's sign (exact in bf16) so that c > 0 and the max commutes with the scaling
+  bf16x8 qf[8];
+  if (active) {
+    const uint16_t* src = qp + int64_t(qi) * D + h * 8;
+    const uint32_t flip = negate ? 0x80008000u : 0u;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(src + kk * 16);
+      v ^= flip;
+      qf[kk] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+
+  WaveState w;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
-  float m_i = -1.0e30f, l_i = 0.f;
+    for (int e = 0; e < 16; ++e) w.acc[i][e] = 0.f;
+  w.m = -INFINITY;
+  w.l = 0.f;
+  f32x16 sacc[2];
+  bf16x8 pf[2][2];
 
-  const int nb = causal ? (q0 + BQ) / BKV : S / BKV;
-  store_block(smem, load_block(kp, vp, 0, tid), tid);
-  __syncthreads();
-
+  // causal: the workgroup needs keys up to its last row; a wave stops at the block holding its
+  // diagonal (blocks past it are fully masked); inactive waves compute nothing
+  const int nb = causal ? min(q0 + BQ, S) / BKV : S / BKV;
+  const int last = !active ? -1 : causal ? (qw0 + 31) / BKV : nb - 1;
+  issue_block(0);
   for (int kb = 0; kb < nb; ++kb) {
-    const uint16_t* st = smem + (kb & 1) * kStageElems;
-    const bool more = kb + 1 < nb;
-    KV nxt;
-    if (more) nxt = load_block(kp, vp, (kb + 1) * BKV, tid);
-    const int key0 = kb * BKV;
-    // causal: skip blocks entirely above this wave's diagonal; mask the straddling one
-    const bool live = !causal || key0 <= qw0 + 31;
-    if (live) {
-      const bool partial = causal && key0 + BKV - 1 > qw0;
-      f32x16 sacc[2];
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[t2][e] = 0.f;
-        const uint16_t* krow = st + (t2 * 32 + fr) * LDK + h * 8;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + kk * 16);
-          sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sacc[t2], 0, 0, 0);
-        }
-      }
-      // scores: lane holds query qi, keys key0 + t2*32 + 8*(e/4) + 4*h + e%4
-      float mloc = -1.0e30f;
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float s = sacc[t2][e] * scale;
-          if (partial) {
-            const int key = key0 + t2 * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-            if (key > qi) s = -1.0e30f;
-          }
-          sacc[t2][e] = s;
-          mloc = fmaxf(mloc, s);
-        }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
-      const float m_new = fmaxf(m_i, mloc);
-      const float alpha = exp_e(m_i - m_new);
-      float lsum = 0.f;
-      bf16x8 pf[2][2];
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = exp_e(sacc[t2][e] - m_new);
-          lsum += p;
-          pf[t2][e >> 3][e & 7] = (__bf16)p;
-        }
-      l_i = l_i * alpha + lsum;  // per-lane partial over this lane's keys; halves combine at the end
-      m_i = m_new;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][e] *= alpha;
-      // O^T[d][q] += V^T[d][key] P^T[key][q]; K-step (t2, k16) covers keys t2*32 + k16*16 .. +16,
-      // lane half h holding keys +4h..+4h+3 and +8+4h..+8+4h+3 (the score tile's own layout)
-      const uint16_t* vt = st + kKElems;
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-        for (int k16 = 0; k16 < 2; ++k16) {
-          const int kbase = t2 * 32 + k16 * 16 + 4 * h;
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const uint16_t* vrow = vt + (dt * 32 + fr) * LDV + kbase;
-            const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-            const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-            const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-            acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t2][k16], acc[dt], 0, 0, 0);
-          }
-        }
+    wait_vmcnt<0>();
+    __syncthreads();  // block kb landed (all waves); every wave is done with block kb-1's stage
+    if (kb + 1 < nb) issue_block(kb + 1);
+    if (kb <= last) {
+      const uint32_t st = lds0 + uint32_t(kb & 1) * kStageBytes;
+      qk_step(sacc, qf, st, koff);
+      if (causal && kb == last)
+        softmax_step<true>(w, sacc, pf, c, qi - kb * BKV - 4 * h);
+      else
+        softmax_step<false>(w, sacc, pf, c, 0);
+      pv_step(w, pf, st + kTileBytes, voff);
     }
-    if (more) store_block(smem + ((kb + 1) & 1) * kStageElems, nxt, tid);
-    __syncthreads();
   }
+  if (!active) return;
 
-  const float l = l_i + __shfl_xor(l_i, 32, kWave);
+  const float l = w.l + __shfl_xor(w.l, 32, kWave);
+  const float inv = 1.f / l;
   uint16_t* orow = op + int64_t(qi) * D;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d0 = dt * 32 + 8 * g4 + 4 * h;
-      const u32x2 w = u32x2{pack_bf16x2(acc[dt][4 * g4] / l, acc[dt][4 * g4 + 1] / l),
-                            pack_bf16x2(acc[dt][4 * g4 + 2] / l, acc[dt][4 * g4 + 3] / l)};
-      *reinterpret_cast<u32x2*>(orow + d0) = w;
+      const u32x2 o = u32x2{pack_bf16x2(w.acc[dt][4 * g4] * inv, w.acc[dt][4 * g4 + 1] * inv),
+                            pack_bf16x2(w.acc[dt][4 * g4 + 2] * inv, w.acc[dt][4 * g4 + 3] * inv)};
+      *reinterpret_cast<u32x2*>(orow + d0) = o;
     }
 }
 
@@ -230,15 +305,20 @@ PTB_EXPORT int ptb_flash_attn_fwd_bf16(const void* q, const void* k, const void*
   if (batch < 0 || hq <= 0 || hkv <= 0 || seq < 0 || head_dim <= 0) return PTB_ERR_SHAPE;
   if (hq % hkv) return PTB_ERR_SHAPE;
   if (head_dim != D) return PTB_ERR_UNSUPPORTED;
+  if (!std::isfinite(scale) || scale == 0.f) return PTB_ERR_UNSUPPORTED;
   if (batch == 0 || seq == 0) return PTB_OK;
   if (!q || !k || !v || !o) return PTB_ERR_NULL;
-  if (seq % BQ) return PTB_ERR_UNSUPPORTED;
+  if (seq % 128) return PTB_ERR_UNSUPPORTED;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return PTB_ERR_ALIGN;
-  const int64_t nt = seq / BQ, nkv = batch * hkv;
+  const int64_t nt = (seq + BQ - 1) / BQ, nkv = batch * hkv;
   const int64_t total = nt * nkv * (hq / hkv);
-  if (total > 0x7fffffff || seq > 0x7fffffff || batch * hq * seq > (int64_t(1) << 40)) return PTB_ERR_GRID;
+  // K/V of one kv head are addressed through a 32-bit buffer range
+  if (total > 0x7fffffff || seq * D * 2 >= (int64_t(1) << 32) || batch * hq * seq > (int64_t(1) << 40))
+    return PTB_ERR_GRID;
+  const float c = std::fabs(scale) * 1.4426950408889634f;
   flash_fwd_kernel<<<dim3(unsigned(total)), dim3(kThreads), 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-      static_cast<uint16_t*>(o), int(seq), int(hq), int(hkv), int(nkv), int(nt), scale, causal ? 1 : 0);
+      static_cast<uint16_t*>(o), int(seq), int(hq), int(hkv), int(nkv), int(nt), c, scale < 0.f ? 1 : 0,
+      causal ? 1 : 0);
   return launch_status();
 }

@@ -31,8 +31,10 @@ def inputs(batch, hq, hkv, s, seed):
     (1, 24, 8, 512, True),      # G = 3
     (1, 64, 8, 256, True),      # G = 8
     (2, 4, 2, 384, True),       # batch > 1, S not a multiple of 256
-    (1, 8, 8, 128, True),       # MHA, a single tile
+    (1, 8, 8, 128, True),       # MHA, a single (partial) tile
+    (1, 8, 2, 640, True),       # S not a multiple of the 256-row tile
     (1, 8, 2, 512, False),      # non-causal path
+    (1, 4, 4, 384, False),      # non-causal, partial tile
 ])
 def test_flash_attention(batch, hq, hkv, s, causal):
     q, k, v = inputs(batch, hq, hkv, s, 0)
