@@ -51,6 +51,8 @@ def test_gemm_layer_shapes(m, k, n, resid):
 @pytest.mark.parametrize("m,k,n", [
     (1, 2048, 768), (8, 768, 2048), (16, 2048, 768), (100, 384, 1152), (300, 768, 128),
     (1024, 2048, 128), (257, 64, 264), (128, 4096, 4096),
+    (2000, 512, 4088),    # 256x128 tiles, ragged in M and N
+    (4000, 256, 4000),    # 256x256 tiles, ragged in M and N
 ])
 def test_gemm_ragged(m, k, n):
     got, want = run_gemm(m, k, n, 3, 1.0, 1.0 / k ** 0.5)
