@@ -3,11 +3,12 @@
 // Layout (the reference's): q, o [B*HQ, S, 128]; k, v [B*HKV, S, 128]; query head h of batch b reads
 // kv head b*HKV + h / (HQ/HKV).
 //
-// Workgroup = 8 waves = 256 query rows of one head (32 per wave); one workgroup per CU, two waves
-// per SIMD.  Blocks of 64 keys move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging)
-// into two 32 KB stages, one block ahead, shared by all 256 rows.  Both tiles keep their global
-// [key][d] layout with the 16-byte chunks of each 256-byte row XOR-swizzled, so every LDS read is
-// bank-conflict free:
+// Workgroup = 8 waves = 256 query rows of one head (32 per wave), one workgroup per CU, two waves
+// per SIMD; or, when that gives fewer than two workgroups per CU, 4 waves = 128 rows, two
+// workgroups per CU.  Blocks of 64 keys move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR
+// staging) into two 32 KB stages, one block ahead, shared by all the workgroup's rows.  Both tiles
+// keep their global [key][d] layout with the 16-byte chunks of each 256-byte row XOR-swizzled, so
+// every LDS read is bank-conflict free:
 //   K: chunk c of key row r sits in slot c ^ (r & 15); the 16 lanes of a 128-bit read take 16 keys.
 //   V: chunk c of key row r sits in slot c ^ (4 * (r & 3)); V^T fragments come from
 //      ds_read_b64_tr_b16 (within each 16-lane group lane 4j+q supplies key k+j, d n+4q..n+4q+3 and
@@ -29,8 +30,8 @@
 //
 // Work order: q tiles heaviest-first (causal), and workgroup ids are spread so that each XCD serves
 // one kv head group at a time (its K/V stay in that XCD's L2 while the group's query heads use them).
-// When S is not a multiple of 256 the last tile's waves past S only keep the loads and barriers
-// going (keys past S read as zero through the buffer range).
+// When S is not a multiple of the tile height, the last tile's waves past S only keep the loads and
+// barriers going (keys past S read as zero through the buffer range).
 #include <cmath>
 
 #include "ptb_common.h"
@@ -40,10 +41,7 @@ using namespace ptb;
 namespace {
 
 constexpr int D = 128;
-constexpr int BQ = 256;            // query rows per workgroup
 constexpr int BKV = 64;            // keys per block
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kTileBytes = BKV * D * 2;        // 16 KB: 64 key rows x 256 B
 constexpr int kStageBytes = 2 * kTileBytes;    // K tile, then V tile
 constexpr int kKPrefetch = 4;                  // K fragment reads kept ahead of the score MFMAs
@@ -159,9 +157,14 @@ __device__ __forceinline__ void pv_step(WaveState& w, const bf16x8 (&pf)[2][2], 
       }
 }
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_fwd_kernel(
+// WAVES = 8: 256 query rows per workgroup, one workgroup per CU; WAVES = 4: 128 rows, two per CU
+// (more, smaller workgroups balance the causal triangle when there are few 256-row tiles).
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int S, int hq, int hkv, int nkv, int nt, float c, int negate, int causal) {
+  constexpr int BQ = 32 * WAVES;               // query rows per workgroup
+  constexpr int kDmaT = 16 / WAVES;            // DMA instructions per wave per 16 KB tile
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
 
   // ---- work decode: r enumerates (q tile heaviest-first, kv head); g = query head within group
@@ -193,15 +196,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int qi = qw0 + fr;             // this lane's query
   const bool active = qw0 < S;         // S is a multiple of 32: a wave's rows are all in or all out
 
-  // ---- K/V loaders: instruction t of this wave fills key rows 4*(2*wave + t) .. +3 of a tile;
+  // ---- K/V loaders: instruction t of this wave fills key rows 4*(kDmaT*wave + t) .. +3 of a tile;
   //      lane L writes row L/16, slot L%16, so it fetches the chunk that belongs in that slot
   const uint32_t kv_bytes = uint32_t(S) * D * 2u;
   const i32x4 rsrc_k = make_rsrc(kp, kv_bytes);
   const i32x4 rsrc_v = make_rsrc(vp, kv_bytes);
-  uint32_t k_voff[2], v_voff[2];
+  uint32_t k_voff[kDmaT], v_voff[kDmaT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int key = 4 * (2 * wave + t) + (lane >> 4);
+  for (int t = 0; t < kDmaT; ++t) {
+    const int key = 4 * (kDmaT * wave + t) + (lane >> 4);
     const int slot = lane & 15;
     k_voff[t] = uint32_t(key * D + ((slot ^ (key & 15)) * 8)) * 2u;
     v_voff[t] = uint32_t(key * D + ((slot ^ (4 * (key & 3))) * 8)) * 2u;
@@ -211,11 +214,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint32_t st = lds0 + uint32_t(kb & 1) * kStageBytes;
     const uint32_t soff = uint32_t(kb) * uint32_t(kTileBytes);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-      dma16(rsrc_k, __builtin_amdgcn_readfirstlane(st + (wave * 2 + t) * 1024), k_voff[t], soff);
+    for (int t = 0; t < kDmaT; ++t)
+      dma16(rsrc_k, __builtin_amdgcn_readfirstlane(st + (wave * kDmaT + t) * 1024), k_voff[t], soff);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-      dma16(rsrc_v, __builtin_amdgcn_readfirstlane(st + kTileBytes + (wave * 2 + t) * 1024), v_voff[t], soff);
+    for (int t = 0; t < kDmaT; ++t)
+      dma16(rsrc_v, __builtin_amdgcn_readfirstlane(st + kTileBytes + (wave * kDmaT + t) * 1024), v_voff[t], soff);
   };
 
   // ---- fragment addressing
@@ -310,15 +313,28 @@ PTB_EXPORT int ptb_flash_attn_fwd_bf16(const void* q, const void* k, const void*
   if (!q || !k || !v || !o) return PTB_ERR_NULL;
   if (seq % 128) return PTB_ERR_UNSUPPORTED;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return PTB_ERR_ALIGN;
-  const int64_t nt = (seq + BQ - 1) / BQ, nkv = batch * hkv;
+  const int64_t nkv = batch * hkv;
+  // 256-row workgroups when there are at least two per CU, else 128-row ones (two per CU)
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const bool wide = ((seq + 255) / 256) * batch * hq >= 2 * int64_t(cus);
+  const int64_t bq = wide ? 256 : 128;
+  const int64_t nt = (seq + bq - 1) / bq;
   const int64_t total = nt * nkv * (hq / hkv);
   // K/V of one kv head are addressed through a 32-bit buffer range
   if (total > 0x7fffffff || seq * D * 2 >= (int64_t(1) << 32) || batch * hq * seq > (int64_t(1) << 40))
     return PTB_ERR_GRID;
   const float c = std::fabs(scale) * 1.4426950408889634f;
-  flash_fwd_kernel<<<dim3(unsigned(total)), dim3(kThreads), 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-      static_cast<uint16_t*>(o), int(seq), int(hq), int(hkv), int(nkv), int(nt), c, scale < 0.f ? 1 : 0,
-      causal ? 1 : 0);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto qp = static_cast<const uint16_t*>(q), kp = static_cast<const uint16_t*>(k), vp = static_cast<const uint16_t*>(v);
+  auto op = static_cast<uint16_t*>(o);
+  if (wide)
+    flash_fwd_kernel<8><<<dim3(unsigned(total)), dim3(512), 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv),
+                                                                   int(nkv), int(nt), c, scale < 0.f ? 1 : 0,
+                                                                   causal ? 1 : 0);
+  else
+    flash_fwd_kernel<4><<<dim3(unsigned(total)), dim3(256), 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv),
+                                                                   int(nkv), int(nt), c, scale < 0.f ? 1 : 0,
+                                                                   causal ? 1 : 0);
   return launch_status();
 }

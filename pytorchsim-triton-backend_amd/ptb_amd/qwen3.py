@@ -2,7 +2,9 @@
 
 The launch sequence is the reference bundle's: validation/pytorchsim/qwen3_8b_layer_prefill_2048x2048_bf16/
 manifest.json lists 14 launches of 12 kernels, 00,01,02,03,04,03,05,06,07,08,00,09,10,11, and
-:meth:`Qwen3Layer.forward` issues them in that order on the current HIP stream:
+:meth:`Qwen3Layer.forward` issues them in that order, the k branch (K03, K04) and the v branch
+(K03, K05) on two side streams that fork after K00 and join before K06, the rest on the current
+HIP stream:
 
   K00 rmsnorm(x, w_in)            K01 q = xn Wq          K02 q-norm + RoPE -> [32,T,128]
   K03 k = xn Wk                   K04 k-norm + RoPE      K03 v = xn Wv      K05 v -> [8,T,128]
@@ -83,12 +85,21 @@ class Qwen3Layer:
         self.cfg = cfg
         self._tables = {}
         self._bufs = {}
+        self._streams = {}
 
     def tables(self, tokens: int, device):
         key = (tokens, str(device))
         if key not in self._tables:
             self._tables[key] = rope_tables(tokens, self.cfg.head_dim, self.cfg.rope_theta, device)
         return self._tables[key]
+
+    def side_streams(self, device):
+        """Two side streams (default priority) and three events for the k/v branches, per device."""
+        key = str(device)
+        if key not in self._streams:
+            self._streams[key] = (torch.cuda.Stream(device), torch.cuda.Stream(device),
+                                  [torch.cuda.Event() for _ in range(3)])
+        return self._streams[key]
 
     def buffers(self, tokens: int, device) -> dict:
         """Activation buffers for one forward at this length, allocated once and reused."""
@@ -116,12 +127,25 @@ class Qwen3Layer:
         b = self.buffers(t, x.device)
         y = b["y"] if out is None else out
         ops.rmsnorm(x, w["w_in"], c.eps, out=b["xn"])                                       # K00
+        # the q, k and v branches are independent: k and v run on side streams, so their small
+        # GEMMs share the chip with q's instead of each leaving most CUs idle
+        main = torch.cuda.current_stream(x.device)
+        sk, sv, ev = self.side_streams(x.device)
+        ev[0].record(main)
+        with torch.cuda.stream(sk):
+            sk.wait_event(ev[0])
+            ops.gemm(b["xn"], w["wk"], out=b["k"])                                          # K03
+            ops.qk_norm_rope(b["k"].view(t, c.kv_heads, c.head_dim), w["w_kn"], cos, sin, c.eps, out=b["kh"])  # K04
+            ev[1].record(sk)
+        with torch.cuda.stream(sv):
+            sv.wait_event(ev[0])
+            ops.gemm(b["xn"], w["wv"], out=b["v"])                                          # K03
+            ops.transpose_heads(b["v"].view(t, c.kv_heads, c.head_dim), out=b["vh"])       # K05
+            ev[2].record(sv)
         ops.gemm(b["xn"], w["wq"], out=b["q"])                                              # K01
         ops.qk_norm_rope(b["q"].view(t, c.heads, c.head_dim), w["w_qn"], cos, sin, c.eps, out=b["qh"])   # K02
-        ops.gemm(b["xn"], w["wk"], out=b["k"])                                              # K03
-        ops.qk_norm_rope(b["k"].view(t, c.kv_heads, c.head_dim), w["w_kn"], cos, sin, c.eps, out=b["kh"])  # K04
-        ops.gemm(b["xn"], w["wv"], out=b["v"])                                              # K03
-        ops.transpose_heads(b["v"].view(t, c.kv_heads, c.head_dim), out=b["vh"])           # K05
+        main.wait_event(ev[1])
+        main.wait_event(ev[2])
         ops.flash_attention(b["qh"], b["kh"], b["vh"], c.heads, c.kv_heads, True,
                             1.0 / math.sqrt(c.head_dim), out=b["oh"])                       # K06
         ops.transpose_heads(b["oh"], out=b["o"])                                            # K07
