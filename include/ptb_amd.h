@@ -72,7 +72,8 @@ int ptb_transpose_heads_bf16(const void* x, void* y, int64_t d0, int64_t d1, int
 /* Per-(token, head) RMSNorm (eps) with weight w[head_dim], then rotate-half RoPE with fp32
  * cos/sin [tokens, head_dim], stored head-major: out[h, t, :].  x is [tokens, heads, head_dim].
  * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/02_..._mmis7ufj_triton.py:17-98 (H=32) and
- *           04_..._ll67ghqi_triton.py (H=8). */
+ *           04_..._ll67ghqi_triton.py (H=8); with tokens = 1, qwen3_8b_layer_decode_1x<S>_bf16/
+ *           02_..._twgfj5dp_triton.py:17-96 (cos/sin of the token's position, [1, head_dim]). */
 int ptb_qk_norm_rope_bf16(const void* x, const void* w, const float* cos_t, const float* sin_t,
                           void* out, int64_t tokens, int64_t heads, int64_t head_dim, float eps,
                           void* stream);
@@ -124,6 +125,45 @@ int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* wq_t, const
 int ptb_flash_attn_fwd_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
                             int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale,
                             int causal, void* stream);
+
+/* ---- single-token (decode) path: qwen3_8b_layer_decode_1x<S>_bf16 and attention_decode_* ---- */
+
+/* out[0] = sum_i (float(x[i]) + float(y[i]))^2 in fp32; y may be NULL (then sum x^2).  One workgroup.
+ * Replaces: qwen3_8b_layer_decode_1x<S>_bf16/00_..._fused__to_copy_mean_pow_3iwn5auz_triton.py:17-41 (x^2) and
+ *           05_..._fused__to_copy_add_mean_pow_tcz6sl32_triton.py:17-43 ((x + a)^2). */
+int ptb_sumsq_bf16(const void* x, const void* y, float* out, int64_t n, void* stream);
+
+/* Matrix-vector products y[n] = bf16( sum_k xp[k] * W[k,n] ), W row-major [k, n] bf16, fp32
+ * accumulation split over k; the fp32 partials live in a caller workspace of
+ * ptb_gemv_workspace_bytes(k, n) bytes.  n % 8 == 0, W 16-byte aligned.
+ *   ptb_gemv_bf16:          xp = x.
+ *     Replaces decode 04_..._fused_add_select_transpose_view_vumxrjnr_triton.py:17-42 (o-projection).
+ *   ptb_gemv_rmsnorm_bf16:  xp = ((x + add) * rsqrt(ss[0]/k + eps)) * g, all fp32; add may be NULL.
+ *     Replaces decode 01_..._fused__to_copy_add_mean_mm_mul_pow_rsqrt_ddfn4f75_triton.py:17-55 (q-projection)
+ *     and 06_..._5gopcdje_triton.py:17-57 (gate/up projection after the post-attention norm).
+ *   ptb_gemv_silu_bf16:     xp = silu(gate_up[k']) * gate_up[k + k'] (gate_up holds 2k values);
+ *     y = bf16( sum + (res_a[n] + res_b[n]) ), res_a/res_b may be NULL.
+ *     Replaces decode 07_..._fused__to_copy_add_mul_silu_slice_3d4ocw7y_triton.py:17-56 (down projection
+ *     plus the residual). */
+size_t ptb_gemv_workspace_bytes(int64_t k, int64_t n);
+int ptb_gemv_bf16(const void* x, const void* w, void* y, int64_t k, int64_t n, void* workspace,
+                  size_t workspace_bytes, void* stream);
+int ptb_gemv_rmsnorm_bf16(const void* x, const void* add, const float* ss, const void* g, float eps,
+                          const void* w, void* y, int64_t k, int64_t n, void* workspace,
+                          size_t workspace_bytes, void* stream);
+int ptb_gemv_silu_bf16(const void* gate_up, const void* w, const void* res_a, const void* res_b, void* y,
+                       int64_t k, int64_t n, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Decode attention for one query token: q, o [nkv, group, 128]; k, v [nkv, seq, 128] (nkv = batch *
+ * kv heads; query head g of kv head h is row h*group + g).  Full softmax over the seq cached keys,
+ * P rounded to bf16 before P.V, fp32 row sums.  group in {1,2,3,4,6,8}; workspace of
+ * ptb_attn_decode_workspace_bytes(nkv, group, seq) bytes.
+ * Replaces: attention_decode_<HQ>x8x<S>_bf16/00__decode_kernel/_decode_kernel_triton.py:4-29 (and
+ *           qwen3_8b_layer_decode_1x<S>_bf16/03__decode_kernel). */
+size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, int64_t seq);
+int ptb_attn_decode_bf16(const void* q, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
+                         int64_t seq, int64_t head_dim, float scale, void* workspace,
+                         size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

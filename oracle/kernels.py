@@ -4,7 +4,9 @@ All inputs/outputs are CPU tensors.  bf16 values are rounded exactly where the r
 stores to a bf16 pointer (Triton's store casts fp32 -> bf16 with round-to-nearest-even); every
 intermediate is fp32 as the reference computes it, unless a docstring says otherwise.
 Reference paths are relative to the reference repository root; ``L2048`` stands for
-``validation/pytorchsim/qwen3_8b_layer_prefill_2048x2048_bf16``.
+``validation/pytorchsim/qwen3_8b_layer_prefill_2048x2048_bf16`` and ``D4096`` for
+``validation/pytorchsim/qwen3_8b_layer_decode_1x4096_bf16`` (the other decode lengths differ only
+in S).
 """
 from __future__ import annotations
 
@@ -20,6 +22,7 @@ __all__ = [
     "rmsnorm", "softmax_rows", "silu_mul", "transpose_heads", "qk_norm_rope", "reduce_sum", "reduce_max",
     "add_scalar", "gemm", "quant_rows_e4m3", "quant_weight_e4m3", "gemm_fp8", "flash_attention",
     "rope_tables", "qwen3_layer", "E4M3_MAX",
+    "sumsq", "gemv", "gemv_rmsnorm", "gemv_silu", "attention_decode", "qwen3_decode_layer",
 ]
 
 E4M3_MAX = 448.0
@@ -211,3 +214,103 @@ def qwen3_layer(x: torch.Tensor, wts: dict, cos: torch.Tensor, sin: torch.Tensor
     gu = gemm(hn, wts["wgu"])
     a = silu_mul(gu)
     return gemm(a, wts["wd"], residual=h)
+
+
+# ---- single-token (decode) path ---------------------------------------------------------------
+
+def sumsq(x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
+    """D4096/00_..._3iwn5auz_triton.py:17-41: sum of float(x)^2 over the vector, fp32 (:34-41);
+    D4096/05_..._tcz6sl32_triton.py:17-43: the same over float(x) + float(a), the sum kept in fp32
+    (:34-38).  Returns shape [1]."""
+    v = x.float().reshape(-1)
+    if y is not None:
+        v = v + y.float().reshape(-1)
+    return (v * v).sum().reshape(1)
+
+
+def gemv(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """D4096/04_..._vumxrjnr_triton.py:17-42: y[n] = bf16(sum_k float(x[k]) * float(W[k, n]))
+    with W [K, N] row-major (in_ptr1 + x0 + N*r0, :36), fp32 accumulation (:35-42)."""
+    return (x.float().reshape(1, -1) @ w.float()).reshape(-1).to(BF16)
+
+
+def gemv_rmsnorm(x: torch.Tensor, ss: torch.Tensor, g: torch.Tensor, w: torch.Tensor,
+                 add: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
+    """D4096/01_..._ddfn4f75_triton.py:17-55 (add None): r = rsqrt(ss/K + eps) (:41-45),
+    xp = (float(x) * r) * float(g) (:46-49), y = bf16(sum_k xp[k] W[k, n]) (:50-55), no bf16
+    rounding of xp.  D4096/06_..._5gopcdje_triton.py:17-57: the same with float(x) + float(a)
+    summed in fp32 first (:41-42)."""
+    k = w.shape[0]
+    v = x.float().reshape(-1)
+    if add is not None:
+        v = v + add.float().reshape(-1)
+    r = torch.rsqrt(ss.float().reshape(()) / float(k) + eps)
+    xp = (v * r) * g.float().reshape(-1)
+    return (xp.reshape(1, -1) @ w.float()).reshape(-1).to(BF16)
+
+
+def gemv_silu(gu: torch.Tensor, w: torch.Tensor, res_a: torch.Tensor | None = None,
+              res_b: torch.Tensor | None = None) -> torch.Tensor:
+    """D4096/07_..._3d4ocw7y_triton.py:17-56: g = gu[:K], u = gu[K:] (:35-36); xp = (g / (exp(-g) + 1))
+    * u in fp32 (:38-46); acc = sum_k xp[k] W[k, n] (:47-51); y = bf16(acc + (float(res_a) +
+    float(res_b))) (:52-56)."""
+    k = w.shape[0]
+    gf = gu.float().reshape(-1)
+    g, u = gf[:k], gf[k:2 * k]
+    xp = (g / (torch.exp(-g) + 1.0)) * u
+    acc = (xp.reshape(1, -1) @ w.float()).reshape(-1)
+    if res_a is not None:
+        r = res_a.float().reshape(-1)
+        if res_b is not None:
+            r = r + res_b.float().reshape(-1)
+        acc = acc + r
+    return acc.to(BF16)
+
+
+def attention_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None,
+                     bkv: int | None = None) -> torch.Tensor:
+    """attention_decode_32x8x4096_bf16/00__decode_kernel/_decode_kernel_triton.py:4-29.  q [NKV, G, D]
+    (program pid = kv head reads q rows pid*G .. +G, :7-13), k/v [NKV, S, D].  Per block of bkv
+    keys (the spec's BKV; every bundle spec has BKV = S): qk = (q @ k^T) * scale in fp32 (:21),
+    m_new = max(m, rowmax) with m from -1e30 (:14, :22), alpha = exp(m - m_new), p = exp(qk - m_new)
+    (:23-24), l = l*alpha + sum(p) (:25), acc = acc*alpha + bf16(p) @ v (:26); o = bf16(acc / l) (:28-29)."""
+    nkv, g, d = q.shape
+    s = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    bkv = s if bkv is None else min(bkv, s)
+    out = torch.empty_like(q)
+    for h in range(nkv):
+        qq = q[h].float()
+        m_i = torch.full((g,), -1.0e30)
+        l_i = torch.zeros(g)
+        acc = torch.zeros(g, d)
+        for st in range(0, s, bkv):
+            kk = k[h, st:st + bkv].float()
+            vv = v[h, st:st + bkv].float()
+            qk = (qq @ kk.t()) * scale
+            m_new = torch.maximum(m_i, qk.amax(dim=1))
+            alpha = torch.exp(m_i - m_new)
+            p = torch.exp(qk - m_new[:, None])
+            l_i = l_i * alpha + p.sum(dim=1)
+            acc = acc * alpha[:, None] + p.to(BF16).float() @ vv
+            m_i = m_new
+        out[h] = (acc / l_i[:, None]).to(BF16)
+    return out
+
+
+def qwen3_decode_layer(x: torch.Tensor, wts: dict, kcache: torch.Tensor, vcache: torch.Tensor,
+                       cos: torch.Tensor, sin: torch.Tensor, hq: int = 32, hkv: int = 8, head_dim: int = 128,
+                       eps: float = 1e-6) -> torch.Tensor:
+    """D4096/manifest.json's 8 launches for one token over a KV cache [hkv, S, D] (data flow read
+    from the kernels' index arithmetic): K00 ss = sum x^2 -> K01 q = (x*r*w_in) Wq -> K02 q-norm +
+    RoPE (cos/sin of the token's position, [D]) -> K03 decode attention -> K04 a = o Wo ->
+    K05 ss2 = sum (x+a)^2 -> K06 gu = ((x+a)*r2*w_post) Wgu -> K07 y = (silu(g)*u) Wd + (x + a)."""
+    ss = sumsq(x)
+    q = gemv_rmsnorm(x, ss, wts["w_in"], wts["wq"], eps=eps)
+    qh = qk_norm_rope(q.view(1, hq, head_dim), wts["w_qn"], cos.reshape(1, head_dim), sin.reshape(1, head_dim), eps)
+    o = attention_decode(qh.view(hkv, hq // hkv, head_dim), kcache, vcache, 1.0 / math.sqrt(head_dim))
+    a = gemv(o.reshape(-1), wts["wo"])
+    ss2 = sumsq(x, a)
+    gu = gemv_rmsnorm(x, ss2, wts["w_post"], wts["wgu"], add=a, eps=eps)
+    return gemv_silu(gu, wts["wd"], x, a)

@@ -87,6 +87,14 @@ SIGNATURES = {
     "ptb_gemm_fp8_scaled": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "ptb_flash_attn_fwd_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32,
                                          _c_int, _vp]),
+    "ptb_sumsq_bf16": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
+    "ptb_gemv_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
+    "ptb_gemv_bf16": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
+    "ptb_gemv_rmsnorm_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_f32, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
+    "ptb_gemv_silu_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
+    "ptb_attn_decode_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
+    "ptb_attn_decode_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _vp, _c_size,
+                                      _vp]),
 }
 
 _lock = threading.Lock()

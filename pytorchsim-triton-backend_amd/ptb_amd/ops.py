@@ -201,3 +201,97 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, hq: int, 
     _lib.call("ptb_flash_attn_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), batch, hq, hkv, s,
               d, sc, 1 if causal else 0, _stream(q))
     return o
+
+
+# ---- single-token (decode) path -------------------------------------------------------------------
+
+def sumsq(x: torch.Tensor, y: torch.Tensor | None = None, out=None) -> torch.Tensor:
+    """sum((x + y)^2) (or sum(x^2)) over all elements of bf16 vectors, as one fp32 value (shape [1])."""
+    _need(x, "x", BF16)
+    if y is not None:
+        _need(y, "y", BF16)
+        if y.numel() != x.numel():
+            raise ValueError("x and y must have the same number of elements")
+    r = _out(out, (1,), F32, x)
+    _lib.call("ptb_sumsq_bf16", x.data_ptr(), y.data_ptr() if y is not None else None, r.data_ptr(), x.numel(),
+              _stream(x))
+    return r
+
+
+def _gemv_args(xk: int, w: torch.Tensor, out, like: torch.Tensor, workspace):
+    _need(w, "w", BF16, 2)
+    k, n = w.shape
+    if xk != k:
+        raise ValueError(f"the vector has {xk} elements, W has {k} rows")
+    y = _out(out, (n,), BF16, like)
+    need = _lib.load().ptb_gemv_workspace_bytes(k, n)
+    if workspace is None:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=like.device)
+    return k, n, y, workspace, workspace.numel() * workspace.element_size()
+
+
+def gemv(x: torch.Tensor, w: torch.Tensor, out=None, workspace=None) -> torch.Tensor:
+    """y[n] = bf16(sum_k x[k] W[k,n]), W [K,N] bf16, fp32 accumulation."""
+    _need(x, "x", BF16)
+    k, n, y, ws, wsb = _gemv_args(x.numel(), w, out, x, workspace)
+    _lib.call("ptb_gemv_bf16", x.data_ptr(), w.data_ptr(), y.data_ptr(), k, n, ws.data_ptr(), wsb, _stream(x))
+    return y
+
+
+def gemv_rmsnorm(x: torch.Tensor, ss: torch.Tensor, g: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None = None,
+                 eps: float = 1e-6, out=None, workspace=None) -> torch.Tensor:
+    """y = bf16( (((x + add) * rsqrt(ss/K + eps)) * g) @ W ), the normalised vector kept in fp32."""
+    _need(x, "x", BF16)
+    _need(ss, "ss", F32)
+    _need(g, "g", BF16)
+    if add is not None:
+        _need(add, "add", BF16)
+        if add.numel() != x.numel():
+            raise ValueError("add must match x")
+    if g.numel() != x.numel():
+        raise ValueError("g must match x")
+    k, n, y, ws, wsb = _gemv_args(x.numel(), w, out, x, workspace)
+    _lib.call("ptb_gemv_rmsnorm_bf16", x.data_ptr(), add.data_ptr() if add is not None else None, ss.data_ptr(),
+              g.data_ptr(), float(eps), w.data_ptr(), y.data_ptr(), k, n, ws.data_ptr(), wsb, _stream(x))
+    return y
+
+
+def gemv_silu(gate_up: torch.Tensor, w: torch.Tensor, res_a: torch.Tensor | None = None,
+              res_b: torch.Tensor | None = None, out=None, workspace=None) -> torch.Tensor:
+    """y = bf16( (silu(g) * u) @ W + (res_a + res_b) ), gate_up = g | u (2K values)."""
+    _need(gate_up, "gate_up", BF16)
+    if gate_up.numel() % 2:
+        raise ValueError("gate_up must hold gate and up halves")
+    for t, name in ((res_a, "res_a"), (res_b, "res_b")):
+        if t is not None:
+            _need(t, name, BF16)
+    if res_b is not None and res_a is None:
+        raise ValueError("res_b needs res_a")
+    k, n, y, ws, wsb = _gemv_args(gate_up.numel() // 2, w, out, gate_up, workspace)
+    for t, name in ((res_a, "res_a"), (res_b, "res_b")):
+        if t is not None and t.numel() != n:
+            raise ValueError(f"{name} must have {n} elements")
+    _lib.call("ptb_gemv_silu_bf16", gate_up.data_ptr(), w.data_ptr(),
+              res_a.data_ptr() if res_a is not None else None, res_b.data_ptr() if res_b is not None else None,
+              y.data_ptr(), k, n, ws.data_ptr(), wsb, _stream(gate_up))
+    return y
+
+
+def attention_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None, out=None,
+                     workspace=None) -> torch.Tensor:
+    """One-token attention over a KV cache: q [NKV, G, D], k/v [NKV, S, D] bf16 -> o [NKV, G, D]."""
+    _need(q, "q", BF16, 3)
+    _need(k, "k", BF16, 3)
+    _need(v, "v", BF16, 3)
+    nkv, g, d = q.shape
+    if k.shape[0] != nkv or k.shape[2] != d or tuple(v.shape) != tuple(k.shape):
+        raise ValueError("k and v must be [NKV, S, D] matching q")
+    s = k.shape[1]
+    o = _out(out, (nkv, g, d), BF16, q)
+    need = _lib.load().ptb_attn_decode_workspace_bytes(nkv, g, s)
+    if workspace is None:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    sc = default_scale(d) if scale is None else float(scale)
+    _lib.call("ptb_attn_decode_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), nkv, g, s, d, sc,
+              workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(q))
+    return o

@@ -159,6 +159,68 @@ class Qwen3Layer:
     __call__ = forward
 
 
+class Qwen3DecodeLayer:
+    """One decoder layer for a single new token over a KV cache, as the reference's decode bundle
+    composes it (validation/pytorchsim/qwen3_8b_layer_decode_1x<S>_bf16/manifest.json, 8 launches):
+
+      K00 ss = sum x^2                       K01 q = (x*r*w_in) Wq            (GEMV, fp32 prologue)
+      K02 q-norm + RoPE (one position)       K03 decode attention over [8, S, 128] K/V
+      K04 a = o Wo                           K05 ss2 = sum (x + a)^2
+      K06 gu = ((x + a)*r2*w_post) Wgu       K07 y = (silu(g)*u) Wd + (x + a)
+
+    (The bundle's decode layer reads the cache as given; it computes no k/v for the new token.)
+    Weights as from :func:`random_weights`; the GEMV and attention workspaces are allocated once."""
+
+    def __init__(self, weights: dict, cfg: Qwen3Config = QWEN3_8B):
+        self.w = weights
+        self.cfg = cfg
+        self._bufs = {}
+
+    def buffers(self, seq: int, device) -> dict:
+        key = (seq, str(device))
+        if key not in self._bufs:
+            c = self.cfg
+            lib = ops._lib.load()
+            gemv_ws = max(lib.ptb_gemv_workspace_bytes(c.hidden, c.heads * c.head_dim),
+                          lib.ptb_gemv_workspace_bytes(c.heads * c.head_dim, c.hidden),
+                          lib.ptb_gemv_workspace_bytes(c.hidden, 2 * c.intermediate),
+                          lib.ptb_gemv_workspace_bytes(c.intermediate, c.hidden))
+            attn_ws = lib.ptb_attn_decode_workspace_bytes(c.kv_heads, c.heads // c.kv_heads, seq)
+
+            def e(*shape, dtype=BF16):
+                return torch.empty(*shape, dtype=dtype, device=device)
+
+            self._bufs[key] = {
+                "ss": e(1, dtype=torch.float32), "q": e(c.heads * c.head_dim), "qh": e(c.heads, 1, c.head_dim),
+                "o": e(c.kv_heads, c.heads // c.kv_heads, c.head_dim), "a": e(c.hidden),
+                "ss2": e(1, dtype=torch.float32), "gu": e(2 * c.intermediate), "y": e(c.hidden),
+                "ws": e(max(gemv_ws, 4), dtype=torch.uint8), "attn_ws": e(max(attn_ws, 4), dtype=torch.uint8),
+            }
+        return self._bufs[key]
+
+    def forward(self, x: torch.Tensor, kcache: torch.Tensor, vcache: torch.Tensor, cos: torch.Tensor,
+                sin: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """x [hidden] bf16; kcache/vcache [kv_heads, S, head_dim] bf16; cos/sin [head_dim] fp32 of the
+        token's position."""
+        c, w = self.cfg, self.w
+        b = self.buffers(kcache.shape[1], x.device)
+        y = b["y"] if out is None else out
+        ops.sumsq(x, out=b["ss"])                                                              # K00
+        ops.gemv_rmsnorm(x, b["ss"], w["w_in"], w["wq"], eps=c.eps, out=b["q"], workspace=b["ws"])  # K01
+        ops.qk_norm_rope(b["q"].view(1, c.heads, c.head_dim), w["w_qn"], cos.view(1, c.head_dim),
+                         sin.view(1, c.head_dim), c.eps, out=b["qh"])                          # K02
+        ops.attention_decode(b["qh"].view(c.kv_heads, c.heads // c.kv_heads, c.head_dim), kcache, vcache,
+                             1.0 / math.sqrt(c.head_dim), out=b["o"], workspace=b["attn_ws"])  # K03
+        ops.gemv(b["o"].view(-1), w["wo"], out=b["a"], workspace=b["ws"])                      # K04
+        ops.sumsq(x, b["a"], out=b["ss2"])                                                     # K05
+        ops.gemv_rmsnorm(x, b["ss2"], w["w_post"], w["wgu"], add=b["a"], eps=c.eps, out=b["gu"],
+                         workspace=b["ws"])                                                    # K06
+        ops.gemv_silu(b["gu"], w["wd"], x, b["a"], out=y, workspace=b["ws"])                   # K07
+        return y
+
+    __call__ = forward
+
+
 def layer_work(tokens: int, cfg: Qwen3Config = QWEN3_8B) -> list:
     """(name, flops, hbm bytes) of each launch at this length: the roofline model of the layer
     (flop conventions as the reference reports: 2*M*N*K per GEMM, 4*H*D*S(S+1)/2 causal attention;

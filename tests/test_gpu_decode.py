@@ -1,0 +1,125 @@
+"""Parity of the single-token (decode) kernels with the oracle's restatements of
+qwen3_8b_layer_decode_1x<S>_bf16/{00..07} and attention_decode_<HQ>x8x<S>_bf16/00__decode_kernel.
+bf16 outputs: rtol 2e-2 with the absolute floor at 2e-2 of the output's mean magnitude (the GEMV
+outputs are not O(1)); fp32 sums within 1e-6 of the sum of |terms|; exact invariants bit for bit."""
+import math
+
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close, bits_equal, randn
+from ptb_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+RTOL = 2e-2
+
+
+def close_scaled(got, want, what):
+    scale = float(want.float().abs().mean()) + 1e-6
+    assert_close(got, want, RTOL, 2e-2 * max(scale, 1e-3), what)
+
+
+@pytest.mark.parametrize("n,seed", [(4096, 0), (12288, 1), (4100, 2), (8, 3), (3, 4)])
+def test_sumsq(n, seed):
+    x, a = randn((n,), seed), randn((n,), seed + 100)
+    for y in (None, a):
+        got = ops.sumsq(x.to(DEV), None if y is None else y.to(DEV)).cpu()
+        want = oracle.sumsq(x, y)
+        terms = (x.float() + (0 if y is None else y.float())).double().pow(2).sum()
+        assert abs(float(got) - float(want)) <= 1e-6 * float(terms) + 1e-6
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 24576), (12288, 4096), (100, 8), (1000, 520), (33, 16)])
+def test_gemv_plain_and_rmsnorm(k, n):
+    x, a = randn((k,), 5), randn((k,), 6)
+    g = randn((k,), 7, std=0.02, mean=1.0)
+    w = randn((k, n), 8, std=0.02)
+    xd, ad, gd, wd = x.to(DEV), a.to(DEV), g.to(DEV), w.to(DEV)
+    close_scaled(ops.gemv(xd, wd).cpu(), oracle.gemv(x, w), f"gemv {k}x{n}")
+    ss = oracle.sumsq(x, a)
+    got = ops.gemv_rmsnorm(xd, ss.to(DEV), gd, wd, add=ad, eps=1e-6).cpu()
+    close_scaled(got, oracle.gemv_rmsnorm(x, ss, g, w, add=a, eps=1e-6), f"gemv_rmsnorm+add {k}x{n}")
+    ss1 = oracle.sumsq(x)
+    got = ops.gemv_rmsnorm(xd, ss1.to(DEV), gd, wd, eps=1e-6).cpu()
+    close_scaled(got, oracle.gemv_rmsnorm(x, ss1, g, w, eps=1e-6), f"gemv_rmsnorm {k}x{n}")
+
+
+@pytest.mark.parametrize("k,n", [(12288, 4096), (64, 8), (777, 264)])
+def test_gemv_silu_with_residual(k, n):
+    gu = randn((2 * k,), 9)
+    w = randn((k, n), 10, std=0.02)
+    ra, rb = randn((n,), 11), randn((n,), 12)
+    gud, wd = gu.to(DEV), w.to(DEV)
+    got = ops.gemv_silu(gud, wd, ra.to(DEV), rb.to(DEV)).cpu()
+    close_scaled(got, oracle.gemv_silu(gu, w, ra, rb), f"gemv_silu {k}x{n}")
+    got = ops.gemv_silu(gud, wd).cpu()
+    close_scaled(got, oracle.gemv_silu(gu, w), f"gemv_silu no residual {k}x{n}")
+
+
+def test_gemv_exact_small_integers():
+    """Small-integer operands: every product and partial sum is exact in fp32, so the split-K order
+    cannot matter and the result is bit-exact."""
+    g = torch.Generator().manual_seed(13)
+    x = torch.randint(-4, 5, (1024,), generator=g).to(torch.bfloat16)
+    w = torch.randint(-4, 5, (1024, 512), generator=g).to(torch.bfloat16)
+    got = ops.gemv(x.to(DEV), w.to(DEV)).cpu()
+    assert bits_equal(got, oracle.gemv(x, w))
+
+
+@pytest.mark.parametrize("hq,s", [(32, 4096), (16, 128), (24, 1024), (64, 8192), (32, 2048), (8, 256)])
+def test_attention_decode_bundle_shapes(hq, s):
+    hkv = 8
+    g = hq // hkv
+    q, k, v = randn((hkv, g, 128), 14), randn((hkv, s, 128), 15), randn((hkv, s, 128), 16)
+    got = ops.attention_decode(q.to(DEV), k.to(DEV), v.to(DEV), 1 / math.sqrt(128)).cpu()
+    want = oracle.attention_decode(q, k, v, 1 / math.sqrt(128))
+    assert_close(got, want, RTOL, 2e-2, f"decode {hq}x{hkv}x{s}")
+
+
+@pytest.mark.parametrize("nkv,g,s", [(3, 6, 200), (2, 1, 130), (1, 3, 1), (4, 2, 127)])
+def test_attention_decode_ragged(nkv, g, s):
+    q, k, v = randn((nkv, g, 128), 17), randn((nkv, s, 128), 18), randn((nkv, s, 128), 19)
+    got = ops.attention_decode(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
+    assert_close(got, oracle.attention_decode(q, k, v), RTOL, 2e-2, f"decode ragged {nkv}x{g}x{s}")
+    if s == 1:   # one key: p = 1, so O = V[0] bit for bit
+        for h in range(nkv):
+            for gi in range(g):
+                assert bits_equal(got[h, gi], v[h, 0])
+
+
+def test_decode_refusals():
+    q = torch.zeros((2, 5, 128), dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros((2, 64, 128), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.UnsupportedError):
+        ops.attention_decode(q, k, k)                                   # group 5 is not built
+    q4 = torch.zeros((2, 4, 128), dtype=torch.bfloat16, device=DEV)
+    small = torch.empty(16, dtype=torch.uint8, device=DEV)
+    with pytest.raises(_lib.PtbError) as e:
+        ops.attention_decode(q4, k, k, workspace=small)
+    assert e.value.status == _lib.PTB_ERR_WORKSPACE
+    x = torch.zeros(64, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros((64, 12), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.UnsupportedError):
+        ops.gemv(x, w)                                                  # n % 8 != 0
+
+
+def test_qwen3_decode_layer_matches_oracle():
+    """The 8 decode launches at Qwen3-8B's full dimensions over a 1024-token cache."""
+    from ptb_amd import qwen3
+
+    s = 1024
+    wts = qwen3.random_weights(seed=3)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(4096, generator=g).to(torch.bfloat16)
+    kc = torch.randn(8, s, 128, generator=g).to(torch.bfloat16)
+    vc = torch.randn(8, s, 128, generator=g).to(torch.bfloat16)
+    cos_t, sin_t = oracle.rope_tables(s + 1, 128, 1.0e6)
+    cos, sin = cos_t[s], sin_t[s]
+    layer = qwen3.Qwen3DecodeLayer({k: v.to(DEV) for k, v in wts.items()})
+    y = layer(x.to(DEV), kc.to(DEV), vc.to(DEV), cos.to(DEV), sin.to(DEV)).cpu()
+    want = oracle.qwen3_decode_layer(x, wts, kc, vc, cos, sin)
+    rms = float(want.float().pow(2).mean().sqrt())
+    assert_close(y, want, RTOL, 2e-2 * max(1.0, rms), "qwen3 decode layer")

@@ -287,6 +287,101 @@ def test_qwen3_layer_matches_fp64_block():
     assert torch.allclose(got.double(), y, rtol=3e-2, atol=3e-2)
 
 
+# ------------------------------------------------------------------ decode path pins
+def test_sumsq_fsum_and_cross_terms():
+    x, a = rnd((4096,), 30), rnd((4096,), 31)
+    got = float(oracle.sumsq(x))
+    want = math.fsum(float(v) ** 2 for v in x.float())
+    assert abs(got - want) <= 1e-6 * want
+    got2 = float(oracle.sumsq(x, a))
+    s32 = (x.float() + a.float()).double()          # the reference adds in fp32, then squares
+    want2 = math.fsum(float(v) ** 2 for v in s32)
+    assert abs(got2 - want2) <= 1e-6 * want2
+    no_cross = math.fsum(float(v) ** 2 for v in x.float()) + math.fsum(float(v) ** 2 for v in a.float())
+    assert abs(no_cross - want2) > 1e-3 * want2      # a slip that drops the cross terms is visible
+
+
+def test_gemv_variants_match_fp64():
+    k, n = 512, 384
+    x, a = rnd((k,), 32), rnd((k,), 33)
+    g = rnd((k,), 34, std=0.02, mean=1.0)
+    w = rnd((k, n), 35, std=0.05)
+    tol = dict(rtol=2 ** -7, atol=1e-3)
+    assert torch.allclose(oracle.gemv(x, w).double(), x.double() @ w.double(), **tol)
+    ss = oracle.sumsq(x, a)
+    got = oracle.gemv_rmsnorm(x, ss, g, w, add=a, eps=1e-6)
+    h = (x.float() + a.float()).double()
+    want = F.rms_norm(h, (k,), g.double(), 1e-6) @ w.double()
+    assert torch.allclose(got.double(), want, **tol)
+    plain = oracle.gemv_rmsnorm(x, oracle.sumsq(x), g, w, eps=1e-6)
+    assert torch.allclose(plain.double(), F.rms_norm(x.double(), (k,), g.double(), 1e-6) @ w.double(), **tol)
+    gu = rnd((2 * k,), 36)
+    wd = rnd((k, n), 37, std=0.05)
+    ra, rb = rnd((n,), 38), rnd((n,), 39)
+    got = oracle.gemv_silu(gu, wd, ra, rb)
+    gd = gu.double()
+    want = (F.silu(gd[:k]) * gd[k:]) @ wd.double() + (ra.float() + rb.float()).double()
+    assert torch.allclose(got.double(), want, **tol)
+    # a transposed weight or a gate/up swap is caught
+    xs, wsq = x[:n], w[:n, :n]
+    assert not torch.allclose(oracle.gemv(xs, wsq.t().contiguous()).double(), xs.double() @ wsq.double(), **tol)
+    swapped = oracle.gemv_silu(torch.cat([gu[k:], gu[:k]]), wd, ra, rb)
+    assert not torch.allclose(swapped.double(), want, **tol)
+
+
+@pytest.mark.parametrize("nkv,g,s", [(2, 4, 256), (3, 3, 128), (1, 8, 64)])
+def test_attention_decode_matches_sdpa(nkv, g, s):
+    q, k, v = rnd((nkv, g, 128), 40), rnd((nkv, s, 128), 41), rnd((nkv, s, 128), 42)
+    scale = 1 / math.sqrt(128)
+    got = oracle.attention_decode(q, k, v, scale)
+    want = F.scaled_dot_product_attention(q.double().unsqueeze(2), k.double().unsqueeze(1).expand(nkv, g, s, 128),
+                                          v.double().unsqueeze(1).expand(nkv, g, s, 128), scale=scale).squeeze(2)
+    assert torch.allclose(got.double(), want, rtol=2e-2, atol=2e-2)
+    blocked = oracle.attention_decode(q, k, v, scale, bkv=max(1, s // 4))   # blocking changes only roundings
+    assert torch.allclose(blocked.double(), want, rtol=2e-2, atol=2e-2)
+
+
+def test_attention_decode_invariants():
+    q, k = rnd((2, 4, 128), 43), rnd((2, 1, 128), 44)
+    v = rnd((2, 1, 128), 45)
+    o = oracle.attention_decode(q, k, v)
+    for h in range(2):
+        for gi in range(4):
+            assert torch.equal(o[h, gi], v[h, 0])                      # one key: p = 1 exactly
+    kk = rnd((2, 64, 128), 46)
+    vc = torch.full((2, 64, 128), -1.25).to(torch.bfloat16)
+    oc = oracle.attention_decode(q, kk, vc).float()
+    assert (oc + 1.25).abs().max() <= 1.25 * 2 ** -7                   # V const -> O const
+
+
+def test_qwen3_decode_layer_matches_fp64_step():
+    """The 8-launch decode composition against an fp64 Qwen3 decode step written from the model's
+    definition over the same KV cache (no bf16 rounding between ops)."""
+    hid, hq, hkv, d, inter, s = 256, 4, 2, 128, 384, 96
+    g = torch.Generator().manual_seed(47)
+
+    def r(*shape, mean=0.0, std=0.02):
+        return (torch.randn(*shape, generator=g) * std + mean).to(torch.bfloat16)
+
+    x = r(hid, std=1.0)
+    w = {"w_in": r(hid, mean=1.0), "wq": r(hid, hq * d), "w_qn": r(d, mean=1.0), "wo": r(hq * d, hid),
+         "w_post": r(hid, mean=1.0), "wgu": r(hid, 2 * inter), "wd": r(inter, hid)}
+    kc, vc = r(hkv, s, d, std=1.0), r(hkv, s, d, std=1.0)
+    cos_t, sin_t = oracle.rope_tables(s + 1, d, 1.0e6)
+    cos, sin = cos_t[s], sin_t[s]                 # the new token's position
+    got = oracle.qwen3_decode_layer(x, w, kc, vc, cos, sin, hq, hkv, d, 1e-6)
+    W = {k: v.double() for k, v in w.items()}
+    X = x.double()
+    q = (F.rms_norm(X, (hid,), W["w_in"], 1e-6) @ W["wq"]).view(1, hq, d)
+    qh = ref_rope(q, w["w_qn"], cos[None], sin[None], 1e-6).reshape(hkv, hq // hkv, 1, d)
+    o = F.scaled_dot_product_attention(qh, kc.double().unsqueeze(1).expand(hkv, hq // hkv, s, d),
+                                       vc.double().unsqueeze(1).expand(hkv, hq // hkv, s, d), scale=1 / math.sqrt(d))
+    h = X + o.reshape(hq * d) @ W["wo"]
+    gu = F.rms_norm(h, (hid,), W["w_post"], 1e-6) @ W["wgu"]
+    y = h + (F.silu(gu[:inter]) * gu[inter:]) @ W["wd"]
+    assert torch.allclose(got.double(), y, rtol=3e-2, atol=3e-2)
+
+
 # ------------------------------------------------------------------ planted slips are caught
 def test_pins_catch_planted_slips(monkeypatch):
     x, w = rnd((64, 4096), 0), rnd((4096,), 1, torch.float32, 0.02, 1.0)
