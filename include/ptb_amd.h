@@ -89,6 +89,11 @@ int ptb_reduce_bf16(const void* x, float* out, int64_t n, int op, void* workspac
 /* y = bf16(float(x) + s) elementwise.  Replaces vector_add1_<R>x<C>_bf16/00_..._du5rd5jd_triton.py. */
 int ptb_add_scalar_bf16(const void* x, void* y, int64_t n, float s, void* stream);
 
+/* out[i] = float(x[first + i]) + s into fp32, i < count (a slice of a bf16 tensor plus a constant).
+ * Replaces vector_slice_<R>x<C>_bf16/00_..._fused__to_copy_add_slice_slnyinbt_triton.py:17-27
+ * (first = 0, count = 1, s = 1). */
+int ptb_slice_add_bf16(const void* x, float* out, int64_t first, int64_t count, float s, void* stream);
+
 /* Dense GEMM, row-major: C[m,n] = bf16( sum_k A[m,k] * B[k,n] (+ float(R[m,n])) ), fp32 accumulation.
  * residual may be NULL.  Requires k % 64 == 0 and n % 8 == 0; m is free.
  * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/01_..._fused_mm_ckb6aiys_triton.py:18-97 (and

@@ -22,7 +22,7 @@ __all__ = [
     "rmsnorm", "softmax_rows", "silu_mul", "transpose_heads", "qk_norm_rope", "reduce_sum", "reduce_max",
     "add_scalar", "gemm", "quant_rows_e4m3", "quant_weight_e4m3", "gemm_fp8", "flash_attention",
     "rope_tables", "qwen3_layer", "E4M3_MAX",
-    "sumsq", "gemv", "gemv_rmsnorm", "gemv_silu", "attention_decode", "qwen3_decode_layer",
+    "slice_add", "sumsq", "gemv", "gemv_rmsnorm", "gemv_silu", "attention_decode", "qwen3_decode_layer",
 ]
 
 E4M3_MAX = 448.0
@@ -96,6 +96,12 @@ def reduce_max(x: torch.Tensor) -> torch.Tensor:
 def add_scalar(x: torch.Tensor, s: float = 1.0) -> torch.Tensor:
     """vector_add1_<R>x<C>_bf16/00_..._du5rd5jd_triton.py: bf16(float(x) + 1.0)."""
     return (x.float() + s).to(BF16)
+
+
+def slice_add(x: torch.Tensor, first: int = 0, count: int = 1, s: float = 1.0) -> torch.Tensor:
+    """vector_slice_<R>x<C>_bf16/00_..._slnyinbt_triton.py:17-27: fp32 out = float(x[0]) + 1.0 (:22-27),
+    generalised to a run of `count` elements from `first`."""
+    return x.reshape(-1)[first:first + count].float() + s
 
 
 def gemm(a: torch.Tensor, b: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:

@@ -357,6 +357,13 @@ __global__ __launch_bounds__(kBlock) void add_scalar(const uint16_t* __restrict_
     for (int64_t i = (chunks << 3) + threadIdx.x; i < n; i += kBlock) y[i] = f32_to_bf16(bf16_to_f32(x[i]) + s);
 }
 
+// out[i] = float(x[first + i]) + s into fp32, for a short run of elements.
+__global__ __launch_bounds__(kBlock) void slice_add(const uint16_t* __restrict__ x, float* __restrict__ out,
+                                                    int64_t count, float s) {
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < count; i += int64_t(gridDim.x) * kBlock)
+    out[i] = bf16_to_f32(x[i]) + s;
+}
+
 int grid_for(int64_t work, int64_t per_block, int64_t cap) {
   int64_t g = (work + per_block - 1) / per_block;
   if (g < 1) g = 1;
@@ -518,5 +525,15 @@ PTB_EXPORT int ptb_add_scalar_bf16(const void* x, void* y, int64_t n, float s, v
   const int g = grid_for(n / 8 + 1, int64_t(kBlock) * 4, 1 << 20);
   add_scalar<<<dim3(g), dim3(kBlock), 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), n, s);
+  return launch_status();
+}
+
+PTB_EXPORT int ptb_slice_add_bf16(const void* x, float* out, int64_t first, int64_t count, float s, void* stream) {
+  if (first < 0 || count < 0) return PTB_ERR_SHAPE;
+  if (count == 0) return PTB_OK;
+  if (!x || !out) return PTB_ERR_NULL;
+  const int g = grid_for(count, kBlock, 1 << 16);
+  slice_add<<<dim3(g), dim3(kBlock), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(x) + first, out, count, s);
   return launch_status();
 }

@@ -16,6 +16,14 @@ the hot path is one of a few hand-written HIP families, chosen from what the spe
   softmax     ``softmax`` kernels with scalars xnumel (rows), r0_numel (cols) (vector_softmax_*)
   reduce      whole-tensor ``sum`` / ``max`` into one fp32 (vector_sum_*, vector_max_*)
   add_scalar  ``fused_add``: bf16(x + c) (vector_add1_*)
+  slice_add   fp32 out[i] = x[first + i] + c (vector_slice_*)
+  attention_decode ``_decode_kernel`` with constexprs HKV, G, S, D (attention_decode_*/00,
+              qwen3_8b_layer_decode_*/03)
+  sumsq       sum of squares of one bf16 vector (or of the sum of two) into one fp32
+              (qwen3_8b_layer_decode_*/00, 05)
+  gemv        out[N] = sum_k xp[k] * W[k, N] with W [K, N] row-major: plain (decode 04 and the M = 1
+              ``mm`` template), with an RMSNorm prologue over a precomputed sum of squares (decode
+              01, 06), or with a silu(g)*u prologue and a residual sum epilogue (decode 07)
 
 Anything else raises :class:`UnsupportedKernel` -- there is no fallback execution.
 """
@@ -120,6 +128,49 @@ def _names(spec):
     return [a.name for a in spec.args]
 
 
+def _gemv_plan(spec: KernelSpec, source: str | None) -> Plan | None:
+    """The decode layer's matrix-vector kernels, recognised by their operands: one bf16 output of N
+    values, a bf16 weight of K*N values read row-major (``in_ptrW + (x0 + N*r0_1)``, checked when
+    the source is at hand) and the vector operands beside it."""
+    pure = [a for a in spec.args if a.role == "in"]
+    outs = spec.outputs()
+    if len(outs) != 1 or outs[0].dtype != "bfloat16" or len(pure) < 2:
+        return None
+    y = outs[0]
+    n = y.numel
+    w = max(pure, key=lambda a: a.numel)
+    if w.dtype != "bfloat16" or n == 0 or w.numel % n or w.numel == n:
+        return None
+    k = w.numel // n
+    rest = [a for a in pure if a is not w]
+    name = spec.name
+    scal = [a for a in rest if a.dtype == "float32" and a.numel == 1]
+    vecs = [a for a in rest if a.dtype == "bfloat16" and a.numel == k]
+    plan = None
+    if "silu" in name:
+        gu = [a for a in rest if a.dtype == "bfloat16" and a.numel == 2 * k]
+        res = [a for a in rest if a.dtype == "bfloat16" and a.numel == n]
+        if len(gu) == 1 and len(res) <= 2 and len(rest) == 1 + len(res):
+            plan = Plan("gemv", dict(mode="silu", k=k, n=n, x=gu[0].name, w=w.name, y=y.name,
+                                     res_a=res[0].name if res else None, res_b=res[1].name if len(res) > 1 else None))
+    elif "rsqrt" in name and len(scal) == 1 and len(rest) == len(vecs) + 1 and len(vecs) in (2, 3):
+        # argument order: x (, a) before the sum of squares, the norm weight after it
+        ss = scal[0]
+        before = [a for a in vecs if rest.index(a) < rest.index(ss)]
+        after = [a for a in vecs if rest.index(a) > rest.index(ss)]
+        if len(after) == 1 and len(before) in (1, 2):
+            plan = Plan("gemv", dict(mode="rms", k=k, n=n, x=before[0].name,
+                                     add=before[1].name if len(before) == 2 else None, ss=ss.name,
+                                     g=after[0].name, eps=1e-6, w=w.name, y=y.name))
+    elif len(rest) == 1 and len(vecs) == 1:
+        plan = Plan("gemv", dict(mode="plain", k=k, n=n, x=vecs[0].name, w=w.name, y=y.name))
+    if plan is not None and source:
+        terms = _index_terms(_load_index(source, w.name))
+        if terms != {"x0": 1, "r0_1": n}:
+            raise UnsupportedKernel(f"{name}: W is read as {terms}, not row-major [K, N]")
+    return plan
+
+
 def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
     """The HIP family and its parameters for one reference kernel."""
     names = _names(spec)
@@ -128,11 +179,22 @@ def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
     # index facts a manifest may carry instead of the Triton source (see kernel_hints)
     hints = (spec.extra or {}).get("hints", {})
     name = spec.name
+    if {"HKV", "G", "S", "D"} <= set(ce) and "decode" in name:
+        if len(spec.args) != 4:
+            raise UnsupportedKernel(f"{name}: decode attention takes q, k, v, o")
+        hkv, g, s, d = int(ce["HKV"]), int(ce["G"]), int(ce["S"]), int(ce["D"])
+        q = spec.args[0]
+        nkv = q.numel // (g * d)
+        if nkv * g * d != q.numel or spec.args[1].numel != nkv * s * d:
+            raise UnsupportedKernel(f"{name}: q/k sizes do not match HKV={hkv}, G={g}, S={s}, D={d}")
+        return Plan("attention_decode", dict(nkv=nkv, group=g, seq=s, head_dim=d,
+                                             scale=float(ce.get("SCALE", 1.0 / math.sqrt(d))),
+                                             q=names[0], k=names[1], v=names[2], o=names[3]))
     if {"HQ", "G", "S", "D"} <= set(ce):
         q = spec.args[0]
         hq, g, s, d = int(ce["HQ"]), int(ce["G"]), int(ce["S"]), int(ce["D"])
         if "decode" in name:
-            raise UnsupportedKernel(f"{name}: decode attention is not on the HIP path yet")
+            raise UnsupportedKernel(f"{name}: decode attention with these constexprs is not on the HIP path")
         if len(spec.args) != 4:
             raise UnsupportedKernel(f"{name}: attention takes q, k, v, o")
         return Plan("attention", dict(batch=q.numel // (hq * s * d), hq=hq, hkv=hq // g, seq=s, head_dim=d,
@@ -173,10 +235,27 @@ def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
             if terms != {"x0": 1, "r0_1": n}:
                 raise UnsupportedKernel(f"{name}: the M = 1 template reads B as {terms}, not row-major [K, N]")
         if a.numel == k and b.numel == k * n and outs[0].numel == n:
-            return Plan("gemm", dict(m=1, k=k, n=n, residual=None, a=a.name, b=b.name, c=outs[0].name))
+            return Plan("gemv", dict(mode="plain", k=k, n=n, x=a.name, w=b.name, y=outs[0].name))
+    pure = [a for a in spec.args if a.role == "in"]
+    if ("pow" in name and "mean" in name and "mm" not in name and "rsqrt" not in name and len(outs) == 1
+            and outs[0].numel == 1 and outs[0].dtype == "float32" and 1 <= len(pure) <= 2
+            and all(a.dtype == "bfloat16" and a.numel == pure[0].numel for a in pure)):
+        return Plan("sumsq", dict(n=pure[0].numel, x=pure[0].name, y=pure[1].name if len(pure) == 2 else None,
+                                  out=outs[0].name))
+    gv = _gemv_plan(spec, source)
+    if gv is not None:
+        return gv
+    if len(ins) == 1 and len(outs) == 1 and outs[0].dtype == "float32" and "slice" in name:
+        # out[i] = float(x[first + i]) + c: the load offset and the constant from the source
+        first = int(hints.get("first", 0))
+        if source is not None:
+            m = re.search(r"tl\.load\(\s*" + re.escape(ins[0].name) + r"\s*\+\s*\(\s*(\d+)\s*\)\s*\)", source)
+            if not m:
+                raise UnsupportedKernel(f"{name}: the slice kernel does not load one fixed element")
+            first = int(m.group(1))
+        return Plan("slice_add", dict(first=first, count=outs[0].numel, s=_float_constant(source, 1.0), x=ins[0].name,
+                                      y=outs[0].name))
     if len(ins) == 1 and len(outs) == 1 and outs[0].numel == 1 and outs[0].dtype == "float32":
-        if "slice" in name:
-            raise UnsupportedKernel(f"{name}: the single-element slice kernel has no HIP family")
         if "_sum_" in name or name.endswith("sum"):
             return Plan("reduce", dict(op="sum", n=ins[0].numel, x=ins[0].name, y=outs[0].name))
         if "_max_" in name or name.endswith("max"):
@@ -186,8 +265,8 @@ def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
             x, w = ins
             return Plan("rmsnorm", dict(rows=x.numel // w.numel, cols=w.numel, eps=1e-6, x=x.name, w=w.name,
                                         y=outs[0].name))
-        if len(ins) == 4 and len(outs) == 1:
-            x, w, cs, sn = ins
+        if len(pure) == 4 and len(outs) == 1:
+            x, w, cs, sn = pure
             d = w.numel
             t = cs.numel // d
             return Plan("qk_norm_rope", dict(tokens=t, heads=x.numel // (t * d), head_dim=d, eps=1e-6, x=x.name,
@@ -224,6 +303,8 @@ def kernel_hints(plan: Plan) -> dict:
         return {k: plan.params[k] for k in ("d0", "d1", "inner")}
     if plan.family == "silu_mul":
         return {"inter": plan.params["inter"]}
+    if plan.family == "slice_add":
+        return {"first": plan.params["first"]}
     return {}
 
 
@@ -260,6 +341,25 @@ def run(plan: Plan, tensors: dict) -> None:
         ops.reduce(t[p["x"]], p["op"], out=t[p["y"]])
     elif f == "add_scalar":
         ops.add_scalar(t[p["x"]], p["s"], out=t[p["y"]])
+    elif f == "slice_add":
+        ops.slice_add(t[p["x"]], p["first"], p["count"], p["s"], out=t[p["y"]])
+    elif f == "attention_decode":
+        nkv, g, s, d = p["nkv"], p["group"], p["seq"], p["head_dim"]
+        ops.attention_decode(t[p["q"]].view(nkv, g, d), t[p["k"]].view(nkv, s, d), t[p["v"]].view(nkv, s, d),
+                             p["scale"], out=t[p["o"]].view(nkv, g, d))
+    elif f == "sumsq":
+        ops.sumsq(t[p["x"]], t[p["y"]] if p["y"] else None, out=t[p["out"]])
+    elif f == "gemv":
+        k, n = p["k"], p["n"]
+        w, y = t[p["w"]].view(k, n), t[p["y"]]
+        if p["mode"] == "plain":
+            ops.gemv(t[p["x"]], w, out=y)
+        elif p["mode"] == "rms":
+            ops.gemv_rmsnorm(t[p["x"]], t[p["ss"]], t[p["g"]], w, add=t[p["add"]] if p["add"] else None,
+                             eps=p["eps"], out=y)
+        else:
+            ops.gemv_silu(t[p["x"]], w, t[p["res_a"]] if p["res_a"] else None,
+                          t[p["res_b"]] if p["res_b"] else None, out=y)
     else:
         raise UnsupportedKernel(f"unknown family {f}")
 
@@ -303,4 +403,17 @@ def work_of(plan: Plan) -> tuple:
         return float(p["n"]), 2.0 * p["n"] + 4.0
     if f == "add_scalar":
         return float(p["n"]), 4.0 * p["n"]
+    if f == "slice_add":
+        return float(p["count"]), 6.0 * p["count"]
+    if f == "attention_decode":
+        rows, s, d = p["nkv"] * p["group"], p["seq"], p["head_dim"]
+        return 4.0 * rows * d * s, 2.0 * (2 * p["nkv"] * s * d + 2 * rows * d)
+    if f == "sumsq":
+        return (3.0 if p["y"] else 2.0) * p["n"], (4.0 if p["y"] else 2.0) * p["n"] + 4.0
+    if f == "gemv":
+        k, n = p["k"], p["n"]
+        xk = 2 * k if p["mode"] == "silu" else k
+        extra = {"plain": 0, "rms": 2 * k + 4 + (2 * k if p.get("add") else 0),
+                 "silu": 2 * n * ((1 if p.get("res_a") else 0) + (1 if p.get("res_b") else 0))}[p["mode"]]
+        return 2.0 * k * n, 2.0 * (k * n + xk + n) + extra
     raise UnsupportedKernel(f"unknown family {f}")

@@ -120,6 +120,16 @@ def add_scalar(x: torch.Tensor, s: float, out=None) -> torch.Tensor:
     return y
 
 
+def slice_add(x: torch.Tensor, first: int, count: int, s: float, out=None) -> torch.Tensor:
+    """out[i] = float(x.flat[first + i]) + s (fp32), i < count."""
+    _need(x, "x", BF16)
+    if first < 0 or count < 0 or first + count > x.numel():
+        raise ValueError(f"slice [{first}, {first + count}) is outside the {x.numel()} elements")
+    y = _out(out, (count,), F32, x)
+    _lib.call("ptb_slice_add_bf16", x.data_ptr(), y.data_ptr(), first, count, float(s), _stream(x))
+    return y
+
+
 def gemm(a: torch.Tensor, b: torch.Tensor, residual: torch.Tensor | None = None, out=None) -> torch.Tensor:
     """C = A[M,K] @ B[K,N] (+ residual[M,N]), bf16 operands, fp32 accumulation, bf16 C."""
     _need(a, "a", BF16, 2)

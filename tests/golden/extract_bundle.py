@@ -30,6 +30,11 @@ WORKLOADS = [
     "gemm_1x768x768_bf16",
     "gemm_512x768x768_bf16",
     "gemm_4096x4096x4096_bf16",
+    "qwen3_8b_layer_decode_1x4096_bf16",
+    "qwen3_8b_layer_decode_1x128_bf16",
+    "attention_decode_32x8x4096_bf16",
+    "attention_decode_24x8x1024_bf16",
+    "vector_slice_8x128_bf16",
 ]
 
 

@@ -75,6 +75,32 @@ def check_against_oracle(plan, host, got):
             assert abs(float(got[p["y"]]) - float(oracle.reduce_sum(x))) <= bound
     elif f == "add_scalar":
         assert bits_equal(got[p["y"]], oracle.add_scalar(host[p["x"]], p["s"]))
+    elif f == "slice_add":
+        assert torch.equal(got[p["y"]], oracle.slice_add(host[p["x"]], p["first"], p["count"], p["s"]))
+    elif f == "sumsq":
+        x = host[p["x"]]
+        y = host[p["y"]] if p["y"] else None
+        terms = (x.float() + (0 if y is None else y.float())).double().pow(2).sum()
+        assert abs(float(got[p["out"]]) - float(oracle.sumsq(x, y))) <= 1e-6 * float(terms) + 1e-6
+    elif f == "attention_decode":
+        nkv, g, s, d = p["nkv"], p["group"], p["seq"], p["head_dim"]
+        want = oracle.attention_decode(host[p["q"]].view(nkv, g, d), host[p["k"]].view(nkv, s, d),
+                                       host[p["v"]].view(nkv, s, d), p["scale"])
+        assert_close(got[p["o"]].view(nkv, g, d), want, 2e-2, 2e-2, "attention_decode")
+    elif f == "gemv":
+        k, n = p["k"], p["n"]
+        w = host[p["w"]].view(k, n)
+        if p["mode"] == "plain":
+            want = oracle.gemv(host[p["x"]], w)
+        elif p["mode"] == "rms":
+            want = oracle.gemv_rmsnorm(host[p["x"]], host[p["ss"]], host[p["g"]], w,
+                                       add=host[p["add"]] if p["add"] else None, eps=p["eps"])
+        else:
+            want = oracle.gemv_silu(host[p["x"]], w, host[p["res_a"]] if p["res_a"] else None,
+                                    host[p["res_b"]] if p["res_b"] else None)
+        finite = want.float().isfinite()
+        scale = float(want.float()[finite].abs().mean()) + 1e-6 if bool(finite.any()) else 1.0
+        assert_close(got[p["y"]], want, 2e-2, 2e-2 * scale, f"gemv {p['mode']}")
     else:
         raise AssertionError(f"no oracle for {f}")
 
@@ -179,3 +205,47 @@ def test_qwen3_layer_from_bundle_manifests_matches_composed_oracle():
     rms = float(want.float().pow(2).mean().sqrt())
     assert_close(y.cpu().view(t, hidden), want, 2e-2, 2e-2 * max(1.0, rms), "qwen3 layer from manifests")
     assert math.isfinite(rms)
+
+
+def test_qwen3_decode_layer_from_bundle_manifests_matches_composed_oracle():
+    """The 8 launches of qwen3_8b_layer_decode_1x128_bf16 chained the way the decode layer's data
+    flows (K00 -> K01 -> K02 -> K03 over the cache -> K04 -> K05 -> K06 -> K07), against the
+    oracle's decode layer on the same weights and cache."""
+    w = MANIFESTS["qwen3_8b_layer_decode_1x128_bf16"]
+    specs = {m["dir"][:2]: contract.spec_from_manifest(m) for m in w["kernels"]}
+    s, hidden, hq, hkv, d, inter = 128, 4096, 32, 8, 128, 12288
+    g = torch.Generator().manual_seed(6)
+
+    def rnd(*shape, std=0.02, mean=0.0):
+        return (torch.randn(*shape, generator=g) * std + mean).to(torch.bfloat16)
+
+    x = rnd(hidden, std=1.0)
+    wts = {"w_in": rnd(hidden, mean=1.0), "wq": rnd(hidden, hq * d), "w_qn": rnd(d, mean=1.0), "wo": rnd(hq * d, hidden),
+           "w_post": rnd(hidden, mean=1.0), "wgu": rnd(hidden, 2 * inter), "wd": rnd(inter, hidden)}
+    kc, vc = rnd(hkv, s, d, std=1.0), rnd(hkv, s, d, std=1.0)
+    cos_t, sin_t = oracle.rope_tables(s + 1, d, 1.0e6)
+    cos, sin = cos_t[s].contiguous(), sin_t[s].contiguous()
+    cu = {k: v.cuda().reshape(-1) for k, v in wts.items()}
+
+    def run(key, **named):
+        spec = specs[key]
+        tens = {}
+        for a in spec.args:
+            tens[a.name] = named[a.name] if a.name in named else torch.empty(
+                a.numel, dtype=getattr(torch, a.dtype), device="cuda")
+        launcher.launch(spec, tens)
+        return tens[spec.outputs()[0].name]
+
+    xc = x.cuda()
+    ss = run("00", in_ptr0=xc)
+    q = run("01", in_ptr0=xc, in_ptr1=ss, in_ptr2=cu["w_in"], in_ptr3=cu["wq"])
+    qh = run("02", in_ptr0=q, in_ptr1=cu["w_qn"], in_ptr2=cos.cuda(), in_ptr3=sin.cuda())
+    o = run("03", q_ptr=qh, k_ptr=kc.cuda().reshape(-1), v_ptr=vc.cuda().reshape(-1))
+    a = run("04", in_ptr0=o, in_ptr1=cu["wo"])
+    ss2 = run("05", in_ptr0=xc, in_ptr1=a)
+    gu = run("06", in_ptr0=xc, in_ptr1=a, in_ptr2=ss2, in_ptr3=cu["w_post"], in_ptr4=cu["wgu"])
+    y = run("07", in_ptr0=gu, in_ptr1=cu["wd"], in_ptr2=xc, in_ptr3=a)
+    torch.cuda.synchronize()
+    want = oracle.qwen3_decode_layer(x, wts, kc, vc, cos, sin, hq, hkv, d, 1e-6)
+    rms = float(want.float().pow(2).mean().sqrt())
+    assert_close(y.cpu(), want, 2e-2, 2e-2 * max(1.0, rms), "qwen3 decode layer from manifests")
