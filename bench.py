@@ -6,8 +6,10 @@ B[4096,12288], fp32 accumulation, bf16 C (Qwen3-8B gate/up projection shape) -- 
 launches over inputs resident in HBM, bracketed by torch.cuda.synchronize().  ``value`` is TFLOP/s
 (2*M*N*K flops per step).  The same JSON line carries, under ``kernels``, each other BASELINE config
 measured the same way (RMSNorm GB/s, fp8 GEMM TFLOP/s, flash-attention TFLOP/s, Qwen3-8B layer
-latency), each with its roofline fraction, and ``cpu_baseline`` times the CPU golden (torch-CPU,
-the oracle's arithmetic) on a bounded sample of the headline workload.
+latency) and the single-token decode path (the decode layer's largest GEMV and the decode attention
+in GB/s, the 8-launch decode layer's latency), each with its roofline fraction, and
+``cpu_baseline`` times the CPU golden (torch-CPU, the oracle's arithmetic) on a bounded sample of
+the headline workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm_bf16,...]
 """
@@ -173,6 +175,94 @@ def bench_layer(steps, warmup):
             "launches": len(work)}
 
 
+def bench_gemv(steps, warmup):
+    """The decode layer's largest GEMV (K06 of qwen3_8b_layer_decode_1x<S>_bf16): the post-attention
+    RMSNorm folded into gu = ((x + a) * r * w_post) Wgu, W [4096, 24576] bf16 streamed once."""
+    import torch
+    from ptb_amd import ops
+
+    k, n = 4096, 24576
+    g = torch.Generator().manual_seed(0)
+    copies = 3   # 3 x 201 MB cycles through more than the 256 MB last-level cache
+    ws = [(torch.randn(k, n, generator=g) * 0.02).to(torch.bfloat16).cuda() for _ in range(copies)]
+    x = torch.randn(k, generator=g).to(torch.bfloat16).cuda()
+    a = torch.randn(k, generator=g).to(torch.bfloat16).cuda()
+    gw = (torch.randn(k, generator=g) * 0.02 + 1).to(torch.bfloat16).cuda()
+    ss = ops.sumsq(x, a)
+    y = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    from ptb_amd import _lib
+    work = torch.empty(_lib.load().ptb_gemv_workspace_bytes(k, n), dtype=torch.uint8, device="cuda")
+    it = [0]
+
+    def step():
+        i = it[0] % copies
+        it[0] += 1
+        ops.gemv_rmsnorm(x, ss, gw, ws[i], add=a, out=y, workspace=work)
+
+    ms, wall = timed(step, steps * 4, warmup)
+    nbytes = 2.0 * (k * n + 3 * k + n) + 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"name": "gemv_decode", "config": "decode K06: ((x+a)*rsqrt(ss/4096+eps)*w) @ Wgu[4096x24576], bf16",
+            "us": ms * 1e3, "wall_us": wall * 1e3, "gbs": gbs,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS}}
+
+
+def bench_attention_decode(steps, warmup):
+    """attention_decode_32x8x4096_bf16: one token, 32 query heads over an [8, 4096, 128] K/V cache."""
+    import torch
+    from ptb_amd import ops
+
+    hkv, g, s, d = 8, 4, 4096, 128
+    gen = torch.Generator().manual_seed(0)
+    copies = 12   # 12 x 16.8 MB of K/V: past the last-level cache
+    kvs = [(torch.randn(hkv, s, d, generator=gen).to(torch.bfloat16).cuda(),
+            torch.randn(hkv, s, d, generator=gen).to(torch.bfloat16).cuda()) for _ in range(copies)]
+    q = torch.randn(hkv, g, d, generator=gen).to(torch.bfloat16).cuda()
+    o = torch.empty_like(q)
+    from ptb_amd import _lib
+    work = torch.empty(_lib.load().ptb_attn_decode_workspace_bytes(hkv, g, s), dtype=torch.uint8, device="cuda")
+    it = [0]
+
+    def step():
+        k, v = kvs[it[0] % copies]
+        it[0] += 1
+        ops.attention_decode(q, k, v, out=o, workspace=work)
+
+    ms, wall = timed(step, steps * 4, warmup)
+    nbytes = 2.0 * (2 * hkv * s * d + 2 * hkv * g * d)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"name": "attention_decode", "config": "attention_decode_32x8x4096_bf16: 1 token, 32/8 heads, S 4096",
+            "us": ms * 1e3, "wall_us": wall * 1e3, "gbs": gbs,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS}}
+
+
+def bench_decode_layer(steps, warmup):
+    """qwen3_8b_layer_decode_1x4096_bf16: the 8-launch decode layer over a 4096-token cache."""
+    import torch
+    from ptb_amd import qwen3
+
+    layer = qwen3.Qwen3DecodeLayer(qwen3.random_weights(device="cuda"))
+    g = torch.Generator().manual_seed(1)
+    s = 4096
+    x = torch.randn(4096, generator=g).to(torch.bfloat16).cuda()
+    kc = torch.randn(8, s, 128, generator=g).to(torch.bfloat16).cuda()
+    vc = torch.randn(8, s, 128, generator=g).to(torch.bfloat16).cuda()
+    cos_t, sin_t = qwen3.rope_tables(s + 1, 128, 1.0e6, "cuda")
+    cos, sin = cos_t[s].contiguous(), sin_t[s].contiguous()
+    y = torch.empty_like(x)
+    ms, wall = timed(lambda: layer.forward(x, kc, vc, cos, sin, out=y), steps, warmup)
+    # bytes the layer must move: every weight once plus the K/V cache
+    nbytes = 2.0 * (4096 * 4096 * 2 + 4096 * 24576 + 12288 * 4096) + 2.0 * 2 * 8 * s * 128
+    roof_us = nbytes / (PEAK_HBM_GBS * 1e9) * 1e6
+    return {"name": "qwen3_8b_decode_layer", "config": "qwen3_8b_layer_decode_1x4096_bf16: 1 token, cache 4096",
+            "us": ms * 1e3, "wall_us": wall * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
+            "roofline": {"bound": "hbm", "roofline_us": roof_us, "measured_us": ms * 1e3, "unit": "us",
+                         "frac": roof_us / (ms * 1e3)},
+            "launches": 8}
+
+
 def cpu_baseline_gemm(a, b, sample_rows=256):
     """The CPU golden for the headline workload: torch-CPU fp32 matmul of the oracle's arithmetic
     (bf16 operands upcast, fp32 accumulation, one bf16 rounding), on `sample_rows` rows of A against
@@ -256,6 +346,9 @@ BENCHES = {
     "gemm_fp8": bench_gemm_fp8,
     "flash_attention": bench_attention,
     "qwen3_8b_layer": bench_layer,
+    "gemv_decode": bench_gemv,
+    "attention_decode": bench_attention_decode,
+    "qwen3_8b_decode_layer": bench_decode_layer,
 }
 
 

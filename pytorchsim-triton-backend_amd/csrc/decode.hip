@@ -11,7 +11,7 @@
 //           meet in LDS and the slice's fp32 partials go to the workspace [splits, N].
 //   pass 2: y[n] = bf16(sum over splits (+ r1[n] + r2[n])), one rounding.
 // Decode attention (one query token, G query heads per kv head, S cached keys, D = 128):
-//   pass 1: workgroup (128-key chunk, kv head): scores t = (q.k) * scale*log2(e) with 16 lanes per
+//   pass 1: workgroup (64-key chunk, kv head): scores t = (q.k) * scale*log2(e) with 16 lanes per
 //           key (one 256-byte row), the chunk's softmax in base 2 (m = chunk max, p = 2^(t-m),
 //           l = sum of fp32 p), acc = sum bf16(p) * v; (m, l, acc) to the workspace.
 //   pass 2: merge the chunks of a kv head: m = max m_c, o = sum acc_c 2^(m_c-m) / sum l_c 2^(m_c-m).
@@ -156,15 +156,33 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __r
   }
 }
 
+// 16 columns a workgroup, 16 split groups of 16 lanes: each lane sums every 16th split with its
+// loads independent (the partials come from L2 or another XCD: latency, not bandwidth, bounds this)
+constexpr int kFinCols = 16;
 __global__ __launch_bounds__(256) void gemv_finish(const float* __restrict__ part, int splits, int N,
                                                    const uint16_t* __restrict__ r1, const uint16_t* __restrict__ r2,
                                                    uint16_t* __restrict__ y) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= N) return;
-  float s = 0.f;
-  for (int sp = 0; sp < splits; ++sp) s += part[int64_t(sp) * N + n];
-  if (r1) s += bf16_to_f32(r1[n]) + (r2 ? bf16_to_f32(r2[n]) : 0.f);
-  y[n] = f32_to_bf16(s);
+  __shared__ float red[16][kFinCols];
+  const int c = threadIdx.x % kFinCols, sg = threadIdx.x / kFinCols;
+  const int n = blockIdx.x * kFinCols + c;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (n < N) {
+    int sp = sg;
+    for (; sp + 48 < splits; sp += 64) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] += part[int64_t(sp + 16 * u) * N + n];
+    }
+    for (; sp < splits; sp += 16) acc[0] += part[int64_t(sp) * N + n];
+  }
+  red[sg][c] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+  if (sg == 0 && n < N) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += red[i][c];
+    if (r1) s += bf16_to_f32(r1[n]) + (r2 ? bf16_to_f32(r2[n]) : 0.f);
+    y[n] = f32_to_bf16(s);
+  }
 }
 
 template <int MODE>
@@ -188,7 +206,7 @@ int launch_gemv(const void* x, const void* add, const float* ss, const void* g, 
   gemv_partial<MODE><<<grid1, dim3(kGemvThreads), 0, s>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(add), ss, static_cast<const uint16_t*>(g), eps,
       static_cast<const uint16_t*>(w), part, int(k), int(n), sp.kb);
-  gemv_finish<<<dim3(unsigned((n + 255) / 256)), dim3(256), 0, s>>>(
+  gemv_finish<<<dim3(unsigned((n + kFinCols - 1) / kFinCols)), dim3(256), 0, s>>>(
       part, sp.splits, int(n), static_cast<const uint16_t*>(r1), static_cast<const uint16_t*>(r2),
       static_cast<uint16_t*>(y));
   return launch_status();
@@ -198,7 +216,7 @@ int launch_gemv(const void* x, const void* add, const float* ss, const void* g, 
 // decode attention
 
 constexpr int kD = 128;
-constexpr int kChunk = 128;      // keys per workgroup
+constexpr int kChunk = 64;       // keys per workgroup
 constexpr int kAttnThreads = 256;
 
 // workspace per (kv head, chunk): m[G], l[G], acc[G][128]
@@ -220,18 +238,30 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial(const uint16
   for (int i = tid; i < G * kD; i += kAttnThreads) qs[i / kD][i % kD] = bf16_to_f32(q[i]);
   __syncthreads();
 
+  // every K and V load of the chunk goes out first (16 x 16 bytes a lane, 64 KB a workgroup in
+  // flight): the kernel is bound by HBM latency x bandwidth, not by its few FMAs
   // scores: 16 lanes per key (8 dims each), 4 keys per wave, 16 keys per pass
   const int d8 = lane & 15;
-#pragma unroll 2
+  const int kj = tid >> 4;   // PV: 16 lanes per key, key kj of each pass
+  u32x4 kreg[kChunk / 16], vreg[kChunk / 16];
+#pragma unroll
+  for (int pass = 0; pass < kChunk / 16; ++pass) {
+    const int key = min(key0 + pass * 16 + wave * 4 + (lane >> 4), S - 1);
+    kreg[pass] = *reinterpret_cast<const u32x4*>(kp + int64_t(key) * kD + 8 * d8);
+  }
+#pragma unroll
+  for (int pass = 0; pass < kChunk / 16; ++pass) {
+    const int key = min(key0 + pass * 16 + kj, S - 1);
+    vreg[pass] = *reinterpret_cast<const u32x4*>(vp + int64_t(key) * kD + 8 * d8);
+  }
+#pragma unroll
   for (int pass = 0; pass < kChunk / 16; ++pass) {
     const int j = pass * 16 + wave * 4 + (lane >> 4);
-    const int key = min(key0 + j, S - 1);
-    const u32x4 kv = *reinterpret_cast<const u32x4*>(kp + int64_t(key) * kD + 8 * d8);
     float kf[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      kf[2 * e] = bf16_lo(kv[e]);
-      kf[2 * e + 1] = bf16_hi(kv[e]);
+      kf[2 * e] = bf16_lo(kreg[pass][e]);
+      kf[2 * e + 1] = bf16_hi(kreg[pass][e]);
     }
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
@@ -275,17 +305,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial(const uint16
   for (int gi = 0; gi < G; ++gi)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[gi][e] = 0.f;
-  const int kj = tid >> 4;   // 0..15
-#pragma unroll 2
+#pragma unroll
   for (int pass = 0; pass < kChunk / 16; ++pass) {
     const int j = pass * 16 + kj;
-    const int key = min(key0 + j, S - 1);
-    const u32x4 vv = *reinterpret_cast<const u32x4*>(vp + int64_t(key) * kD + 8 * d8);
     float vf[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      vf[2 * e] = bf16_lo(vv[e]);
-      vf[2 * e + 1] = bf16_hi(vv[e]);
+      vf[2 * e] = bf16_lo(vreg[pass][e]);
+      vf[2 * e + 1] = bf16_hi(vreg[pass][e]);
     }
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
@@ -322,21 +349,41 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial(const uint16
   }
 }
 
+// One workgroup per (kv head, query head): the chunk maxima reduce across the workgroup first,
+// then each lane (one of the 128 dims) sums the chunks with independent loads.
 template <int G>
 __global__ __launch_bounds__(kD) void attn_decode_combine(const float* __restrict__ ws, uint16_t* __restrict__ O,
                                                           int nchunks) {
+  __shared__ float red[2];
   const int kvh = blockIdx.x, gi = blockIdx.y, d = threadIdx.x;
   const float* base = ws + int64_t(kvh) * nchunks * (G * (kD + 2));
+  constexpr int stride = G * (kD + 2);
   float m = -INFINITY;
-  for (int ch = 0; ch < nchunks; ++ch) m = fmaxf(m, base[int64_t(ch) * G * (kD + 2) + gi]);
-  float l = 0.f, o = 0.f;
-  for (int ch = 0; ch < nchunks; ++ch) {
-    const float* p = base + int64_t(ch) * G * (kD + 2);
-    const float w = __builtin_amdgcn_exp2f(p[gi] - m);
-    l = __builtin_fmaf(p[G + gi], w, l);
-    o = __builtin_fmaf(p[2 * G + gi * kD + d], w, o);
+  for (int ch = d; ch < nchunks; ch += kD) m = fmaxf(m, base[int64_t(ch) * stride + gi]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+  if ((d & 63) == 0) red[d >> 6] = m;
+  __syncthreads();
+  m = fmaxf(red[0], red[1]);
+  float l[4] = {0.f, 0.f, 0.f, 0.f}, o[4] = {0.f, 0.f, 0.f, 0.f};
+  int ch = 0;
+  for (; ch + 3 < nchunks; ch += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* p = base + int64_t(ch + u) * stride;
+      const float w = __builtin_amdgcn_exp2f(p[gi] - m);
+      l[u] = __builtin_fmaf(p[G + gi], w, l[u]);
+      o[u] = __builtin_fmaf(p[2 * G + gi * kD + d], w, o[u]);
+    }
   }
-  O[(int64_t(kvh) * G + gi) * kD + d] = f32_to_bf16(o / l);
+  for (; ch < nchunks; ++ch) {
+    const float* p = base + int64_t(ch) * stride;
+    const float w = __builtin_amdgcn_exp2f(p[gi] - m);
+    l[0] = __builtin_fmaf(p[G + gi], w, l[0]);
+    o[0] = __builtin_fmaf(p[2 * G + gi * kD + d], w, o[0]);
+  }
+  const float lt = (l[0] + l[1]) + (l[2] + l[3]), ot = (o[0] + o[1]) + (o[2] + o[3]);
+  O[(int64_t(kvh) * G + gi) * kD + d] = f32_to_bf16(ot / lt);
 }
 
 template <int G>
