@@ -318,6 +318,24 @@ def pmc_driver(which: str) -> None:
         w = (torch.randn(4096, generator=g) * 0.02 + 1).cuda()
         y = torch.empty_like(x)
         run = lambda: ops.rmsnorm(x, w, 1e-6, out=y)  # noqa: E731
+    elif which == "gemv_decode":
+        from ptb_amd import _lib
+        wg = (torch.randn(4096, 24576, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        x = torch.randn(4096, generator=g).to(torch.bfloat16).cuda()
+        a = torch.randn(4096, generator=g).to(torch.bfloat16).cuda()
+        gw = (torch.randn(4096, generator=g) * 0.02 + 1).to(torch.bfloat16).cuda()
+        ss = ops.sumsq(x, a)
+        y = torch.empty(24576, dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(_lib.load().ptb_gemv_workspace_bytes(4096, 24576), dtype=torch.uint8, device="cuda")
+        run = lambda: ops.gemv_rmsnorm(x, ss, gw, wg, add=a, out=y, workspace=ws)  # noqa: E731
+    elif which == "attention_decode":
+        from ptb_amd import _lib
+        q = torch.randn(8, 4, 128, generator=g).to(torch.bfloat16).cuda()
+        k = torch.randn(8, 4096, 128, generator=g).to(torch.bfloat16).cuda()
+        v = torch.randn(8, 4096, 128, generator=g).to(torch.bfloat16).cuda()
+        o = torch.empty_like(q)
+        ws = torch.empty(_lib.load().ptb_attn_decode_workspace_bytes(8, 4, 4096), dtype=torch.uint8, device="cuda")
+        run = lambda: ops.attention_decode(q, k, v, out=o, workspace=ws)  # noqa: E731
     else:
         raise SystemExit(f"unknown --pmc-driver {which}")
     for _ in range(5):
