@@ -279,7 +279,7 @@ def cpu_baseline_gemm(a, b, sample_rows=256):
     while True:
         (a_s @ b_f).to(torch.bfloat16)
         reps += 1
-        if time.perf_counter() - t0 > 10.0 or reps >= 50:
+        if time.perf_counter() - t0 > 10.0:   # a bounded sample: about 10 s of CPU work
             break
     sec = (time.perf_counter() - t0) / reps
     flops = 2.0 * sample_rows * b.shape[0] * b.shape[1]
