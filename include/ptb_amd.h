@@ -59,6 +59,12 @@ int ptb_rmsnorm_bf16(const void* x, const void* w, int w_dtype, void* y, int64_t
  * Replaces: validation/pytorchsim/vector_softmax_2048x6144_bf16/00_..._sa7wwqqf/..._triton.py:17-68 */
 int ptb_softmax_rows_bf16(const void* x, void* y, int64_t rows, int64_t cols, void* stream);
 
+/* The same row softmax with the probabilities stored as fp32 (no rounding): the MoE router's
+ * softmax over expert logits.
+ * Replaces: validation/pytorchsim/layer_layer_decode_1x1024_bf16/16_..._qslpdpud/
+ *           pytorchsim_triton_compiler_fused__softmax__to_copy_qslpdpud_triton.py:17-45 */
+int ptb_softmax_rows_bf16_f32(const void* x, void* y, int64_t rows, int64_t cols, void* stream);
+
 /* SiLU gate: out[t,j] = bf16( (g / (1 + exp(-g))) * u ), g = gu[t, j], u = gu[t, inter + j].
  * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/10_..._ktzl5s2h/..._triton.py:17-36 */
 int ptb_silu_mul_bf16(const void* gate_up, void* out, int64_t rows, int64_t inter, void* stream);
@@ -85,6 +91,12 @@ int ptb_qk_norm_rope_bf16(const void* x, const void* w, const float* cos_t, cons
 size_t ptb_reduce_workspace_bytes(int64_t n);
 int ptb_reduce_bf16(const void* x, float* out, int64_t n, int op, void* workspace,
                     size_t workspace_bytes, void* stream);
+/* The same reduction over fp32 elements (16-byte aligned).
+ * Replaces: validation/pytorchsim/layer_layer_decode_1x1024_bf16/18_..._7gslrk5a/
+ *           pytorchsim_triton_compiler_fused_sum_7gslrk5a_triton.py:17-38 (the MoE router's sum of
+ *           its top-k weights). */
+int ptb_reduce_f32(const float* x, float* out, int64_t n, int op, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 /* y = bf16(float(x) + s) elementwise.  Replaces vector_add1_<R>x<C>_bf16/00_..._du5rd5jd_triton.py. */
 int ptb_add_scalar_bf16(const void* x, void* y, int64_t n, float s, void* stream);

@@ -38,14 +38,16 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor
     return ((xf * r) * w.float()).to(BF16)
 
 
-def softmax_rows(x: torch.Tensor) -> torch.Tensor:
+def softmax_rows(x: torch.Tensor, out_dtype=BF16) -> torch.Tensor:
     """vector_softmax_2048x6144_bf16/00_..._sa7wwqqf_triton.py:17-68: NaN-propagating row max
     (tl.maximum(..., PropagateNan.ALL), :30-33), sum of exp(x - max) (:35-47), exp(x - max) / sum
-    stored as bf16 (:49-68)."""
+    stored as bf16 (:49-68).  out_dtype fp32: the MoE router's softmax, stored unrounded
+    (layer_layer_decode_1x1024_bf16/16_..._qslpdpud_triton.py:31-45; its max2 does not propagate NaN,
+    which only differs for rows holding a NaN)."""
     xf = x.float()
     m = torch.amax(xf, dim=-1, keepdim=True)  # amax propagates NaN
     e = torch.exp(xf - m)
-    return (e / e.sum(dim=-1, keepdim=True)).to(BF16)
+    return (e / e.sum(dim=-1, keepdim=True)).to(out_dtype)
 
 
 def silu_mul(gu: torch.Tensor) -> torch.Tensor:

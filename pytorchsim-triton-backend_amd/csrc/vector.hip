@@ -120,9 +120,21 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_long(const uint16_t* __re
 }
 
 // ---------------------------------------------------------------- softmax
-template <int TPR, int VPT>
+// Eight results of chunk c of a row: one bf16 rounding each (OutT = uint16_t) or fp32 as computed.
+template <typename OutT>
+__device__ __forceinline__ void store8(OutT* __restrict__ yrow, int c, const float (&f)[8]) {
+  if constexpr (sizeof(OutT) == 2) {
+    reinterpret_cast<u32x4*>(yrow)[c] = pack8(f);
+  } else {
+    f32x4v* p = reinterpret_cast<f32x4v*>(yrow) + 2 * c;
+    p[0] = f32x4v{f[0], f[1], f[2], f[3]};
+    p[1] = f32x4v{f[4], f[5], f[6], f[7]};
+  }
+}
+
+template <int TPR, int VPT, typename OutT>
 __global__ __launch_bounds__(kBlock) void softmax_rows(const uint16_t* __restrict__ x,
-                                                       uint16_t* __restrict__ y, int64_t rows, int cols) {
+                                                       OutT* __restrict__ y, int64_t rows, int cols) {
   __shared__ float red[kBlock / kWave];
   constexpr int kTeams = kBlock / TPR;
   const int team = threadIdx.x / TPR, lt = threadIdx.x % TPR;
@@ -158,7 +170,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows(const uint16_t* __restric
   }
   s = team_sum<TPR>(s, red);
   if (!live) return;
-  u32x4* yr = reinterpret_cast<u32x4*>(y + row * int64_t(cols));
+  OutT* yr = y + row * int64_t(cols);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = lt + i * TPR;
@@ -167,12 +179,13 @@ __global__ __launch_bounds__(kBlock) void softmax_rows(const uint16_t* __restric
     unpack8(v[i], f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = exp_e(f[e] - mx) / s;
-    yr[c] = pack8(f);
+    store8(yr, c, f);
   }
 }
 
+template <typename OutT>
 __global__ __launch_bounds__(kBlock) void softmax_rows_long(const uint16_t* __restrict__ x,
-                                                            uint16_t* __restrict__ y, int cols) {
+                                                            OutT* __restrict__ y, int cols) {
   __shared__ float red[kBlock / kWave];
   const int64_t row = blockIdx.x;
   const int chunks = cols >> 3;
@@ -193,13 +206,13 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_long(const uint16_t* __re
     for (int e = 0; e < 8; ++e) s += exp_e(f[e] - mx);
   }
   s = block_sum<kBlock / kWave>(s, red);
-  u32x4* yr = reinterpret_cast<u32x4*>(y + row * int64_t(cols));
+  OutT* yr = y + row * int64_t(cols);
   for (int c = threadIdx.x; c < chunks; c += kBlock) {
     float f[8];
     unpack8(xr[c], f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = exp_e(f[e] - mx) / s;
-    yr[c] = pack8(f);
+    store8(yr, c, f);
   }
 }
 
@@ -309,8 +322,20 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope(const uint16_t* __restric
 
 // ---------------------------------------------------------------- whole-tensor sum / max
 constexpr int kReduceBlocks = 1024;
-template <int OP>
-__global__ __launch_bounds__(kBlock) void reduce_partial(const uint16_t* __restrict__ x, int64_t n,
+// Eight consecutive elements (chunk c) as fp32: one 16-byte load of bf16, two of fp32.
+__device__ __forceinline__ void load8(const uint16_t* __restrict__ x, int64_t c, float (&f)[8]) {
+  unpack8(reinterpret_cast<const u32x4*>(x)[c], f);
+}
+__device__ __forceinline__ void load8(const float* __restrict__ x, int64_t c, float (&f)[8]) {
+  const f32x4v* p = reinterpret_cast<const f32x4v*>(x) + 2 * c;
+  const f32x4v a = p[0], b = p[1];
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ __forceinline__ float as_f32(uint16_t v) { return bf16_to_f32(v); }
+__device__ __forceinline__ float as_f32(float v) { return v; }
+
+template <int OP, typename InT>
+__global__ __launch_bounds__(kBlock) void reduce_partial(const InT* __restrict__ x, int64_t n,
                                                          float* __restrict__ part) {
   __shared__ float red[kBlock / kWave];
   const int64_t chunks = n >> 3;
@@ -318,13 +343,13 @@ __global__ __launch_bounds__(kBlock) void reduce_partial(const uint16_t* __restr
   float acc = OP == PTB_REDUCE_SUM ? 0.f : -INFINITY;
   for (int64_t c = int64_t(blockIdx.x) * kBlock + threadIdx.x; c < chunks; c += stride) {
     float f[8];
-    unpack8(reinterpret_cast<const u32x4*>(x)[c], f);
+    load8(x, c, f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc = OP == PTB_REDUCE_SUM ? acc + f[e] : max_nan(acc, f[e]);
   }
   if (blockIdx.x == 0) {
     for (int64_t i = (chunks << 3) + threadIdx.x; i < n; i += kBlock) {
-      const float f = bf16_to_f32(x[i]);
+      const float f = as_f32(x[i]);
       acc = OP == PTB_REDUCE_SUM ? acc + f : max_nan(acc, f);
     }
   }
@@ -420,7 +445,10 @@ PTB_EXPORT int ptb_rmsnorm_bf16(const void* x, const void* w, int w_dtype, void*
   return launch_status();
 }
 
-PTB_EXPORT int ptb_softmax_rows_bf16(const void* x, void* y, int64_t rows, int64_t cols, void* stream) {
+namespace {
+
+template <typename OutT>
+int softmax_launch(const void* x, void* y, int64_t rows, int64_t cols, void* stream) {
   if (rows < 0 || cols <= 0 || cols > (int64_t(1) << 30)) return PTB_ERR_SHAPE;
   if (rows == 0) return PTB_OK;
   if (!x || !y) return PTB_ERR_NULL;
@@ -428,7 +456,7 @@ PTB_EXPORT int ptb_softmax_rows_bf16(const void* x, void* y, int64_t rows, int64
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int c = int(cols);
   const uint16_t* xi = static_cast<const uint16_t*>(x);
-  uint16_t* yo = static_cast<uint16_t*>(y);
+  OutT* yo = static_cast<OutT*>(y);
   int tpr, vpt;
   if (row_shape(c, &tpr, &vpt)) {
     const int teams = kBlock / tpr;
@@ -436,15 +464,25 @@ PTB_EXPORT int ptb_softmax_rows_bf16(const void* x, void* y, int64_t rows, int64
     if (blocks > 0x7fffffff) return PTB_ERR_GRID;
 #define SM_CASE(T, V)                                                                                 \
   if (tpr == T && vpt == V) {                                                                         \
-    softmax_rows<T, V><<<dim3(unsigned(blocks)), dim3(kBlock), 0, s>>>(xi, yo, rows, c);            \
+    softmax_rows<T, V, OutT><<<dim3(unsigned(blocks)), dim3(kBlock), 0, s>>>(xi, yo, rows, c);      \
     return launch_status();                                                                           \
   }
     SM_CASE(64, 1) SM_CASE(64, 2) SM_CASE(64, 4) SM_CASE(256, 2) SM_CASE(256, 4) SM_CASE(256, 8)
 #undef SM_CASE
   }
   if (rows > 0x7fffffff) return PTB_ERR_GRID;
-  softmax_rows_long<<<dim3(unsigned(rows)), dim3(kBlock), 0, s>>>(xi, yo, c);
+  softmax_rows_long<OutT><<<dim3(unsigned(rows)), dim3(kBlock), 0, s>>>(xi, yo, c);
   return launch_status();
+}
+
+}  // namespace
+
+PTB_EXPORT int ptb_softmax_rows_bf16(const void* x, void* y, int64_t rows, int64_t cols, void* stream) {
+  return softmax_launch<uint16_t>(x, y, rows, cols, stream);
+}
+
+PTB_EXPORT int ptb_softmax_rows_bf16_f32(const void* x, void* y, int64_t rows, int64_t cols, void* stream) {
+  return softmax_launch<float>(x, y, rows, cols, stream);
 }
 
 PTB_EXPORT int ptb_silu_mul_bf16(const void* gate_up, void* out, int64_t rows, int64_t inter, void* stream) {
@@ -496,8 +534,11 @@ PTB_EXPORT size_t ptb_reduce_workspace_bytes(int64_t n) {
   return kReduceBlocks * sizeof(float);
 }
 
-PTB_EXPORT int ptb_reduce_bf16(const void* x, float* out, int64_t n, int op, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+namespace {
+
+template <typename InT>
+int reduce_launch(const InT* x, float* out, int64_t n, int op, void* workspace, size_t workspace_bytes,
+                  void* stream) {
   if (!x || !out || !workspace) return PTB_ERR_NULL;
   if (n < 0) return PTB_ERR_SHAPE;
   if (op != PTB_REDUCE_SUM && op != PTB_REDUCE_MAX) return PTB_ERR_DTYPE;
@@ -506,15 +547,26 @@ PTB_EXPORT int ptb_reduce_bf16(const void* x, float* out, int64_t n, int op, voi
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int g = grid_for(n / 8, int64_t(kBlock) * 8, kReduceBlocks);
   float* part = static_cast<float*>(workspace);
-  const uint16_t* xi = static_cast<const uint16_t*>(x);
   if (op == PTB_REDUCE_SUM) {
-    reduce_partial<PTB_REDUCE_SUM><<<dim3(g), dim3(kBlock), 0, s>>>(xi, n, part);
+    reduce_partial<PTB_REDUCE_SUM, InT><<<dim3(g), dim3(kBlock), 0, s>>>(x, n, part);
     reduce_final<PTB_REDUCE_SUM><<<dim3(1), dim3(kBlock), 0, s>>>(part, g, out);
   } else {
-    reduce_partial<PTB_REDUCE_MAX><<<dim3(g), dim3(kBlock), 0, s>>>(xi, n, part);
+    reduce_partial<PTB_REDUCE_MAX, InT><<<dim3(g), dim3(kBlock), 0, s>>>(x, n, part);
     reduce_final<PTB_REDUCE_MAX><<<dim3(1), dim3(kBlock), 0, s>>>(part, g, out);
   }
   return launch_status();
+}
+
+}  // namespace
+
+PTB_EXPORT int ptb_reduce_bf16(const void* x, float* out, int64_t n, int op, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  return reduce_launch(static_cast<const uint16_t*>(x), out, n, op, workspace, workspace_bytes, stream);
+}
+
+PTB_EXPORT int ptb_reduce_f32(const float* x, float* out, int64_t n, int op, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  return reduce_launch(x, out, n, op, workspace, workspace_bytes, stream);
 }
 
 PTB_EXPORT int ptb_add_scalar_bf16(const void* x, void* y, int64_t n, float s, void* stream) {

@@ -75,11 +75,13 @@ SIGNATURES = {
     "ptb_status_string": (ctypes.c_char_p, [_c_int]),
     "ptb_rmsnorm_bf16": (_c_int, [_vp, _vp, _c_int, _vp, _c_i64, _c_i64, _c_f32, _vp]),
     "ptb_softmax_rows_bf16": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
+    "ptb_softmax_rows_bf16_f32": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "ptb_silu_mul_bf16": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "ptb_transpose_heads_bf16": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "ptb_qk_norm_rope_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_f32, _vp]),
     "ptb_reduce_workspace_bytes": (_c_size, [_c_i64]),
     "ptb_reduce_bf16": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _c_size, _vp]),
+    "ptb_reduce_f32": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _c_size, _vp]),
     "ptb_add_scalar_bf16": (_c_int, [_vp, _vp, _c_i64, _c_f32, _vp]),
     "ptb_slice_add_bf16": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_f32, _vp]),
     "ptb_gemm_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
@@ -113,6 +115,10 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
             raise LibraryMissing(
                 f"{p} is not built: run __graft_entry__.build() (or python -m ptb_amd.build); "
                 "ptb_amd has no non-HIP fallback")
+        # torch ships its own HIP runtime: load it first so the library binds to that one instance
+        # (a second runtime loaded ahead of torch's sees no device once torch has claimed it)
+        import torch  # noqa: F401
+
         lib = ctypes.CDLL(str(p))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

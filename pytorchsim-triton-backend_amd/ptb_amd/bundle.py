@@ -10,11 +10,12 @@ The Triton source is kept as text: the kernel families that need index facts rea
 from __future__ import annotations
 
 import ast
+import gzip
 import json
 import os
 from dataclasses import dataclass, field
 
-from .contract import Arg, KernelSpec
+from .contract import Arg, KernelSpec, spec_from_manifest
 
 SUITE_KEYS = {
     # validation/{vector,gemm,attention,layer,qwen3_8b}/simulate_shapes.py KEYS
@@ -128,4 +129,33 @@ def load_bundle(bundle_dir: str, suite: str | None = None, where=None) -> list:
         if callable(where) and not where(man):
             continue
         out.append(load_workload(p))
+    return out
+
+
+def read_manifests(path: str) -> dict:
+    """A manifests file (``.json`` or ``.json.gz``): workload name -> {suite, keys, order, kernels},
+    each kernel a manifest dict (``KernelSpec.manifest()`` plus ``extra.hints``, ``launches``,
+    ``dir``) -- the bundle's facts without its directory tree."""
+    opener = gzip.open if str(path).endswith(".gz") else open
+    with opener(path, "rt") as fh:
+        return json.load(fh)
+
+
+def workloads_from_manifests(data: dict, suite: str | None = None, where=None) -> list:
+    """The workloads of a manifests file as :class:`Workload` objects (the Triton source is absent;
+    kernels that need index facts carry them as ``extra.hints``), filtered as :func:`load_bundle`."""
+    out = []
+    for name in sorted(data):
+        w = data[name]
+        if suite and w["suite"] != suite:
+            continue
+        if isinstance(where, dict) and any(str(w["keys"].get(k)) != str(v) for k, v in where.items()):
+            continue
+        if callable(where) and not where(dict(w["keys"], workload=name, suite=w["suite"])):
+            continue
+        wl = Workload(name=name, suite=w["suite"], keys=dict(w["keys"]), order=list(w["order"]))
+        for man in w["kernels"]:
+            wl.kernels.append(BundleKernel(dir=man["dir"], spec=spec_from_manifest(man), source="",
+                                           launches=int(man.get("launches", 1))))
+        out.append(wl)
     return out

@@ -225,7 +225,10 @@ def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
         cols = sizes("r0_numel")
         if not cols or ins[0].numel % cols:
             raise UnsupportedKernel(f"{name}: softmax needs its row length r0_numel")
-        return Plan("softmax", dict(rows=ins[0].numel // cols, cols=cols, x=ins[0].name, y=outs[0].name))
+        if ins[0].dtype != "bfloat16" or outs[0].dtype not in ("bfloat16", "float32"):
+            raise UnsupportedKernel(f"{name}: softmax reads bf16 and writes bf16 or fp32")
+        return Plan("softmax", dict(rows=ins[0].numel // cols, cols=cols, x=ins[0].name, y=outs[0].name,
+                                    out_f32=outs[0].dtype == "float32"))
     if "_mm_" in name and len(ins) == 2 and len(outs) == 1 and sizes("r0_numel") and sizes("xnumel"):
         # the M = 1 template: out[n] = sum_k in0[k] * in1[k * N + n] (gemm_1x<K>x<N>_bf16)
         k, n = sizes("r0_numel"), sizes("xnumel")
@@ -248,18 +251,21 @@ def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
     if len(ins) == 1 and len(outs) == 1 and outs[0].dtype == "float32" and "slice" in name:
         # out[i] = float(x[first + i]) + c: the load offset and the constant from the source
         first = int(hints.get("first", 0))
-        if source is not None:
+        if source:
             m = re.search(r"tl\.load\(\s*" + re.escape(ins[0].name) + r"\s*\+\s*\(\s*(\d+)\s*\)\s*\)", source)
             if not m:
                 raise UnsupportedKernel(f"{name}: the slice kernel does not load one fixed element")
             first = int(m.group(1))
         return Plan("slice_add", dict(first=first, count=outs[0].numel, s=_float_constant(source, 1.0), x=ins[0].name,
                                       y=outs[0].name))
-    if len(ins) == 1 and len(outs) == 1 and outs[0].numel == 1 and outs[0].dtype == "float32":
+    if (len(ins) == 1 and len(outs) == 1 and outs[0].numel == 1 and outs[0].dtype == "float32"
+            and ins[0].dtype in ("bfloat16", "float32")):
         if "_sum_" in name or name.endswith("sum"):
-            return Plan("reduce", dict(op="sum", n=ins[0].numel, x=ins[0].name, y=outs[0].name))
+            return Plan("reduce", dict(op="sum", n=ins[0].numel, x=ins[0].name, y=outs[0].name,
+                                       in_f32=ins[0].dtype == "float32"))
         if "_max_" in name or name.endswith("max"):
-            return Plan("reduce", dict(op="max", n=ins[0].numel, x=ins[0].name, y=outs[0].name))
+            return Plan("reduce", dict(op="max", n=ins[0].numel, x=ins[0].name, y=outs[0].name,
+                                       in_f32=ins[0].dtype == "float32"))
     if "rsqrt" in name and "mean" in name:
         if len(ins) == 2 and len(outs) == 1:
             x, w = ins
@@ -276,7 +282,7 @@ def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
         if "silu" in name and x.numel == 2 * y.numel:
             if "inter" in hints:
                 inter = int(hints["inter"])
-            elif source is not None:
+            elif source:
                 inter = _row_length_from_source(source)
             else:
                 raise UnsupportedKernel(f"{name}: silu_mul needs the kernel source (or an 'inter' hint)")
@@ -284,7 +290,7 @@ def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
         if "transpose" in name and x.numel == y.numel:
             if {"d0", "d1", "inner"} <= set(hints):
                 d0, d1, inner = int(hints["d0"]), int(hints["d1"]), int(hints["inner"])
-            elif source is not None:
+            elif source:
                 d0, d1, inner = _permutation_from_source(source, x.numel)
             else:
                 raise UnsupportedKernel(f"{name}: a transpose needs the kernel source (or d0/d1/inner hints)")
@@ -336,7 +342,8 @@ def run(plan: Plan, tensors: dict) -> None:
     elif f == "silu_mul":
         ops.silu_mul(t[p["x"]].view(p["rows"], 2 * p["inter"]), out=t[p["y"]].view(p["rows"], p["inter"]))
     elif f == "softmax":
-        ops.softmax_rows(t[p["x"]].view(p["rows"], p["cols"]), out=t[p["y"]].view(p["rows"], p["cols"]))
+        ops.softmax_rows(t[p["x"]].view(p["rows"], p["cols"]), out=t[p["y"]].view(p["rows"], p["cols"]),
+                         out_dtype=ops.F32 if p["out_f32"] else ops.BF16)
     elif f == "reduce":
         ops.reduce(t[p["x"]], p["op"], out=t[p["y"]])
     elif f == "add_scalar":
@@ -398,9 +405,9 @@ def work_of(plan: Plan) -> tuple:
         return 5.0 * n, 6.0 * n
     if f == "softmax":
         n = p["rows"] * p["cols"]
-        return 5.0 * n, 4.0 * n
+        return 5.0 * n, (6.0 if p.get("out_f32") else 4.0) * n
     if f == "reduce":
-        return float(p["n"]), 2.0 * p["n"] + 4.0
+        return float(p["n"]), (4.0 if p.get("in_f32") else 2.0) * p["n"] + 4.0
     if f == "add_scalar":
         return float(p["n"]), 4.0 * p["n"]
     if f == "slice_add":

@@ -57,10 +57,14 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6, out=None) -> to
     return y
 
 
-def softmax_rows(x: torch.Tensor, out=None) -> torch.Tensor:
+def softmax_rows(x: torch.Tensor, out=None, out_dtype=BF16) -> torch.Tensor:
+    """Row softmax of bf16 rows; the result in bf16 (one rounding) or, with out_dtype fp32, unrounded."""
     _need(x, "x", BF16, 2)
-    y = _out(out, tuple(x.shape), BF16, x)
-    _lib.call("ptb_softmax_rows_bf16", x.data_ptr(), y.data_ptr(), x.shape[0], x.shape[1], _stream(x))
+    if out_dtype not in (BF16, F32):
+        raise TypeError(f"softmax_rows writes bf16 or fp32, not {out_dtype}")
+    y = _out(out, tuple(x.shape), out_dtype, x)
+    fn = "ptb_softmax_rows_bf16_f32" if out_dtype == F32 else "ptb_softmax_rows_bf16"
+    _lib.call(fn, x.data_ptr(), y.data_ptr(), x.shape[0], x.shape[1], _stream(x))
     return y
 
 
@@ -101,14 +105,15 @@ def qk_norm_rope(x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch
 
 
 def reduce(x: torch.Tensor, op: str = "sum", out=None, workspace=None) -> torch.Tensor:
-    """Whole-tensor sum or max of a bf16 tensor, as one fp32 value (shape [1])."""
-    _need(x, "x", BF16)
+    """Whole-tensor sum or max of a bf16 or fp32 tensor, as one fp32 value (shape [1])."""
+    _need(x, "x", (BF16, F32))
     code = {"sum": _lib.PTB_REDUCE_SUM, "max": _lib.PTB_REDUCE_MAX}[op]
     y = _out(out, (1,), F32, x)
     need = _lib.load().ptb_reduce_workspace_bytes(x.numel())
     if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-    _lib.call("ptb_reduce_bf16", x.data_ptr(), y.data_ptr(), x.numel(), code, workspace.data_ptr(),
+    fn = "ptb_reduce_f32" if x.dtype == F32 else "ptb_reduce_bf16"
+    _lib.call(fn, x.data_ptr(), y.data_ptr(), x.numel(), code, workspace.data_ptr(),
               workspace.numel() * workspace.element_size(), _stream(x))
     return y
 

@@ -10,6 +10,10 @@ the specs' seeded ``make_inputs`` convention, and adds TFLOP/s, GB/s and the MI3
 fraction per kernel.  ``--shard K/N`` and ``--merge`` split and join runs as the reference's do.
 
     python -m ptb_amd.validation qwen3_8b --bundle <reference>/validation/pytorchsim --out results.json
+    python -m ptb_amd.validation gemm --manifests bundle_manifests.json.gz --out results.json
+
+``--manifests`` reads the workloads from a manifests file (tests/golden/extract_bundle.py writes
+one for the whole bundle) where the bundle's directory tree is not at hand.
 """
 from __future__ import annotations
 
@@ -25,7 +29,7 @@ MI355X = {"name": "MI355X (gfx950)", "peak_bf16_tflops": 2500.0, "peak_fp8_tflop
 SUITES = tuple(bundle.SUITE_KEYS)
 
 
-def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0) -> dict:
+def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0, settle: float = 0.02) -> dict:
     """Run one bundle kernel on the GPU and time it; returns its record."""
     import torch
 
@@ -37,9 +41,14 @@ def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0) -> dict:
             tensors[a.name] = host[a.name].to("cuda")
         else:
             tensors[a.name] = torch.empty(a.numel, dtype=getattr(torch, a.dtype), device="cuda")
-    for _ in range(warmup):
-        kernels.run(plan, tensors)
-    torch.cuda.synchronize()
+    # the clock needs tens of ms of load to leave idle: run the kernel for `settle` seconds first
+    t_end = time.perf_counter() + settle
+    while True:
+        for _ in range(max(1, warmup)):
+            kernels.run(plan, tensors)
+        torch.cuda.synchronize()
+        if time.perf_counter() >= t_end:
+            break
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -55,14 +64,14 @@ def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0) -> dict:
             "tflops": tflops, "gbs": gbs, "roofline_us": roof_us, "roofline_frac": roof_us / us if us else None}
 
 
-def run_workload(w, reps: int = 20, warmup: int = 3) -> dict:
+def run_workload(w, reps: int = 20, warmup: int = 3, settle: float = 0.02) -> dict:
     got = dict(w.keys, kernel=w.name, rc=0, failed_step=None, kernels=[])
     t0 = time.monotonic()
     step = "resolve"
     try:
         for bk in w.kernels:
             step = bk.dir
-            got["kernels"].append(time_kernel(bk, reps, warmup))
+            got["kernels"].append(time_kernel(bk, reps, warmup, settle=settle))
         got["us"] = sum(k["us"] * k["launches"] for k in got["kernels"])
         got["roofline_us"] = sum(k["roofline_us"] * k["launches"] for k in got["kernels"])
     except Exception as e:  # noqa: BLE001 - a workload's failure is recorded, never lost
@@ -105,6 +114,7 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="time a validation suite's bundle workloads on the GPU")
     ap.add_argument("suite", choices=SUITES)
     ap.add_argument("--bundle", required=False, help="the reference's validation/pytorchsim directory")
+    ap.add_argument("--manifests", required=False, help="a manifests file (.json or .json.gz) instead of --bundle")
     ap.add_argument("--out", default="results.json")
     ap.add_argument("--where", action="append", help="key=value filter on the workload's keys (repeatable)")
     ap.add_argument("--only", action="append", help="workload name (repeatable)")
@@ -112,15 +122,20 @@ def main(argv=None) -> int:
     ap.add_argument("--merge", nargs="+", help="join shard results.json files into --out")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--settle", type=float, default=0.02, help="seconds of back-to-back launches before timing")
     args = ap.parse_args(argv)
     if args.merge:
         return merge(args.merge, args.out)
-    if not args.bundle:
-        ap.error("--bundle is required unless --merge")
+    if bool(args.bundle) == bool(args.manifests):
+        ap.error("give one of --bundle or --manifests (unless --merge)")
     from . import _lib
 
     _lib.load()
-    ws = bundle.load_bundle(args.bundle, args.suite, parse_where(args.where) or None)
+    if args.bundle:
+        ws = bundle.load_bundle(args.bundle, args.suite, parse_where(args.where) or None)
+    else:
+        ws = bundle.workloads_from_manifests(bundle.read_manifests(args.manifests), args.suite,
+                                             parse_where(args.where) or None)
     if args.only:
         ws = [w for w in ws if w.name in set(args.only)]
     part = None
@@ -131,7 +146,7 @@ def main(argv=None) -> int:
     done = []
     write_results(args.out, args.suite, done, len(ws), part)
     for w in ws:
-        r = run_workload(w, args.reps, args.warmup)
+        r = run_workload(w, args.reps, args.warmup, args.settle)
         done.append(r)
         write_results(args.out, args.suite, done, len(ws), part)
         print(f"{w.name}: rc={r['rc']} us={r.get('us', float('nan')):.1f}", flush=True)

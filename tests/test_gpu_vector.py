@@ -124,6 +124,16 @@ def test_reduce(n, seed):
     assert abs(gs - ws) <= 1e-5 * abs(ws), (gs, ws)
 
 
+@pytest.mark.parametrize("n,seed", [(8, 0), (1000003, 1), (4096 * 4096, 2)])
+def test_reduce_fp32_input(n, seed):
+    """fp32 elements (the MoE router's sum of its top-k weights is the 8-element case)."""
+    x = torch.randn(n, generator=torch.Generator().manual_seed(seed)) + 0.5
+    xd = x.to(DEV)
+    assert torch.equal(ops.reduce(xd, "max").cpu(), oracle.reduce_max(x))
+    got, want = float(ops.reduce(xd, "sum")), float(oracle.reduce_sum(x))
+    assert abs(got - want) <= 1e-6 * float(x.abs().sum()) + 1e-6, (got, want)
+
+
 def test_reduce_max_nan():
     x = randn((4096,), 9)
     x[1234] = float("nan")

@@ -8,11 +8,11 @@ import numpy as np
 import pytest
 import torch
 
-from ptb_amd import contract, device, kernels, launcher, verify
+from ptb_amd import bundle, contract, device, kernels, launcher, verify
 from ptb_amd.contract import Arg, KernelSpec
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-MANIFESTS = json.loads((GOLDEN / "bundle_manifests.json").read_text())
+MANIFESTS = bundle.read_manifests(GOLDEN / "bundle_manifests.json.gz")
 
 
 def spec_of(workload, i):
@@ -59,10 +59,45 @@ def test_seeded_inputs_follow_the_spec_convention():
 @pytest.mark.parametrize("workload", sorted(MANIFESTS))
 def test_every_fixture_kernel_resolves_to_its_recorded_family(workload):
     for man in MANIFESTS[workload]["kernels"]:
+        if man["family"] is None:
+            with pytest.raises(kernels.UnsupportedKernel):
+                kernels.resolve(contract.spec_from_manifest(man))
+            continue
         plan = kernels.resolve(contract.spec_from_manifest(man))
         assert plan.family == man["family"], man["name"]
         flops, nbytes = kernels.work_of(plan)
         assert nbytes > 0
+
+
+def test_fixture_covers_the_whole_bundle():
+    """All 502 workloads; the only kernels no HIP family serves are the Qwen3-30B-A3B MoE layer
+    suite's routing / grouped-GEMM kernels (validation/layer)."""
+    assert len(MANIFESTS) == 502
+    suites = {}
+    for w in MANIFESTS.values():
+        suites[w["suite"]] = suites.get(w["suite"], 0) + 1
+        for m in w["kernels"]:
+            assert m["family"] is not None or w["suite"] == "layer", m["name"]
+    assert suites == {"vector": 228, "gemm": 110, "attention": 56, "layer": 96, "qwen3_8b": 12}
+
+
+def test_workloads_from_manifests_filters_like_the_bundle_reader():
+    ws = bundle.workloads_from_manifests(MANIFESTS, "gemm", {"M": 4096})
+    assert ws and all(w.suite == "gemm" and str(w.keys["M"]) == "4096" for w in ws)
+    w = bundle.workloads_from_manifests(MANIFESTS, "qwen3_8b", {"T": 2048, "name": "prefill"})
+    assert [x.name for x in w] == ["qwen3_8b_layer_prefill_2048x2048_bf16"]
+    assert len(w[0].order) == 14 and sum(k.launches for k in w[0].kernels) == 14
+    assert all(kernels.resolve(k.spec, k.source).family for k in w[0].kernels)
+
+
+def test_every_workload_resolves_from_its_manifest_alone():
+    """The validation runner's --manifests path: no Triton source, only the manifest's hints."""
+    for w in bundle.workloads_from_manifests(MANIFESTS):
+        for bk in w.kernels:
+            if w.suite == "layer" and bk.spec.extra["hints"] == {} and MANIFESTS[w.name]["kernels"][
+                    [k.dir for k in w.kernels].index(bk.dir)]["family"] is None:
+                continue
+            assert kernels.resolve(bk.spec, bk.source).family, (w.name, bk.dir)
 
 
 def test_qwen3_layer_plans_match_the_model_shapes():

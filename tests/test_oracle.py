@@ -144,6 +144,18 @@ def test_softmax_matches_library_and_invariants():
     assert torch.isnan(oracle.softmax_rows(xn)[0]).all()
 
 
+def test_softmax_fp32_out_is_the_unrounded_library_softmax():
+    """The router's fp32-out softmax: within fp32 rounding of the fp64 softmax, rows sum to 1 within
+    fp32 error, and rounding it to bf16 gives the bf16-out oracle (one rounding, nothing else)."""
+    x = rnd((7, 128), 40)
+    got = oracle.softmax_rows(x, torch.float32)
+    assert got.dtype == torch.float32
+    want = torch.softmax(x.double(), dim=-1)
+    assert torch.allclose(got.double(), want, rtol=1e-6, atol=1e-9)
+    assert torch.allclose(got.double().sum(-1), torch.ones(7, dtype=torch.float64), atol=1e-6)
+    assert torch.equal(got.to(torch.bfloat16), oracle.softmax_rows(x))
+
+
 def test_silu_mul_matches_library():
     gu = rnd((17, 2 * 1032), 5)
     got = oracle.silu_mul(gu)
