@@ -29,7 +29,7 @@ MI355X = {"name": "MI355X (gfx950)", "peak_bf16_tflops": 2500.0, "peak_fp8_tflop
 SUITES = tuple(bundle.SUITE_KEYS)
 
 
-def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0, settle: float = 0.02) -> dict:
+def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0, settle: float = 0.02, graph: bool = True) -> dict:
     """Run one bundle kernel on the GPU and time it; returns its record."""
     import torch
 
@@ -49,29 +49,52 @@ def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0, settle: floa
         torch.cuda.synchronize()
         if time.perf_counter() >= t_end:
             break
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        kernels.run(plan, tensors)
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
+    eager_us = _time(lambda: [kernels.run(plan, tensors) for _ in range(reps)], torch) / reps
+    # the same launches captured once as a HIP graph and replayed: the device time without the
+    # host's per-launch cost (which sets the time of kernels shorter than a Python call)
+    us, timing = eager_us, "eager"
+    if graph:
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side), torch.cuda.graph(g, stream=side):
+                for _ in range(reps):
+                    kernels.run(plan, tensors)
+            torch.cuda.current_stream().wait_stream(side)
+            g.replay()
+            torch.cuda.synchronize()
+            us = min(_time(g.replay, torch) for _ in range(3)) / reps
+            timing = "graph"
+        except Exception:  # noqa: BLE001 - a kernel that cannot be captured keeps its eager time
+            torch.cuda.synchronize()
     flops, nbytes = kernels.work_of(plan)
     tflops = flops / (us * 1e-6) / 1e12
     gbs = nbytes / (us * 1e-6) / 1e9
     roof_us = max(flops / (MI355X["peak_bf16_tflops"] * 1e12), nbytes / (MI355X["hbm_gbs"] * 1e9)) * 1e6
     return {"dir": bk.dir, "name": bk.spec.name, "launches": bk.launches, "family": plan.family, "us": us,
+            "eager_us": eager_us, "timing": timing, "flops": flops, "bytes": nbytes,
             "tflops": tflops, "gbs": gbs, "roofline_us": roof_us, "roofline_frac": roof_us / us if us else None}
 
 
-def run_workload(w, reps: int = 20, warmup: int = 3, settle: float = 0.02) -> dict:
+def _time(fn, torch) -> float:
+    """Microseconds fn() takes on the current stream, by HIP events."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3
+
+
+def run_workload(w, reps: int = 20, warmup: int = 3, settle: float = 0.02, graph: bool = True) -> dict:
     got = dict(w.keys, kernel=w.name, rc=0, failed_step=None, kernels=[])
     t0 = time.monotonic()
     step = "resolve"
     try:
         for bk in w.kernels:
             step = bk.dir
-            got["kernels"].append(time_kernel(bk, reps, warmup, settle=settle))
+            got["kernels"].append(time_kernel(bk, reps, warmup, settle=settle, graph=graph))
         got["us"] = sum(k["us"] * k["launches"] for k in got["kernels"])
         got["roofline_us"] = sum(k["roofline_us"] * k["launches"] for k in got["kernels"])
     except Exception as e:  # noqa: BLE001 - a workload's failure is recorded, never lost
@@ -123,6 +146,7 @@ def main(argv=None) -> int:
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--settle", type=float, default=0.02, help="seconds of back-to-back launches before timing")
+    ap.add_argument("--eager", action="store_true", help="time Python launches only (no HIP graph replay)")
     args = ap.parse_args(argv)
     if args.merge:
         return merge(args.merge, args.out)
@@ -146,7 +170,7 @@ def main(argv=None) -> int:
     done = []
     write_results(args.out, args.suite, done, len(ws), part)
     for w in ws:
-        r = run_workload(w, args.reps, args.warmup, args.settle)
+        r = run_workload(w, args.reps, args.warmup, args.settle, graph=not args.eager)
         done.append(r)
         write_results(args.out, args.suite, done, len(ws), part)
         print(f"{w.name}: rc={r['rc']} us={r.get('us', float('nan')):.1f}", flush=True)
