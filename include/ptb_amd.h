@@ -40,6 +40,8 @@ extern "C" {
 
 #define PTB_DTYPE_BF16 0
 #define PTB_DTYPE_F32 1
+#define PTB_DTYPE_I32 2
+#define PTB_DTYPE_I64 3
 
 #define PTB_REDUCE_SUM 0
 #define PTB_REDUCE_MAX 1
@@ -181,6 +183,117 @@ size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, int64_t seq);
 int ptb_attn_decode_bf16(const void* q, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
                          int64_t seq, int64_t head_dim, float scale, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* ---- Qwen3-30B-A3B mixture-of-experts layer (validation/pytorchsim/layer_op_* and layer_layer_*).
+ * Paths below are relative to validation/pytorchsim/; LOP_<op> = layer_op_<op>_1024x0_bf16 and
+ * LL = layer_layer_prefill_1024x1024_bf16 (other token counts differ only in sizes).  Index
+ * arguments are int64 (int32 where named); entries outside a table are bounds-checked and give
+ * zeros where the reference would stop on a device_assert. */
+
+/* Zero nbytes at out (a fill kernel, no memset: safe in captured graphs).
+ * Replaces: LOP_gmm_gate_up/00_..._fused_new_zeros_q6uym5lr_triton.py:17-22 */
+int ptb_fill_zero(void* out, int64_t nbytes, void* stream);
+
+/* y[i] = (int32) x[i] (two's-complement wrap).
+ * Replaces: LOP_gmm_gate_up/04_..._fused__to_copy_oeoxw6br_triton.py:17-23 */
+int ptb_cast_i64_i32(const int64_t* x, int32_t* y, int64_t n, void* stream);
+
+/* Inclusive prefix sum of n <= 8192 integers (x_dtype, y_dtype: PTB_DTYPE_I32 / _I64), into y0 and,
+ * when not NULL, y1; int32 results wrap.
+ * Replaces: LOP_gmm_gate_up/01_..._fused_cumsum_6fi3sv3v_triton.py:17-33, LOP_combine/01_..._fused_cumsum_
+ *           qi2bfo64_triton.py:17-33, LL/08_..._fused__to_copy_cumsum_ggousx36_triton.py:17-35 */
+int ptb_cumsum_int(const void* x, int x_dtype, void* y0, void* y1, int y_dtype, int64_t n, void* stream);
+
+/* From inclusive group ends (int32 or int64, n <= 8192): starts[i] = ends[i-1] (0 for i = 0),
+ * rows[i] = ends[i] - starts[i], nonempty[i] = #{j <= i : rows[j] > 0}; all int64.
+ * Replaces: LOP_gmm_gate_up/02_..._fused__to_copy_cat_cumsum_gt_new_zeros_slice_sub_gnib2ocx_triton.py:17-57 */
+int ptb_moe_group_table(const void* ends, int ends_dtype, int64_t n, int64_t* nonempty, int64_t* starts,
+                        int64_t* rows, void* stream);
+
+/* out[i] = #{r < n : x[r] <= i} as int32, i < m.
+ * Replaces: LOP_gmm_gate_up/03_..._fused__to_copy_arange_le_sum_unsqueeze_j72wougd_triton.py:17-35 */
+int ptb_count_le(const int64_t* x, int64_t n, int32_t* out, int64_t m, void* stream);
+
+/* Expert histogram of r slot ids over e <= 1024 experts: counts[x] (and counts2[x] when not NULL)
+ * = #{s : ids[s] == x}; cum[s*e + x] = #{s' <= s : ids[s'] == x}.
+ * Replaces: LOP_combine/00_..._fused__to_copy_arange_cumsum_eq_sum_unsqueeze_view_dmnbvm2a_triton.py:17-54
+ *           and LL/07_..._vrrn72ou (two count outputs) */
+int ptb_moe_expert_count(const int64_t* ids, int64_t r, int64_t e, int64_t* counts, int64_t* counts2,
+                         int64_t* cum, void* stream);
+
+/* out[s] = cum[s*e + ids[s]] (each slot's 1-based rank within its expert; 0 if ids[s] is no expert).
+ * Replaces: LOP_combine/02_..._fused__to_copy_arange_eq_mul_sum_unsqueeze_view_dmbn5ao4_triton.py:17-44 */
+int ptb_moe_rank_select(const int64_t* cum, const int64_t* ids, int64_t r, int64_t e, int64_t* out, void* stream);
+
+/* Stable sort of each of `rows` rows of e keys (key_dtype PTB_DTYPE_I64 or PTB_DTYPE_F32, values
+ * the same dtype): values in order, indices = original positions (int64); floats order NaN above
+ * +inf and -0 as +0.  Rows longer than 8192 need ptb_sort_workspace_bytes(rows, e) of workspace.
+ * Replaces: LOP_dispatch/00__sort_kernel/_sort_kernel_triton.py:4-49 */
+size_t ptb_sort_workspace_bytes(int64_t rows, int64_t e);
+int ptb_sort_rows(const void* x, int key_dtype, void* values, int64_t* indices, int64_t rows, int64_t e,
+                  int descending, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The k largest (largest != 0) or smallest of each row of e <= 1024 fp32 values, in order, ties to
+ * the lowest position; indices int64.
+ * Replaces: LOP_router_post/01__topk_kernel/_topk_kernel_triton.py:4-30 */
+int ptb_topk_rows_f32(const float* x, int64_t rows, int64_t e, int64_t k, int largest, float* values,
+                      int64_t* indices, void* stream);
+
+/* out[s, :] = x[floor(slot[s] / k), :] for r slots (bf16 rows of c; the token index wraps from the
+ * end when negative; rows with no such token are zeros).
+ * Replaces: LOP_dispatch/01_..._fused_floor_divide_index_select_guslzqr3_triton.py:17-42 and
+ *           LL/23_..._fused__to_copy_floor_divide_index_select_4hjjds7p */
+int ptb_moe_gather_rows_bf16(const int64_t* slot, int64_t r, int64_t k, const void* x, int64_t t, int64_t c,
+                             void* out, void* stream);
+
+/* Each of `tokens` tokens' weighted sum of its k expert rows of y (yrows x c, bf16): slot s = t*k + j
+ * of expert id = ids[s] sits at row ends[id] - counts[id] + rank[s] - 1.  w_dtype PTB_DTYPE_BF16: w
+ * bf16, wsum NULL, out = bf16(sum); PTB_DTYPE_F32: weight w[s] / wsum[t] and, with h, out is updated
+ * in place: out = bf16((h + out) + sum).  fp32 accumulation.
+ * Replaces: LOP_combine/03_..._fused__to_copy_add_index_select_mul_sub_sum_unsqueeze_view_jskr7oe3_triton.py
+ *           :17-54 and LL/27_..._fused__to_copy_add_div_index_select_mul_sub_sum_unsqueeze_view_pjwo6jhr
+ *           _triton.py:17-63 */
+int ptb_moe_combine_bf16(const int64_t* ids, const int64_t* ends, const int64_t* counts, const int64_t* rank,
+                         const void* y, int64_t yrows, const void* w, int w_dtype, const float* wsum, const void* h,
+                         void* out, int64_t tokens, int64_t k, int64_t e, int64_t c, void* stream);
+
+/* Rows of k fp32 values: out_bf16[r, j] = bf16(x[r, j] / sum_j x[r, j]) (out_sum NULL), or
+ * out_sum[r] = sum_j x[r, j] (out_bf16 NULL).
+ * Replaces: LOP_router_post/02_..._fused__to_copy_div_sum_d4c5sb6k_triton.py:17-35 and
+ *           LL/22_..._fused_sum_kon7yqsn_triton.py:17-34 */
+int ptb_normalize_rows_f32(const float* x, int64_t rows, int64_t k, void* out_bf16, float* out_sum, void* stream);
+
+/* y = bf16(float(a) + float(b)).
+ * Replaces: LOP_residual/00_..._fused_add_dfgomnnn_triton.py:17-26 */
+int ptb_add_bf16(const void* a, const void* b, void* y, int64_t n, void* stream);
+
+/* Rotate-half RoPE without a norm: x, out [tokens, heads, 128] bf16, cos/sin [tokens, 128] fp32.
+ * Replaces: LOP_rope_q/00_..._fused__to_copy_add_cat_mul_neg_slice_unsqueeze_4de5dxfe_triton.py:17-47
+ *           (and rope_k) */
+int ptb_rope_bf16(const void* x, const float* cos_t, const float* sin_t, void* out, int64_t tokens, int64_t heads,
+                  int64_t head_dim, void* stream);
+
+/* y = bf16( (x + a) * rsqrt(sum((x + a)^2) / cols + eps) * w ) per row, x + a in fp32 (a may be NULL).
+ * Replaces: LL/18_..._fused__to_copy_add_mean_mul_pow_rsqrt_p5e5f5kj_triton.py:17-58 */
+int ptb_rmsnorm_add_bf16(const void* x, const void* a, const void* w, void* y, int64_t rows, int64_t cols,
+                         float eps, void* stream);
+
+/* One token's normalised vector to each of its `rows` slots: out[s, :] = bf16( (x + a) *
+ * rsqrt(ss[0] / cols + eps) * w ).
+ * Replaces: layer_layer_decode_1x1024_bf16/19_..._fused__to_copy_add_floor_divide_index_select_mean_mul_pow_
+ *           rsqrt_wkrpkilh_triton.py:17-60 */
+int ptb_rms_broadcast_bf16(const void* x, const void* a, const float* ss, const void* w, void* out, int64_t rows,
+                           int64_t cols, float eps, void* stream);
+
+/* Grouped GEMM: for program p < nprog (<= 256), g = group[p] (int32): C[start[g] + i, :] =
+ * bf16( A[start[g] + i, :] . B_g ) for i < rows[g], B_g the row-major [k, n] bf16 matrix at
+ * b + g * weight_stride (nweights of them); A is [a_rows, k], C [a_rows, n]; start/rows hold ntab
+ * int32 entries.  Entries that do not describe rows inside A or a weight inside B count as empty.
+ * k % 64 == 0, n % 8 == 0.
+ * Replaces: LOP_gmm_gate_up/05__grouped_mm_kernel/_grouped_mm_kernel_triton.py:4-46 (and gmm_down) */
+int ptb_grouped_gemm_bf16(const void* a, const void* b, const int32_t* group, const int32_t* start,
+                          const int32_t* rows, void* c, int64_t nprog, int64_t ntab, int64_t a_rows,
+                          int64_t nweights, int64_t k, int64_t n, int64_t weight_stride, void* stream);
 
 #ifdef __cplusplus
 }

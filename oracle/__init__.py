@@ -21,9 +21,14 @@ How each function is pinned (tests/test_oracle.py):
                             row 0 attends only to key 0
   qwen3_layer               composition of the above in the manifest's launch order, checked
                             against an independent fp64 restatement of the Qwen3 block
+  moe.*                     (the Qwen3-30B-A3B MoE kernels) torch.sort / torch.topk / torch.cumsum
+                            / one-hot sums on the same inputs, brute-force Python loops on tiny
+                            inputs, routing invariants (every slot lands in exactly one expert
+                            row, dispatch -> grouped GEMM -> combine equals the dense mixture)
 
 Parity for the reference's *execution* arithmetic (its MXU accumulation order and EUP exp inside
 the un-vendored Coprocessor model) is unpinned beyond the tolerances its own baselines record;
 fp8 has no reference-side pin at all (fp8 is refused on tpuv6e, tests/baselines/tpuv6e.txt:174).
 """
 from .kernels import *  # noqa: F401,F403
+from .moe import *  # noqa: F401,F403

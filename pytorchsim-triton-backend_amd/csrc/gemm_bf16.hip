@@ -63,24 +63,87 @@ struct Shape {
   static constexpr int kBSlots = BN / 8;                 // 16-byte chunks per B row
 };
 
-template <int WM, int WN, bool RESID>
+// Grouped mode (the MoE grouped GEMM): program p of the launch multiplies group g = grp[p]'s
+// rows [gstart[g], gstart[g] + grows[g]) of A by weight g of B (row-major K x N at B + g*sbg) into
+// the same rows of C.  A workgroup's linear tile index runs over every program's row tiles in
+// program order (times the column tiles); the per-program tile counts are scanned in LDS, so
+// workgroups past the last tile leave at once.  Table entries that do not describe rows inside A
+// (or a weight inside B) count as empty.
+struct Groups {
+  const int32_t* grp;
+  const int32_t* gstart;
+  const int32_t* grows;
+  int nprog, ntab, nweights, a_rows;
+  int64_t sbg;
+};
+constexpr int kMaxPrograms = 256;
+
+template <int WM, int WN, bool RESID, bool GROUPED>
 __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_kernel(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const uint16_t* __restrict__ R,
-    uint16_t* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
+    const uint16_t* __restrict__ A_in, const uint16_t* __restrict__ B_in, const uint16_t* __restrict__ R,
+    uint16_t* __restrict__ C_in, int M_in, int N, int K, int tiles_m, int tiles_n, Groups gp) {
   using Sh = Shape<WM, WN>;
   constexpr int BM = Sh::BM, BN = Sh::BN, kABytes = Sh::kABytes, kStageBytes = Sh::kStageBytes;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStageBytes];
 
   // ---- tile selection
-  const int ntiles = tiles_m * tiles_n;
-  int pid = blockIdx.x;
-  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
-  const int width = kGroupM * tiles_n;
-  const int first_m = (pid / width) * kGroupM;
-  const int gsize = min(tiles_m - first_m, kGroupM);
-  const int tm = first_m + (pid % width) % gsize;
-  const int tn = (pid % width) / gsize;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const uint16_t* A = A_in;
+  const uint16_t* B = B_in;
+  uint16_t* C = C_in;
+  int M = M_in, m0, n0;
+  if constexpr (GROUPED) {
+    __shared__ int pref[kMaxPrograms + 1];
+    __shared__ int wsum[kThreads / 64];
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
+    int cnt = 0;
+    if (t < gp.nprog) {
+      const int g = gp.grp[t];
+      if (g >= 0 && g < gp.ntab) {
+        const int s0 = gp.gstart[g], nr = gp.grows[g];
+        if (nr > 0 && s0 >= 0 && int64_t(s0) + nr <= gp.a_rows && g < gp.nweights) cnt = (nr + BM - 1) / BM;
+      }
+    }
+    int v = cnt;   // inclusive scan over the 256 programs: within waves, then across the 4 waves
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int u = __shfl_up(v, off, 64);
+      if (l >= off) v += u;
+    }
+    if (l == 63) wsum[w] = v;
+    __syncthreads();
+    for (int i = 0; i < w; ++i) v += wsum[i];
+    pref[t + 1] = v;
+    if (t == 0) pref[0] = 0;
+    __syncthreads();
+    const int total = pref[gp.nprog];
+    const int tn = int(blockIdx.x) % tiles_n, mt_all = int(blockIdx.x) / tiles_n;
+    if (mt_all >= total) return;   // uniform over the workgroup, before the pipeline starts
+    int lo = 0, hi = gp.nprog;     // the last program p with pref[p] <= mt_all
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (pref[mid] <= mt_all) lo = mid;
+      else hi = mid;
+    }
+    const int g = gp.grp[lo], mt = mt_all - pref[lo];
+    const int first = gp.gstart[g] + mt * BM;
+    M = min(BM, gp.grows[g] - mt * BM);
+    A = A_in + int64_t(first) * K;
+    C = C_in + int64_t(first) * N;
+    B = B_in + int64_t(g) * gp.sbg;
+    m0 = 0;
+    n0 = tn * BN;
+  } else {
+    const int ntiles = tiles_m * tiles_n;
+    int pid = blockIdx.x;
+    if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+    const int width = kGroupM * tiles_n;
+    const int first_m = (pid / width) * kGroupM;
+    const int gsize = min(tiles_m - first_m, kGroupM);
+    const int tm = first_m + (pid % width) % gsize;
+    const int tn = (pid % width) / gsize;
+    m0 = tm * BM;
+    n0 = tn * BN;
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -258,14 +321,15 @@ int launch_gemm(const void* a, const void* b, const void* residual, void* c, int
   const int64_t tm = (m + Sh::BM - 1) / Sh::BM, tn = (n + Sh::BN - 1) / Sh::BN;
   if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
   const dim3 grid(unsigned(tm * tn)), block(kThreads);
+  const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
   if (residual)
-    gemm_bf16_kernel<WM, WN, true><<<grid, block, 0, s>>>(
+    gemm_bf16_kernel<WM, WN, true, false><<<grid, block, 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), static_cast<const uint16_t*>(residual),
-        static_cast<uint16_t*>(c), int(m), int(n), int(k), int(tm), int(tn));
+        static_cast<uint16_t*>(c), int(m), int(n), int(k), int(tm), int(tn), none);
   else
-    gemm_bf16_kernel<WM, WN, false><<<grid, block, 0, s>>>(
+    gemm_bf16_kernel<WM, WN, false, false><<<grid, block, 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, static_cast<uint16_t*>(c), int(m),
-        int(n), int(k), int(tm), int(tn));
+        int(n), int(k), int(tm), int(tn), none);
   return launch_status();
 }
 
@@ -297,4 +361,26 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
   if (tiles(256, 256) >= cus) return launch_gemm<4, 4>(a, b, residual, c, m, n, k, s);
   if (tiles(256, 128) >= cus) return launch_gemm<4, 2>(a, b, residual, c, m, n, k, s);
   return launch_gemm<2, 2>(a, b, residual, c, m, n, k, s);
+}
+
+PTB_EXPORT int ptb_grouped_gemm_bf16(const void* a, const void* b, const int32_t* group, const int32_t* start,
+                                     const int32_t* rows, void* c, int64_t nprog, int64_t ntab, int64_t a_rows,
+                                     int64_t nweights, int64_t k, int64_t n, int64_t weight_stride, void* stream) {
+  if (nprog < 0 || ntab < 0 || a_rows < 0 || nweights < 0 || k < 0 || n < 0) return PTB_ERR_SHAPE;
+  if (nprog == 0 || a_rows == 0 || n == 0) return PTB_OK;
+  if (!a || !b || !group || !start || !rows || !c) return PTB_ERR_NULL;
+  if (k == 0 || k % 64 || n % 8 || nprog > kMaxPrograms) return PTB_ERR_UNSUPPORTED;
+  if (weight_stride < k * n || a_rows > 0x7fffffff || ntab > 0x7fffffff || nweights > 0x7fffffff) return PTB_ERR_SHAPE;
+  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || int64_t(128) * k * 2 >= (int64_t(1) << 32))
+    return PTB_ERR_UNSUPPORTED;
+  if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (weight_stride % 8)) return PTB_ERR_ALIGN;
+  // a bound on the row tiles of every program together: each program's rows lie inside A
+  const int64_t tn = (n + 127) / 128, tm_bound = (a_rows + 127) / 128 + nprog;
+  if (tm_bound * tn > 0x7fffffff) return PTB_ERR_GRID;
+  const Groups gp{group, start, rows, int(nprog), int(ntab), int(nweights), int(a_rows), weight_stride};
+  gemm_bf16_kernel<2, 2, false, true><<<dim3(unsigned(tm_bound * tn)), dim3(kThreads), 0,
+                                        static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, static_cast<uint16_t*>(c), 0, int(n),
+      int(k), 0, int(tn), gp);
+  return launch_status();
 }

@@ -23,6 +23,8 @@ PTB_ERR_WORKSPACE = -7
 
 PTB_DTYPE_BF16 = 0
 PTB_DTYPE_F32 = 1
+PTB_DTYPE_I32 = 2
+PTB_DTYPE_I64 = 3
 PTB_REDUCE_SUM = 0
 PTB_REDUCE_MAX = 1
 
@@ -95,6 +97,26 @@ SIGNATURES = {
     "ptb_gemv_bf16": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
     "ptb_gemv_rmsnorm_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_f32, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
     "ptb_gemv_silu_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
+    "ptb_fill_zero": (_c_int, [_vp, _c_i64, _vp]),
+    "ptb_cast_i64_i32": (_c_int, [_vp, _vp, _c_i64, _vp]),
+    "ptb_cumsum_int": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_i64, _vp]),
+    "ptb_moe_group_table": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _vp, _vp]),
+    "ptb_count_le": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp]),
+    "ptb_moe_expert_count": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
+    "ptb_moe_rank_select": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp, _vp]),
+    "ptb_sort_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
+    "ptb_sort_rows": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_int, _vp, _c_size, _vp]),
+    "ptb_topk_rows_f32": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_int, _vp, _vp, _vp]),
+    "ptb_moe_gather_rows_bf16": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp]),
+    "ptb_moe_combine_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_int, _vp, _vp, _vp, _c_i64, _c_i64,
+                                      _c_i64, _c_i64, _vp]),
+    "ptb_normalize_rows_f32": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp]),
+    "ptb_add_bf16": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
+    "ptb_rope_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
+    "ptb_rmsnorm_add_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_f32, _vp]),
+    "ptb_rms_broadcast_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_f32, _vp]),
+    "ptb_grouped_gemm_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                       _c_i64, _vp]),
     "ptb_attn_decode_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "ptb_attn_decode_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _vp, _c_size,
                                       _vp]),

@@ -13,6 +13,7 @@ import ast
 import gzip
 import json
 import os
+import re
 from dataclasses import dataclass, field
 
 from .contract import Arg, KernelSpec, spec_from_manifest
@@ -77,13 +78,36 @@ def parse_spec_text(text: str, where: str = "<spec>") -> KernelSpec:
     raise ValueError(f"{where}: no SPEC = KernelSpec(...) assignment")
 
 
+_RECORDED = re.compile(r"out\[\s*'(\w+)'\s*\]\s*=\s*recorded\[")
+
+
+def recorded_args(spec_text: str) -> list:
+    """Arguments a spec's make_inputs takes from its recorded ``*_inputs.pt`` (``out['x'] =
+    recorded['x']``) rather than from the seeded generator, in argument order."""
+    return _RECORDED.findall(spec_text)
+
+
+def read_recorded(path: str, workload: str, kernel_dir: str) -> dict:
+    """The recorded inputs of one bundle kernel from a recorded-inputs file (``.npz`` written by
+    tests/golden/extract_bundle.py: keys ``<workload>/<kernel dir>/<arg>``), as numpy arrays."""
+    import numpy as np
+
+    pre = f"{workload}/{kernel_dir}/"
+    with np.load(path, allow_pickle=False) as z:
+        return {k[len(pre):]: z[k] for k in z.files if k.startswith(pre)}
+
+
 def load_kernel_dir(path: str) -> tuple:
     """(spec, triton source text) of one bundle kernel directory."""
     specs = sorted(f for f in os.listdir(path) if f.endswith("_spec.py"))
     if len(specs) != 1:
         raise ValueError(f"{path}: expected one *_spec.py, found {specs}")
     with open(os.path.join(path, specs[0])) as fh:
-        spec = parse_spec_text(fh.read(), specs[0])
+        text = fh.read()
+    spec = parse_spec_text(text, specs[0])
+    rec = recorded_args(text)
+    if rec:
+        spec.extra = dict(spec.extra or {}, recorded=rec)
     src = ""
     tri = specs[0][: -len("_spec.py")] + "_triton.py"
     if os.path.exists(os.path.join(path, tri)):

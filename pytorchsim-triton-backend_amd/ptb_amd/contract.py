@@ -137,13 +137,24 @@ def spec_from_manifest(manifest: dict) -> KernelSpec:
                       grid=tuple(manifest.get("grid", (1,))), extra=extra)
 
 
-def seeded_inputs(spec: KernelSpec, torch, seed: int = 0) -> dict:
+def seeded_inputs(spec: KernelSpec, torch, seed: int = 0, recorded: dict | None = None) -> dict:
     """The inputs the reference's generated specs draw (validation/pytorchsim/*/..._spec.py:28-36):
     one generator seeded once, then ``torch.randn(numel, generator=g).to(dtype)`` for every read
-    argument in argument order.  CPU tensors, flat, as the specs make them."""
+    argument in argument order.  Arguments the spec takes from its recorded ``*_inputs.pt`` instead
+    (named in ``extra["recorded"]``; the MoE kernels' index tables) come from `recorded` and draw
+    nothing from the generator, as the spec's make_inputs does.  CPU tensors, flat."""
     g = torch.Generator().manual_seed(seed)
+    taken = set((spec.extra or {}).get("recorded", ()))
     out = {}
     for a in spec.inputs():
+        if a.name in taken:
+            if recorded is None or a.name not in recorded:
+                raise KeyError(f"{spec.name}: argument {a.name} comes from the recorded inputs, which were not given")
+            t = torch.as_tensor(recorded[a.name]).reshape(-1)
+            if t.numel() != a.numel:
+                raise ValueError(f"{spec.name}: recorded {a.name} has {t.numel()} elements, the spec says {a.numel}")
+            out[a.name] = t.to(getattr(torch, a.dtype))
+            continue
         dt = getattr(torch, a.dtype)
         out[a.name] = torch.randn(a.numel, generator=g).to(dt)
     return out

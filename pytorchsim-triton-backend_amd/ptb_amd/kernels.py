@@ -25,6 +25,23 @@ the hot path is one of a few hand-written HIP families, chosen from what the spe
               ``mm`` template), with an RMSNorm prologue over a precomputed sum of squares (decode
               01, 06), or with a silu(g)*u prologue and a residual sum epilogue (decode 07)
 
+The Qwen3-30B-A3B (MoE) layer's kernels (layer_op_* and layer_layer_*), identified by name
+fragment, argument roles, dtypes and sizes (no source needed):
+
+  fill_zero, cast, cumsum, group_table, count_le   the expert-table bookkeeping around the grouped
+              GEMM (``new_zeros``, ``_to_copy``, ``cumsum``, ``cat_cumsum_gt_new_zeros_slice_sub``,
+              ``arange_..._le_sum``)
+  expert_count, rank_select   per-expert slot counts with each slot's running rank
+              (``arange_cumsum_eq_sum``, ``arange_eq_mul_sum``)
+  sort, topk  ``_sort_kernel`` (stable, int64 or fp32 keys) and ``_topk_kernel``
+  gather_rows, rms_broadcast   token rows laid out slot by slot (``floor_divide_index_select``; the
+              single-token form fused with the RMSNorm)
+  combine     the weighted sum of each token's expert rows (``index_select_mul_sub_sum``), with
+              bf16 weights, or fp32 weights over their sum plus the residual
+  normalize_rows, row_sum, add, rope, rmsnorm_add   router weights over their sum, their row sums,
+              the residual add, RoPE without the norm, and add + RMSNorm
+  grouped_mm  ``_grouped_mm_kernel``
+
 Anything else raises :class:`UnsupportedKernel` -- there is no fallback execution.
 """
 from __future__ import annotations
@@ -171,6 +188,146 @@ def _gemv_plan(spec: KernelSpec, source: str | None) -> Plan | None:
     return plan
 
 
+_I64, _I32, _F32, _BF16 = "int64", "int32", "float32", "bfloat16"
+
+
+def _moe_plan(spec: KernelSpec, name: str, sizes) -> Plan | None:
+    """The MoE layer's kernels; None when `spec` is not one of them."""
+    ce = spec.constexprs or {}
+    pure = [a for a in spec.args if a.role == "in"]
+    outs = [a for a in spec.args if a.role in ("out", "inout")]
+    n_grid = 1
+    for g in spec.grid:
+        n_grid *= int(g)
+
+    def need(ok: bool, why: str):
+        if not ok:
+            raise UnsupportedKernel(f"{name}: {why}")
+
+    if name == "_sort_kernel":
+        x, v, i = spec.arg("x_ptr"), spec.arg("v_ptr"), spec.arg("i_ptr")
+        rows = n_grid
+        need(x.dtype in (_I64, _F32) and v.dtype == x.dtype and i.dtype == _I64, "sort keys int64 or fp32")
+        need(bool(ce.get("FLOAT", False)) == (x.dtype == _F32), "FLOAT constexpr and key dtype disagree")
+        need(x.numel % rows == 0 and v.numel == x.numel == i.numel, "sort rows do not divide the keys")
+        return Plan("sort", dict(rows=rows, e=x.numel // rows, descending=bool(ce.get("DESCENDING", False)),
+                                 x=x.name, v=v.name, i=i.name))
+    if name == "_topk_kernel":
+        x, v, i = spec.arg("x_ptr"), spec.arg("v_ptr"), spec.arg("i_ptr")
+        e, k = int(ce["E"]), int(ce["K"])
+        need(x.dtype == _F32 and v.dtype == _F32 and i.dtype == _I64, "top-k over fp32")
+        need(x.numel % e == 0 and v.numel == i.numel == (x.numel // e) * k, "top-k sizes")
+        return Plan("topk", dict(e=e, k=k, largest=bool(ce.get("LARGEST", True)), x=x.name, v=v.name, i=i.name))
+    if name == "_grouped_mm_kernel":
+        a, b, c = spec.arg("a_ptr"), spec.arg("b_ptr"), spec.arg("c_ptr")
+        k, n = int(ce["K"]), int(ce["N"])
+        sbg, sbk, sbn = int(ce["sbg"]), int(ce["sbk"]), int(ce["sbn"])
+        need(sbn == 1 and sbk == n, "grouped weights are not row-major [K, N]")
+        need(int(ce.get("BN", n)) * int(spec.grid[1] if len(spec.grid) > 1 else 1) >= n, "column tiles short of N")
+        need(a.dtype == b.dtype == c.dtype == _BF16 and a.numel % k == 0 and c.numel == a.numel // k * n,
+             "grouped GEMM operand sizes")
+        return Plan("grouped_mm", dict(k=k, n=n, stride=sbg, a_rows=a.numel // k, nprog=spec.arg("group_ptr").numel,
+                                       nweights=b.numel // sbg, a=a.name, b=b.name, group="group_ptr",
+                                       start="start_ptr", rows="rows_ptr", c=c.name))
+    if not name.startswith("pytorchsim_triton_compiler_fused"):
+        return None
+    if "new_zeros" in name and not pure and len(outs) == 1 and "cumsum" not in name:
+        return Plan("fill_zero", dict(y=outs[0].name))
+    if "cumsum_eq_sum" in name:
+        need(len(pure) == 1 and pure[0].dtype == _I64 and all(o.dtype == _I64 for o in outs), "expert histogram")
+        r = pure[0].numel
+        small = [o for o in outs if any(q.numel == o.numel * r for q in outs if q is not o)]
+        big = [o for o in outs if o not in small]
+        need(len(big) == 1 and 1 <= len(small) <= 2, "expert histogram outputs")
+        e = small[0].numel
+        return Plan("expert_count", dict(r=r, e=e, ids=pure[0].name, counts=small[0].name,
+                                         counts2=small[1].name if len(small) == 2 else None, cum=big[0].name))
+    if "eq_mul_sum" in name:
+        need(len(pure) == 2 and len(outs) == 1 and all(a.dtype == _I64 for a in pure + outs), "rank select")
+        cum, ids = sorted(pure, key=lambda a: -a.numel)
+        need(cum.numel % ids.numel == 0 and outs[0].numel == ids.numel, "rank select sizes")
+        return Plan("rank_select", dict(r=ids.numel, e=cum.numel // ids.numel, cum=cum.name, ids=ids.name,
+                                        y=outs[0].name))
+    if "cat_cumsum_gt_new_zeros_slice_sub" in name:
+        need(len(pure) == 1 and len(outs) == 3 and pure[0].dtype in (_I32, _I64)
+             and all(o.dtype == _I64 and o.numel == pure[0].numel for o in outs), "group table")
+        return Plan("group_table", dict(n=pure[0].numel, ends=pure[0].name, nonempty=outs[0].name,
+                                        starts=outs[1].name, rows=outs[2].name))
+    if "cumsum" in name:
+        need(len(pure) == 1 and 1 <= len(outs) <= 2 and pure[0].dtype in (_I32, _I64)
+             and all(o.dtype == outs[0].dtype and o.dtype in (_I32, _I64) and o.numel == pure[0].numel for o in outs),
+             "integer scan")
+        return Plan("cumsum", dict(n=pure[0].numel, x=pure[0].name, y=outs[0].name,
+                                   y2=outs[1].name if len(outs) == 2 else None))
+    if "_le_" in name and len(pure) == 1 and len(outs) == 1 and pure[0].dtype == _I64 and outs[0].dtype == _I32:
+        return Plan("count_le", dict(n=pure[0].numel, m=outs[0].numel, x=pure[0].name, y=outs[0].name))
+    if (len(pure) == 1 and len(outs) == 1 and pure[0].dtype == _I64 and outs[0].dtype == _I32
+            and pure[0].numel == outs[0].numel):
+        return Plan("cast", dict(n=pure[0].numel, x=pure[0].name, y=outs[0].name))
+    if "floor_divide_index_select" in name and "rsqrt" in name:
+        slot, x, a, ss, w = pure
+        need(len(outs) == 1 and slot.dtype == _I64 and ss.dtype == _F32 and ss.numel == 1
+             and x.dtype == a.dtype == w.dtype == outs[0].dtype == _BF16 and x.numel == a.numel == w.numel
+             and outs[0].numel == slot.numel * x.numel, "single-token dispatch with RMSNorm")
+        return Plan("rms_broadcast", dict(rows=slot.numel, cols=x.numel, eps=1e-6, x=x.name, a=a.name, ss=ss.name,
+                                          w=w.name, y=outs[0].name))
+    if "floor_divide_index_select" in name:
+        need(len(pure) == 2 and len(outs) == 1, "dispatch gather args")
+        slot, x = pure
+        r = slot.numel
+        need(slot.dtype == _I64 and x.dtype == outs[0].dtype == _BF16 and outs[0].numel % r == 0, "dispatch gather")
+        cols = outs[0].numel // r
+        t = x.numel // cols
+        need(t > 0 and x.numel == t * cols and r % t == 0, "dispatch gather sizes")
+        return Plan("gather_rows", dict(r=r, t=t, k=r // t, cols=cols, slot=slot.name, x=x.name, y=outs[0].name))
+    if "index_select_mul_sub_sum" in name:
+        io = [a for a in spec.args if a.role == "inout"]
+        if io:   # (h + io) + sum_j y * (w / wsum)
+            need(len(pure) == 8, "combine with residual args")
+            ids, ends, counts, rank, y, w, wsum, h = pure
+            tokens, cols = wsum.numel, h.numel // wsum.numel
+            out = io[0]
+            need(w.dtype == wsum.dtype == _F32 and h.dtype == out.dtype == _BF16, "combine with residual dtypes")
+        else:
+            need(len(pure) == 6 and len(outs) == 1, "combine args")
+            ids, ends, counts, rank, y, w = pure
+            out, wsum, h = outs[0], None, None
+            need(w.dtype == _BF16 and out.dtype == _BF16, "combine dtypes")
+            cols = y.numel // ids.numel
+            tokens = out.numel // cols
+        k = ids.numel // tokens if tokens else 0
+        need(tokens > 0 and k > 0 and ids.numel == tokens * k and out.numel == tokens * cols and y.numel % cols == 0
+             and all(a.dtype == _I64 for a in (ids, ends, counts, rank)) and y.dtype == _BF16, "combine sizes")
+        return Plan("combine", dict(tokens=tokens, k=k, cols=cols, ids=ids.name, ends=ends.name, counts=counts.name,
+                                    rank=rank.name, y=y.name, w=w.name, wsum=wsum.name if wsum else None,
+                                    h=h.name if h else None, out=out.name))
+    if "div_sum" in name and len(pure) == 1 and len(outs) == 1:
+        k = sizes("r0_numel")
+        need(bool(k) and pure[0].dtype == _F32 and outs[0].dtype == _BF16 and pure[0].numel == outs[0].numel
+             and pure[0].numel % k == 0, "router weight normalisation")
+        return Plan("normalize_rows", dict(k=k, n=pure[0].numel, x=pure[0].name, y=outs[0].name))
+    if ("_sum_" in name or name.endswith("sum") or "fused_sum" in name) and len(pure) == 1 and len(outs) == 1 \
+            and pure[0].dtype == outs[0].dtype == _F32 and outs[0].numel > 1 and pure[0].numel % outs[0].numel == 0:
+        return Plan("row_sum", dict(rows=outs[0].numel, n=pure[0].numel, x=pure[0].name, y=outs[0].name))
+    if "fused_add_" in name and len(pure) == 2 and len(outs) == 1 and \
+            all(a.dtype == _BF16 and a.numel == outs[0].numel for a in pure + outs):
+        return Plan("add", dict(n=outs[0].numel, a=pure[0].name, b=pure[1].name, y=outs[0].name))
+    if "cat_mul_neg_slice" in name and "rsqrt" not in name and len(pure) == 3 and len(outs) == 1:
+        x, cs, sn = pure
+        tokens = cs.numel // 128
+        need(x.dtype == outs[0].dtype == _BF16 and cs.dtype == sn.dtype == _F32 and cs.numel == sn.numel == tokens * 128
+             and tokens > 0 and x.numel % (tokens * 128) == 0 and outs[0].numel == x.numel, "RoPE sizes")
+        return Plan("rope", dict(tokens=tokens, n=x.numel, x=x.name, cos=cs.name, sin=sn.name, y=outs[0].name))
+    if ("rsqrt" in name and "mean" in name and "_mm_" not in name and len(pure) == 3 and len(outs) == 1
+            and pure[0].numel == pure[1].numel == outs[0].numel and pure[2].numel < pure[0].numel
+            and all(a.dtype == _BF16 for a in pure + outs)):
+        x, a, w = pure
+        need(x.numel % w.numel == 0, "add + RMSNorm rows")
+        return Plan("rmsnorm_add", dict(rows=x.numel // w.numel, cols=w.numel, eps=1e-6, x=x.name, a=a.name, w=w.name,
+                                        y=outs[0].name))
+    return None
+
+
 def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
     """The HIP family and its parameters for one reference kernel."""
     names = _names(spec)
@@ -220,6 +377,10 @@ def resolve(spec: KernelSpec, source: str | None = None) -> Plan:
     def sizes(key):  # a size the kernel pins as a runtime scalar or as a constexpr
         v = sv.get(key, ce.get(key))
         return int(v) if v is not None else None
+
+    moe_plan = _moe_plan(spec, name, sizes)
+    if moe_plan is not None:
+        return moe_plan
 
     if "softmax" in name and len(ins) == 1 and len(outs) == 1:
         cols = sizes("r0_numel")
@@ -367,8 +528,60 @@ def run(plan: Plan, tensors: dict) -> None:
         else:
             ops.gemv_silu(t[p["x"]], w, t[p["res_a"]] if p["res_a"] else None,
                           t[p["res_b"]] if p["res_b"] else None, out=y)
+    elif f in _MOE_FAMILIES:
+        _run_moe(plan, t)
     else:
         raise UnsupportedKernel(f"unknown family {f}")
+
+
+_MOE_FAMILIES = {"fill_zero", "cast", "cumsum", "group_table", "count_le", "expert_count", "rank_select", "sort",
+                 "topk", "gather_rows", "rms_broadcast", "combine", "normalize_rows", "row_sum", "add", "rope",
+                 "rmsnorm_add", "grouped_mm"}
+
+
+def _run_moe(plan: Plan, t: dict) -> None:
+    from . import moe
+
+    p, f = plan.params, plan.family
+    if f == "fill_zero":
+        moe.fill_zero(t[p["y"]])
+    elif f == "cast":
+        moe.cast_i64_i32(t[p["x"]], t[p["y"]])
+    elif f == "cumsum":
+        moe.cumsum(t[p["x"]], t[p["y"]], t[p["y2"]] if p["y2"] else None)
+    elif f == "group_table":
+        moe.group_table(t[p["ends"]], t[p["nonempty"]], t[p["starts"]], t[p["rows"]])
+    elif f == "count_le":
+        moe.count_le(t[p["x"]], t[p["y"]])
+    elif f == "expert_count":
+        moe.expert_count(t[p["ids"]], t[p["counts"]], t[p["cum"]], t[p["counts2"]] if p["counts2"] else None)
+    elif f == "rank_select":
+        moe.rank_select(t[p["cum"]], t[p["ids"]], t[p["y"]])
+    elif f == "sort":
+        moe.sort_rows(t[p["x"]], t[p["v"]], t[p["i"]], p["rows"], p["descending"])
+    elif f == "topk":
+        moe.topk_rows(t[p["x"]], t[p["v"]], t[p["i"]], p["e"], p["k"], p["largest"])
+    elif f == "gather_rows":
+        moe.gather_rows(t[p["slot"]], t[p["x"]], t[p["y"]], p["k"], p["cols"])
+    elif f == "rms_broadcast":
+        moe.rms_broadcast(t[p["x"]], t[p["a"]], t[p["ss"]], t[p["w"]], t[p["y"]], p["eps"])
+    elif f == "combine":
+        moe.combine(t[p["ids"]], t[p["ends"]], t[p["counts"]], t[p["rank"]], t[p["y"]], t[p["w"]], t[p["out"]],
+                    p["tokens"], p["k"], p["cols"], wsum=t[p["wsum"]] if p["wsum"] else None,
+                    h=t[p["h"]] if p["h"] else None)
+    elif f == "normalize_rows":
+        moe.normalize_rows(t[p["x"]], t[p["y"]], p["k"])
+    elif f == "row_sum":
+        moe.row_sum(t[p["x"]], t[p["y"]])
+    elif f == "add":
+        moe.add(t[p["a"]], t[p["b"]], t[p["y"]])
+    elif f == "rope":
+        moe.rope(t[p["x"]], t[p["cos"]], t[p["sin"]], t[p["y"]], p["tokens"])
+    elif f == "rmsnorm_add":
+        moe.rmsnorm_add(t[p["x"]], t[p["a"]], t[p["w"]], t[p["y"]], p["eps"])
+    elif f == "grouped_mm":
+        moe.grouped_gemm(t[p["a"]], t[p["b"]], t[p["group"]], t[p["start"]], t[p["rows"]], t[p["c"]], p["k"], p["n"],
+                         p["stride"])
 
 
 def launch(spec: KernelSpec, tensors: dict, source: str | None = None) -> Plan:
@@ -423,4 +636,41 @@ def work_of(plan: Plan) -> tuple:
         extra = {"plain": 0, "rms": 2 * k + 4 + (2 * k if p.get("add") else 0),
                  "silu": 2 * n * ((1 if p.get("res_a") else 0) + (1 if p.get("res_b") else 0))}[p["mode"]]
         return 2.0 * k * n, 2.0 * (k * n + xk + n) + extra
+    # the MoE kernels: bytes each must move (index tables at their width), flops where they compute
+    if f == "grouped_mm":   # every row of A through one weight; each program's weight read once
+        r, k, n = p["a_rows"], p["k"], p["n"]
+        return 2.0 * r * k * n, 2.0 * (r * k + r * n + min(p["nprog"], p["nweights"]) * k * n)
+    if f in ("fill_zero", "cast", "cumsum", "count_le"):
+        n = p.get("n", p.get("m", 1))
+        return float(n), 12.0 * n
+    if f == "group_table":
+        return float(p["n"]), 32.0 * p["n"]
+    if f == "expert_count":
+        return float(p["r"] * p["e"]), 8.0 * (p["r"] + p["r"] * p["e"] + p["e"])
+    if f == "rank_select":
+        return float(p["r"]), 24.0 * p["r"]
+    if f == "sort":
+        n = p["rows"] * p["e"]
+        return n * max(1.0, math.log2(max(p["e"], 2))), 24.0 * n
+    if f == "topk":
+        return float(p["k"]) * p["e"] * 2, 4.0 * p["e"] + 12.0 * p["k"]
+    if f == "gather_rows":
+        return 0.0, 2.0 * 2 * p["r"] * p["cols"] + 8.0 * p["r"]
+    if f == "rms_broadcast":
+        return 4.0 * p["rows"] * p["cols"], 2.0 * (3 * p["cols"] + p["rows"] * p["cols"]) + 4.0
+    if f == "combine":
+        tk, c = p["tokens"] * p["k"], p["cols"]
+        res = 3 if p["h"] else 1
+        return 2.0 * tk * c, 2.0 * (tk * c + res * p["tokens"] * c) + 32.0 * tk
+    if f == "normalize_rows":
+        return 2.0 * p["n"], 6.0 * p["n"]
+    if f == "row_sum":
+        return float(p["n"]), 4.0 * (p["n"] + p["rows"])
+    if f == "add":
+        return float(p["n"]), 6.0 * p["n"]
+    if f == "rope":
+        return 3.0 * p["n"], 4.0 * p["n"] + 8.0 * 128 * p["tokens"]
+    if f == "rmsnorm_add":
+        n = p["rows"] * p["cols"]
+        return 5.0 * n, 6.0 * n + 2.0 * p["cols"]
     raise UnsupportedKernel(f"unknown family {f}")

@@ -4,15 +4,23 @@
 Run in a container that has the reference checkout (default /root/reference).  It parses the
 bundle's manifest.json and *_spec.py files with ptb_amd.bundle (ast, nothing imported or executed)
 and stores per kernel only data: name, args (name, role, dtype, flat shape), grid, scalars,
-constexprs, the launch count, the family that serves it (null when none does), and the index facts
-the HIP families otherwise read from the Triton source (``extra.hints``).  The GPU tests and the
-validation runner (``--manifests``) read these manifests where the bundle itself is absent.
+constexprs, the launch count, the family that serves it (null when none does), the index facts
+the HIP families otherwise read from the Triton source (``extra.hints``) and the arguments the
+spec takes from its recorded inputs (``extra.recorded``).  The GPU tests and the validation runner
+(``--manifests``) read these manifests where the bundle itself is absent.
+
+The recorded inputs themselves (the MoE kernels' index tables, ``*_inputs.pt`` beside their specs,
+loaded with ``torch.load(weights_only=True)``) go to ``recorded_inputs.npz`` as plain int arrays
+keyed ``<workload>/<kernel dir>/<arg>``.
 """
 import gzip
 import json
 import os
 import sys
 from pathlib import Path
+
+import numpy as np
+import torch
 
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parents[1] / "pytorchsim-triton-backend_amd"))
@@ -23,6 +31,7 @@ from ptb_amd import bundle, kernels  # noqa: E402
 def main(ref="/root/reference"):
     root = os.path.join(ref, "validation", "pytorchsim")
     out = {}
+    recorded = {}
     for name in sorted(os.listdir(root)):
         if not os.path.isfile(os.path.join(root, name, "manifest.json")):
             continue
@@ -35,6 +44,10 @@ def main(ref="/root/reference"):
             except kernels.UnsupportedKernel:
                 plan = None
             man["extra"] = {"hints": kernels.kernel_hints(plan) if plan else {}}
+            if (bk.spec.extra or {}).get("recorded"):
+                man["extra"]["recorded"] = list(bk.spec.extra["recorded"])
+                for arg, val in torch.load(_inputs_pt(root, name, bk.dir), weights_only=True).items():
+                    recorded[f"{name}/{bk.dir}/{arg}"] = val.numpy()
             man["launches"] = bk.launches
             man["dir"] = bk.dir
             man["family"] = plan.family if plan else None
@@ -45,6 +58,17 @@ def main(ref="/root/reference"):
     with gzip.GzipFile(path, "wb", mtime=0) as fh:
         fh.write((json.dumps(out, indent=0, sort_keys=True) + "\n").encode())
     print(f"wrote {path} ({len(out)} workloads)")
+    rpath = HERE / "recorded_inputs.npz"
+    np.savez_compressed(rpath, **dict(sorted(recorded.items())))
+    print(f"wrote {rpath} ({len(recorded)} arrays)")
+
+
+def _inputs_pt(root, workload, kernel_dir):
+    d = os.path.join(root, workload, kernel_dir)
+    pts = [f for f in os.listdir(d) if f.endswith("_inputs.pt")]
+    if len(pts) != 1:
+        raise ValueError(f"{d}: expected one *_inputs.pt, found {pts}")
+    return os.path.join(d, pts[0])
 
 
 if __name__ == "__main__":

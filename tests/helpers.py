@@ -28,7 +28,8 @@ def assert_close(got, want, rtol, atol, what=""):
 
 
 def bits_equal(got, want):
-    """Exact equality of the stored bits (bf16/fp8/int tensors)."""
+    """Exact equality of the stored bits (any dtype: floats compared as their bit patterns, so NaN
+    payloads and the sign of zero count)."""
     a, b = got.detach().cpu().contiguous(), want.detach().cpu().contiguous()
     if a.dtype != b.dtype or a.shape != b.shape:
         return False
@@ -36,4 +37,8 @@ def bits_equal(got, want):
         return torch.equal(a.view(torch.int16), b.view(torch.int16))
     if a.element_size() == 1:
         return torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+    if a.element_size() == 4:
+        return torch.equal(a.view(torch.int32), b.view(torch.int32))
+    if a.element_size() == 8:
+        return torch.equal(a.view(torch.int64), b.view(torch.int64))
     return torch.equal(a, b)

@@ -19,6 +19,11 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 MANIFESTS = bundle.read_manifests(GOLDEN / "bundle_manifests.json.gz")
+RECORDED = GOLDEN / "recorded_inputs.npz"
+
+
+def plan_family(spec):
+    return kernels.resolve(spec).family
 
 
 def _unique_cases():
@@ -123,15 +128,88 @@ def check_against_oracle(plan, host, got):
         finite = want.float().isfinite()
         scale = float(want.float()[finite].abs().mean()) + 1e-6 if bool(finite.any()) else 1.0
         assert_close(got[p["y"]], want, 2e-2, 2e-2 * scale, f"gemv {p['mode']}")
+    elif f in MOE_FAMILIES:
+        check_moe_against_oracle(plan, host, got)
     else:
         raise AssertionError(f"no oracle for {f}")
+
+
+MOE_FAMILIES = {"fill_zero", "cast", "cumsum", "group_table", "count_le", "expert_count", "rank_select", "sort",
+                "topk", "gather_rows", "rms_broadcast", "combine", "normalize_rows", "row_sum", "add", "rope",
+                "rmsnorm_add", "grouped_mm"}
+
+
+def check_moe_against_oracle(plan, host, got):
+    """The MoE layer's kernels (integer and index results exact, bf16 within 2e-2 of the output's
+    scale); `host` holds every argument's initial value (inout included)."""
+    p, f = plan.params, plan.family
+    if f == "fill_zero":
+        assert not got[p["y"]].any()
+    elif f == "cast":
+        assert torch.equal(got[p["y"]], oracle.cast_i64_i32(host[p["x"]]))
+    elif f == "cumsum":
+        want = oracle.cumsum_int(host[p["x"]], got[p["y"]].dtype)
+        assert torch.equal(got[p["y"]], want) and (not p["y2"] or torch.equal(got[p["y2"]], want))
+    elif f == "group_table":
+        for name, want in zip(("nonempty", "starts", "rows"), oracle.group_table(host[p["ends"]])):
+            assert torch.equal(got[p[name]], want), name
+    elif f == "count_le":
+        assert torch.equal(got[p["y"]], oracle.count_le(host[p["x"]], p["m"]))
+    elif f == "expert_count":
+        counts, cum = oracle.expert_count(host[p["ids"]], p["e"])
+        assert torch.equal(got[p["counts"]], counts) and torch.equal(got[p["cum"]], cum)
+        if p["counts2"]:
+            assert torch.equal(got[p["counts2"]], counts)
+    elif f == "rank_select":
+        assert torch.equal(got[p["y"]], oracle.rank_select(host[p["cum"]], host[p["ids"]], p["e"]))
+    elif f == "sort":
+        v, i = oracle.sort_rows(host[p["x"]], p["rows"], p["descending"])
+        assert torch.equal(got[p["i"]], i) and bits_equal(got[p["v"]], v)
+    elif f == "topk":
+        v, i = oracle.topk_rows(host[p["x"]], p["e"], p["k"], p["largest"])
+        assert torch.equal(got[p["i"]], i) and torch.equal(got[p["v"]], v)
+    elif f == "gather_rows":
+        assert bits_equal(got[p["y"]], oracle.gather_rows(host[p["slot"]], host[p["x"]], p["k"], p["cols"]))
+    elif f == "rms_broadcast":
+        want = oracle.rms_broadcast(host[p["x"]], host[p["a"]], host[p["ss"]], host[p["w"]], p["rows"], p["eps"])
+        assert_close(got[p["y"]], want, 2e-2, 2e-2, "rms_broadcast")
+    elif f == "combine":
+        io = host[p["out"]] if p["h"] else None
+        want = oracle.combine(host[p["ids"]], host[p["ends"]], host[p["counts"]], host[p["rank"]], host[p["y"]],
+                              host[p["w"]], p["tokens"], p["k"], p["cols"],
+                              wsum=host[p["wsum"]] if p["wsum"] else None, h=host[p["h"]] if p["h"] else None, io=io)
+        finite = want.float().isfinite()
+        scale = float(want.float()[finite].abs().mean()) + 1e-6 if bool(finite.any()) else 1.0
+        assert_close(got[p["out"]], want, 2e-2, 2e-2 * scale, "combine")
+    elif f == "normalize_rows":
+        assert_close(got[p["y"]], oracle.normalize_rows(host[p["x"]], p["k"]), 2e-2, 2e-2, "normalize_rows")
+    elif f == "row_sum":
+        want = oracle.row_sum(host[p["x"]], p["rows"])
+        bound = 1e-6 * host[p["x"]].float().abs().reshape(p["rows"], -1).sum(1) + 1e-6
+        assert bool(((got[p["y"]] - want).abs() <= bound).all())
+    elif f == "add":
+        assert bits_equal(got[p["y"]], oracle.add_bf16(host[p["a"]], host[p["b"]]))
+    elif f == "rope":
+        want = oracle.rope(host[p["x"]], host[p["cos"]], host[p["sin"]], p["tokens"])
+        assert_close(got[p["y"]], want, 2e-2, 2e-2, "rope")
+    elif f == "rmsnorm_add":
+        want = oracle.rmsnorm_add(host[p["x"]], host[p["a"]], host[p["w"]], p["eps"])
+        assert_close(got[p["y"]], want, 2e-2, 2e-2, "rmsnorm_add")
+    elif f == "grouped_mm":
+        want = oracle.grouped_mm(host[p["a"]], host[p["b"]], host[p["group"]], host[p["start"]], host[p["rows"]],
+                                 p["k"], p["n"], p["stride"], c=host[p["c"]])
+        finite = want.float().isfinite()
+        scale = float(want.float()[finite].abs().mean()) + 1e-6 if bool(finite.any()) else 1.0
+        assert_close(got[p["c"]], want, 2e-2, 2e-2 * scale, "grouped_mm")
 
 
 @pytest.mark.parametrize("workload,index", CASES)
 def test_bundle_kernel_through_launcher(workload, index):
     man = MANIFESTS[workload]["kernels"][index]
     spec = contract.spec_from_manifest(man)
-    host = contract.seeded_inputs(spec, torch, seed=0)
+    rec = bundle.read_recorded(RECORDED, workload, man["dir"]) if man["extra"].get("recorded") else None
+    host = contract.seeded_inputs(spec, torch, seed=0, recorded=rec)
+    print(f"[case] {workload}/{man['dir']} {plan_family(spec)}", flush=True)
     dev = {a.name: (host[a.name].cuda() if a.name in host
                     else torch.empty(a.numel, dtype=getattr(torch, a.dtype), device="cuda")) for a in spec.args}
     plan = launcher.launch(spec, dev, grid=tuple(man["grid"]))
