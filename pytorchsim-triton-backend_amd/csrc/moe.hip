@@ -9,6 +9,8 @@
 // device_assert, these write zeros for the offending element instead of reading out of bounds.
 #include "ptb_common.h"
 
+#include <type_traits>
+
 using namespace ptb;
 
 namespace {
@@ -127,14 +129,20 @@ __global__ __launch_bounds__(kScanThreads) void group_table_block(const InT* __r
   }
 }
 
-// out[i] = number of r with x[r] <= i, for i < m.
+// out[i] = number of r with x[r] <= i, for i < m: x staged through LDS in blocks of kB values.
 __global__ __launch_bounds__(kB) void count_le(const int64_t* __restrict__ x, int64_t n, int32_t* __restrict__ out,
                                                int64_t m) {
+  __shared__ int64_t xs[kB];
   const int64_t i = int64_t(blockIdx.x) * kB + threadIdx.x;
-  if (i >= m) return;
   int64_t c = 0;
-  for (int64_t r = 0; r < n; ++r) c += x[r] <= i ? 1 : 0;
-  out[i] = int32_t(c);
+  for (int64_t r0 = 0; r0 < n; r0 += kB) {
+    const int64_t cnt = n - r0 < kB ? n - r0 : kB;
+    if (threadIdx.x < cnt) xs[threadIdx.x] = x[r0 + threadIdx.x];
+    __syncthreads();
+    for (int j = 0; j < cnt; ++j) c += xs[j] <= i ? 1 : 0;
+    __syncthreads();
+  }
+  if (i < m) out[i] = int32_t(c);
 }
 
 // ---------------------------------------------------------------- expert histogram and ranks
@@ -212,31 +220,169 @@ __device__ __forceinline__ void store_sorted(void* v, int64_t* idx, int64_t at, 
   idx[at] = pos;
 }
 __device__ __forceinline__ bool key_less(int64_t ka, int32_t ia, int64_t kb, int32_t ib) {
-  return ka < kb || (ka == kb && ia < ib);
+  return (ka < kb) | ((ka == kb) & (ia < ib));   // bitwise: no short-circuit branches
 }
 
 constexpr int kSortChunk = 8192;   // elements one workgroup sorts in LDS (96 KB)
-// Bitonic sort of chunk blockIdx.y of row blockIdx.x (chunk length p, a power of two <= kSortChunk;
-// positions past e pad with the largest key).  final_out: write values + indices of the row,
-// else write (key, position) pairs to the workspace for the merge passes.
-__global__ __launch_bounds__(1024) void sort_chunk(const void* __restrict__ x, int64_t e, int p, bool is_f32,
-                                                   bool desc, bool final_out, void* __restrict__ v,
-                                                   int64_t* __restrict__ idx, int64_t* __restrict__ wk,
-                                                   int32_t* __restrict__ wi) {
-  __shared__ int64_t key[kSortChunk];
-  __shared__ int32_t pos[kSortChunk];
+constexpr int kSortThreads = 1024;
+
+// Bitonic network over p = kSortThreads * R elements held R per thread (element g = tid*R + r):
+// strides below R run in registers, the rest exchange through LDS.  Elements are unsigned words
+// whose order is the wanted (key, position) order, so each step is one min / max.
+// LDS slot of element g: one pad word after every 8, so the R = 8 words a thread writes (and the
+// partner words it reads) fall in distinct banks across the wave.
+__device__ __forceinline__ int lds_slot(int g) { return g + (g >> 3); }
+
+template <typename W, int R>
+__device__ __forceinline__ void bitonic_packed(W (&v)[R], W* lds, int p) {
+  const int base = threadIdx.x * R;
+  for (int size = 2; size <= p; size <<= 1) {
+    // strides of size/2 .. R: partners in other threads, through LDS
+    for (int stride = size >> 1; stride >= R; stride >>= 1) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) lds[lds_slot(base + r)] = v[r];
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int g = base + r;
+        const W o = lds[lds_slot(g ^ stride)];
+        const bool keep_min = ((g & stride) == 0) == ((g & size) == 0);
+        const W lo = v[r] < o ? v[r] : o, hi = v[r] < o ? o : v[r];
+        v[r] = keep_min ? lo : hi;
+      }
+      __syncthreads();
+    }
+    // strides below R: partners in this thread's registers (compile-time indices)
+#pragma unroll
+    for (int st = R / 2; st > 0; st >>= 1) {
+      if (st < size) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (r & st) continue;
+          const bool up = ((base + r) & size) == 0;
+          const W a = v[r], b = v[r | st];
+          const W lo = a < b ? a : b, hi = a < b ? b : a;
+          v[r] = up ? lo : hi;
+          v[r | st] = up ? hi : lo;
+        }
+      }
+    }
+  }
+}
+
+// Sort one chunk of p (power of two, <= kSortChunk) elements of row blockIdx.x, chunk blockIdx.y.
+// When the chunk's keys span a small enough range the (key, position) pair is packed into one
+// 32-bit word (key range < 2^(32 - log2 p): expert ids) or one 64-bit word (range < 2^32: floats,
+// int32-sized integers), and sorted as plain unsigned words in registers + LDS; any other int64
+// keys take the general compare-exchange over separate key / position arrays.  final_out: write
+// values + indices of the row, else (key, position) pairs to the workspace for the merge passes.
+__global__ __launch_bounds__(kSortThreads) void sort_chunk(const void* __restrict__ x, int64_t e, int p, bool is_f32,
+                                                           bool desc, bool final_out, void* __restrict__ v,
+                                                           int64_t* __restrict__ idx, int64_t* __restrict__ wk,
+                                                           int32_t* __restrict__ wi) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[kSortChunk * 12];   // >= (8192 + 1024) * 8 B packed
+  __shared__ int64_t red_min[kSortThreads / kWave], red_max[kSortThreads / kWave];
+  int64_t* key = reinterpret_cast<int64_t*>(lds_raw);
+  int32_t* pos = reinterpret_cast<int32_t*>(lds_raw + kSortChunk * 8);
   const int64_t row = blockIdx.x, c0 = int64_t(blockIdx.y) * p;
   const void* xr = is_f32 ? static_cast<const void*>(static_cast<const float*>(x) + row * e)
                           : static_cast<const void*>(static_cast<const int64_t*>(x) + row * e);
-  for (int i = threadIdx.x; i < p; i += 1024) {
+  // keys (padding past e with the largest key) and their range over the chunk's live elements
+  int64_t kmin = INT64_MAX, kmax = INT64_MIN;
+  constexpr int kPer = kSortChunk / kSortThreads;   // every load of the chunk issued before the first use
+  int64_t kk[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int i = threadIdx.x + q * kSortThreads;
     const int64_t g = c0 + i;
-    key[i] = g < e ? sort_key(xr, g, is_f32, desc) : INT64_MAX;
-    pos[i] = int32_t(g);
+    kk[q] = (i < p && g < e) ? sort_key(xr, g, is_f32, desc) : INT64_MAX;
   }
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int i = threadIdx.x + q * kSortThreads;
+    if (i < p) {
+      key[i] = kk[q];
+      if (c0 + i < e) {
+        kmin = kk[q] < kmin ? kk[q] : kmin;
+        kmax = kk[q] > kmax ? kk[q] : kmax;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int64_t a = __shfl_xor(kmin, off, kWave), b = __shfl_xor(kmax, off, kWave);
+    kmin = a < kmin ? a : kmin;
+    kmax = b > kmax ? b : kmax;
+  }
+  if (threadIdx.x % kWave == 0) {
+    red_min[threadIdx.x / kWave] = kmin;
+    red_max[threadIdx.x / kWave] = kmax;
+  }
+  __syncthreads();
+  kmin = red_min[0];
+  kmax = red_max[0];
+  for (int w = 1; w < kSortThreads / kWave; ++w) {
+    kmin = red_min[w] < kmin ? red_min[w] : kmin;
+    kmax = red_max[w] > kmax ? red_max[w] : kmax;
+  }
+  int pbits = 0;
+  while ((1 << pbits) < p) ++pbits;
+  // range + 1 distinct key codes, one more for the padding: code = key - kmin, padding = range + 1
+  const uint64_t range = kmax >= kmin ? uint64_t(kmax) - uint64_t(kmin) : 0;
+  const int mode = (p >= kSortThreads && p % kSortThreads == 0)
+                       ? (range + 1 < (uint64_t(1) << (32 - pbits)) ? 1 : (range + 1 < (uint64_t(1) << 32) ? 2 : 0))
+                       : 0;
+  const auto emit = [&](int i, int64_t k, int32_t ps) __attribute__((always_inline)) {
+    const int64_t g = c0 + i;
+    if (final_out) {
+      if (g < e) store_sorted(static_cast<uint8_t*>(v) + row * e * (is_f32 ? 4 : 8), idx + row * e, g, k, ps, is_f32, desc);
+    } else {
+      wk[row * int64_t(gridDim.y) * p + g] = k;
+      wi[row * int64_t(gridDim.y) * p + g] = ps;
+    }
+  };
+  if (mode == 1 || mode == 2) {
+    const int r_per = p / kSortThreads;   // 1 .. 8
+    __syncthreads();                      // keys complete before the packed words overwrite them
+    const auto run = [&](auto tag, auto rtag) __attribute__((always_inline)) {
+      using W = decltype(tag);
+      constexpr int R = decltype(rtag)::value;
+      W w[R];
+      const int shift = mode == 1 ? pbits : 32;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x * R + r;
+        const int64_t g = c0 + i;
+        const uint64_t code = g < e ? uint64_t(key[i]) - uint64_t(kmin) : range + 1;
+        w[r] = W((code << shift) | uint64_t(i));
+      }
+      __syncthreads();
+      bitonic_packed<W, R>(w, reinterpret_cast<W*>(lds_raw), p);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x * R + r;
+        const uint64_t u = uint64_t(w[r]);
+        const int32_t local = int32_t(u & ((uint64_t(1) << shift) - 1));
+        const uint64_t code = u >> shift;
+        const int64_t k = code > range ? INT64_MAX : int64_t(uint64_t(kmin) + code);
+        emit(i, k, int32_t(c0 + local));
+      }
+    };
+    const auto dispatch_r = [&](auto tag) __attribute__((always_inline)) {
+      if (r_per == 1) run(tag, std::integral_constant<int, 1>{});
+      else if (r_per == 2) run(tag, std::integral_constant<int, 2>{});
+      else if (r_per == 4) run(tag, std::integral_constant<int, 4>{});
+      else run(tag, std::integral_constant<int, 8>{});
+    };
+    if (mode == 1) dispatch_r(uint32_t{});
+    else dispatch_r(uint64_t{});
+    return;
+  }
+  for (int i = threadIdx.x; i < p; i += kSortThreads) pos[i] = int32_t(c0 + i);
   __syncthreads();
   for (int size = 2; size <= p; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = threadIdx.x; t < p / 2; t += 1024) {
+      for (int t = threadIdx.x; t < p / 2; t += kSortThreads) {
         const int lo = 2 * t - (t & (stride - 1));   // t with a zero bit inserted at `stride`
         const int hi = lo + stride;
         const bool up = (lo & size) == 0;
@@ -250,16 +396,7 @@ __global__ __launch_bounds__(1024) void sort_chunk(const void* __restrict__ x, i
       __syncthreads();
     }
   }
-  for (int i = threadIdx.x; i < p; i += 1024) {
-    const int64_t g = c0 + i;
-    if (final_out) {
-      if (g < e) store_sorted(static_cast<uint8_t*>(v) + row * e * (is_f32 ? 4 : 8), idx + row * e, g, key[i], pos[i],
-                              is_f32, desc);
-    } else {
-      wk[row * int64_t(gridDim.y) * p + g] = key[i];
-      wi[row * int64_t(gridDim.y) * p + g] = pos[i];
-    }
-  }
+  for (int i = threadIdx.x; i < p; i += kSortThreads) emit(i, key[i], pos[i]);
 }
 
 // One merge pass over runs of length run (a power of two): each element finds its place in the
@@ -299,50 +436,41 @@ __global__ __launch_bounds__(kB) void sort_emit(const int64_t* __restrict__ sk, 
 }
 
 // ---------------------------------------------------------------- top-k
-// One wave per row: lane l holds elements l, l + 64, ...; each round takes the largest (smallest)
-// value, the lowest position among equal values, and marks it spent with -inf (+inf).
-constexpr int kTopkPer = 16;   // rows of up to 1024 elements
+// One wave per row, the row in LDS: element c's rank is the number of elements ordered before it
+// (larger -- smaller for largest = false -- or equal at a lower position); the elements of rank < k
+// are the k selected, in order.  This is the order the reference's k rounds of "take the best,
+// lowest position first, mark it spent" produce.
+constexpr int kTopkMax = 1024;   // row length
+constexpr int kTopkRows = kB / kWave;
 __global__ __launch_bounds__(kB) void topk_rows(const float* __restrict__ x, int64_t rows, int e, int k, bool largest,
                                                 float* __restrict__ vals, int64_t* __restrict__ idx) {
-  const int64_t row = int64_t(blockIdx.x) * (kB / kWave) + threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  if (row >= rows) return;
-  const float spent = largest ? -INFINITY : INFINITY;
-  float v[kTopkPer];
+  __shared__ __attribute__((aligned(16))) float sx[kTopkRows][kTopkMax];
+  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t row = int64_t(blockIdx.x) * kTopkRows + w;
+  if (row >= rows) return;   // a whole wave; no block barrier below
+  float* r = sx[w];
+  // smallest-k is largest-k of the negated values (negation reverses the order, keeps ties)
+  const float sgn = largest ? 1.0f : -1.0f;
+  const int e4 = (e + 3) & ~3;   // padded with -inf, which never ranks before a real element
+  for (int c = lane; c < e4; c += kWave) r[c] = c < e ? sgn * x[row * e + c] : -INFINITY;
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  const f32x4v* r4 = reinterpret_cast<const f32x4v*>(r);
+  for (int c = lane; c < e; c += kWave) {
+    const float v = r[c];
+    int rank = 0;
+#pragma unroll 8
+    for (int q = 0; q < e4 / 4; ++q) {
+      const f32x4v o = r4[q];
 #pragma unroll
-  for (int i = 0; i < kTopkPer; ++i) {
-    const int c = lane + i * kWave;
-    v[i] = c < e ? x[row * e + c] : spent;
-  }
-  for (int n = 0; n < k; ++n) {
-    float best = spent;
-    int at = 1 << 30;
-#pragma unroll
-    for (int i = 0; i < kTopkPer; ++i) {
-      const int c = lane + i * kWave;
-      const bool better = largest ? v[i] > best : v[i] < best;
-      if (c < e && (better || (v[i] == best && c < at))) {
-        best = v[i];
-        at = c;
+      for (int t = 0; t < 4; ++t) {
+        const int j = 4 * q + t;
+        rank += int((o[t] > v) | ((o[t] == v) & (j < c)));   // bitwise: no short-circuit branches
       }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ob = __shfl_xor(best, off, kWave);
-      const int oa = __shfl_xor(at, off, kWave);
-      const bool better = largest ? ob > best : ob < best;
-      if (better || (ob == best && oa < at)) {
-        best = ob;
-        at = oa;
-      }
+    if (rank < k) {
+      vals[row * k + rank] = sgn * v;
+      idx[row * k + rank] = c;
     }
-    if (lane == 0) {
-      vals[row * k + n] = best;
-      idx[row * k + n] = at < e ? at : e;
-    }
-#pragma unroll
-    for (int i = 0; i < kTopkPer; ++i)
-      if (lane + i * kWave == at) v[i] = spent;
   }
 }
 
@@ -594,7 +722,7 @@ PTB_EXPORT int ptb_count_le(const int64_t* x, int64_t n, int32_t* out, int64_t m
   if (n < 0 || m < 0) return PTB_ERR_SHAPE;
   if (m == 0) return PTB_OK;
   if (!out || (n > 0 && !x)) return PTB_ERR_NULL;
-  count_le<<<blocks_for(m, kB, 1 << 30), kB, 0, static_cast<hipStream_t>(stream)>>>(x, n, out, m);
+  count_le<<<blocks_for(m, kB, 1 << 30), kB, 0, static_cast<hipStream_t>(stream)>>>(x, n, out, m);   // n may be 0
   return launch_status();
 }
 
@@ -667,8 +795,8 @@ PTB_EXPORT int ptb_topk_rows_f32(const float* x, int64_t rows, int64_t e, int64_
   if (rows < 0 || e < 0 || k < 0) return PTB_ERR_SHAPE;
   if (rows == 0 || k == 0) return PTB_OK;
   if (!x || !values || !indices) return PTB_ERR_NULL;
-  if (e > kTopkPer * kWave || k > e) return PTB_ERR_UNSUPPORTED;
-  const int64_t blocks = (rows + kB / kWave - 1) / (kB / kWave);
+  if (e > kTopkMax || k > e) return PTB_ERR_UNSUPPORTED;
+  const int64_t blocks = (rows + kTopkRows - 1) / kTopkRows;
   if (blocks > 0x7fffffff) return PTB_ERR_GRID;
   topk_rows<<<dim3(unsigned(blocks)), kB, 0, static_cast<hipStream_t>(stream)>>>(x, rows, int(e), int(k), largest != 0,
                                                                                values, indices);

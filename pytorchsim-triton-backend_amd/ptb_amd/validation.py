@@ -29,12 +29,14 @@ MI355X = {"name": "MI355X (gfx950)", "peak_bf16_tflops": 2500.0, "peak_fp8_tflop
 SUITES = tuple(bundle.SUITE_KEYS)
 
 
-def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0, settle: float = 0.02, graph: bool = True) -> dict:
-    """Run one bundle kernel on the GPU and time it; returns its record."""
+def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0, settle: float = 0.02, graph: bool = True,
+                recorded: dict | None = None) -> dict:
+    """Run one bundle kernel on the GPU and time it; returns its record.  `recorded` holds the
+    arguments the spec takes from its recorded inputs (the MoE kernels' index tables)."""
     import torch
 
     plan = kernels.resolve(bk.spec, bk.source)
-    host = contract.seeded_inputs(bk.spec, torch, seed)
+    host = contract.seeded_inputs(bk.spec, torch, seed, recorded=recorded)
     tensors = {}
     for a in bk.spec.args:
         if a.name in host:
@@ -87,14 +89,33 @@ def _time(fn, torch) -> float:
     return e0.elapsed_time(e1) * 1e3
 
 
-def run_workload(w, reps: int = 20, warmup: int = 3, settle: float = 0.02, graph: bool = True) -> dict:
+def _recorded_for(w, bk, recorded_path):
+    """The recorded inputs of one kernel: from a recorded-inputs file, or from the ``*_inputs.pt``
+    beside the spec when the workload was read from the bundle itself."""
+    if not (bk.spec.extra or {}).get("recorded"):
+        return None
+    if recorded_path:
+        return bundle.read_recorded(recorded_path, w.name, bk.dir)
+    if w.path:
+        import torch
+
+        d = os.path.join(w.path, bk.dir)
+        pts = [f for f in os.listdir(d) if f.endswith("_inputs.pt")]
+        if len(pts) == 1:
+            return torch.load(os.path.join(d, pts[0]), weights_only=True)
+    raise FileNotFoundError(f"{w.name}/{bk.dir}: recorded inputs needed (--recorded)")
+
+
+def run_workload(w, reps: int = 20, warmup: int = 3, settle: float = 0.02, graph: bool = True,
+                 recorded_path: str | None = None) -> dict:
     got = dict(w.keys, kernel=w.name, rc=0, failed_step=None, kernels=[])
     t0 = time.monotonic()
     step = "resolve"
     try:
         for bk in w.kernels:
             step = bk.dir
-            got["kernels"].append(time_kernel(bk, reps, warmup, settle=settle, graph=graph))
+            got["kernels"].append(time_kernel(bk, reps, warmup, settle=settle, graph=graph,
+                                              recorded=_recorded_for(w, bk, recorded_path)))
         got["us"] = sum(k["us"] * k["launches"] for k in got["kernels"])
         got["roofline_us"] = sum(k["roofline_us"] * k["launches"] for k in got["kernels"])
     except Exception as e:  # noqa: BLE001 - a workload's failure is recorded, never lost
@@ -147,6 +168,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--settle", type=float, default=0.02, help="seconds of back-to-back launches before timing")
     ap.add_argument("--eager", action="store_true", help="time Python launches only (no HIP graph replay)")
+    ap.add_argument("--recorded", help="recorded-inputs file (.npz) for kernels whose specs take recorded inputs")
     args = ap.parse_args(argv)
     if args.merge:
         return merge(args.merge, args.out)
@@ -170,7 +192,7 @@ def main(argv=None) -> int:
     done = []
     write_results(args.out, args.suite, done, len(ws), part)
     for w in ws:
-        r = run_workload(w, args.reps, args.warmup, args.settle, graph=not args.eager)
+        r = run_workload(w, args.reps, args.warmup, args.settle, graph=not args.eager, recorded_path=args.recorded)
         done.append(r)
         write_results(args.out, args.suite, done, len(ws), part)
         print(f"{w.name}: rc={r['rc']} us={r.get('us', float('nan')):.1f}", flush=True)
