@@ -116,6 +116,15 @@ int ptb_slice_add_bf16(const void* x, float* out, int64_t first, int64_t count, 
 int ptb_gemm_bf16(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n,
                   int64_t k, void* stream);
 
+/* The same GEMM with a caller workspace for split-K: when the 128x128 output tiles would fill at
+ * most a quarter of the CUs (and K >= 512), K is cut into slices multiplied by separate workgroups into
+ * fp32 partials that a finish pass sums (+ residual) and rounds once.  ptb_gemm_bf16_workspace_bytes
+ * is 0 for shapes that do not split; then ptb_gemm_bf16_ws is ptb_gemm_bf16.
+ * Replaces: the same kernels as ptb_gemm_bf16 (the small M x N gemm_<M>x<K>x<N>_bf16 shapes). */
+size_t ptb_gemm_bf16_workspace_bytes(int64_t m, int64_t n, int64_t k);
+int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n, int64_t k,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 /* Per-row dynamic e4m3 quantisation of bf16 activations: scale[r] = max_c |x[r,c]| / 448,
  * xq[r,c] = e4m3fn(x[r,c] / scale[r]) (round to nearest even; an all-zero row gets scale 1).
  * Semantics: tests/cases/mechanism/ops/ops_fp8_e4m3_dot.py:41-44 (the e4m3 cast) and

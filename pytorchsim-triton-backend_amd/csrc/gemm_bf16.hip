@@ -78,10 +78,15 @@ struct Groups {
 };
 constexpr int kMaxPrograms = 256;
 
-template <int WM, int WN, bool RESID, bool GROUPED>
+// Split-K mode: workgroup (tile, blockIdx.y = s) multiplies K columns [s*kchunk, s*kchunk + kchunk)
+// and stores its fp32 partial tile at part + s*M*N; splitk_finish sums the partials.
+enum { kPlain = 0, kGrouped = 1, kSplit = 2 };
+
+template <int WM, int WN, bool RESID, int MODE>
 __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A_in, const uint16_t* __restrict__ B_in, const uint16_t* __restrict__ R,
-    uint16_t* __restrict__ C_in, int M_in, int N, int K, int tiles_m, int tiles_n, Groups gp) {
+    uint16_t* __restrict__ C_in, int M_in, int N, int K, int tiles_m, int tiles_n, Groups gp,
+    float* __restrict__ part, int kchunk) {
   using Sh = Shape<WM, WN>;
   constexpr int BM = Sh::BM, BN = Sh::BN, kABytes = Sh::kABytes, kStageBytes = Sh::kStageBytes;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStageBytes];
@@ -91,7 +96,8 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   const uint16_t* B = B_in;
   uint16_t* C = C_in;
   int M = M_in, m0, n0;
-  if constexpr (GROUPED) {
+  int Kl = K;    // the K columns this workgroup multiplies
+  if constexpr (MODE == kGrouped) {
     __shared__ int pref[kMaxPrograms + 1];
     __shared__ int wsum[kThreads / 64];
     const int t = threadIdx.x, l = t & 63, w = t >> 6;
@@ -133,6 +139,12 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     m0 = 0;
     n0 = tn * BN;
   } else {
+    if constexpr (MODE == kSplit) {
+      const int k0 = int(blockIdx.y) * kchunk;
+      Kl = min(kchunk, K - k0);
+      A = A_in + k0;
+      B = B_in + int64_t(k0) * N;
+    }
     const int ntiles = tiles_m * tiles_n;
     int pid = blockIdx.x;
     if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
@@ -151,8 +163,9 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
 
   // ---- loaders: A tile rows past M read as zero (num_records); B columns past N are read from
   //      the next row or as zero, and only feed columns of C that are never stored
-  const i32x4 rsrc_a = make_rsrc(A + int64_t(m0) * K, uint32_t(min(BM, M - m0)) * uint32_t(K) * 2u);
-  const i32x4 rsrc_b = make_rsrc(B + n0, uint32_t((int64_t(K) * N - n0) * 2));
+  const int koff = MODE == kSplit ? int(blockIdx.y) * kchunk : 0;   // this split's first K column
+  const i32x4 rsrc_a = make_rsrc(A + int64_t(m0) * K, uint32_t(int64_t(min(BM, M - m0)) * K - koff) * 2u);
+  const i32x4 rsrc_b = make_rsrc(B + n0, uint32_t((int64_t(K - koff) * N - n0) * 2));
   // A: instruction t of this wave covers rows 16*(kDmaA*wave + t) .. +16; lane -> row l/4, slot l%4
   // B: instruction t covers rows kBRowsPerKB*(kDmaB*wave + t) + lane/kBSlots; lane -> slot lane%kBSlots
   uint32_t a_voff[Sh::kDmaA], b_voff[Sh::kDmaB];
@@ -241,7 +254,7 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   constexpr int U = Sh::kMfma, P = Sh::kPieces, D = Sh::kDma;
   constexpr bool kOneReadPerMfma = P <= U;
   constexpr bool kStaggered = D <= U && P + 1 <= U;
-  const int nk = K / BK;
+  const int nk = Kl / BK;
   for (int s = 0; s < kStages - 1; ++s)
 #pragma unroll
     for (int t = 0; t < D; ++t) dma_one(s, t);
@@ -301,6 +314,10 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
         if (col >= N) continue;  // N % 8 == 0: a 4-column group is all in or all out
         const int64_t o = int64_t(row) * N + col;
         float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1], v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
+        if constexpr (MODE == kSplit) {
+          *reinterpret_cast<f32x4v*>(part + int64_t(blockIdx.y) * M * N + o) = f32x4v{v0, v1, v2, v3};
+          continue;
+        }
         if constexpr (RESID) {
           const u32x2 rr = *reinterpret_cast<const u32x2*>(R + o);
           v0 += bf16_lo(rr[0]);
@@ -323,13 +340,13 @@ int launch_gemm(const void* a, const void* b, const void* residual, void* c, int
   const dim3 grid(unsigned(tm * tn)), block(kThreads);
   const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
   if (residual)
-    gemm_bf16_kernel<WM, WN, true, false><<<grid, block, 0, s>>>(
+    gemm_bf16_kernel<WM, WN, true, kPlain><<<grid, block, 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), static_cast<const uint16_t*>(residual),
-        static_cast<uint16_t*>(c), int(m), int(n), int(k), int(tm), int(tn), none);
+        static_cast<uint16_t*>(c), int(m), int(n), int(k), int(tm), int(tn), none, nullptr, 0);
   else
-    gemm_bf16_kernel<WM, WN, false, false><<<grid, block, 0, s>>>(
+    gemm_bf16_kernel<WM, WN, false, kPlain><<<grid, block, 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, static_cast<uint16_t*>(c), int(m),
-        int(n), int(k), int(tm), int(tn), none);
+        int(n), int(k), int(tm), int(tn), none, nullptr, 0);
   return launch_status();
 }
 
@@ -354,13 +371,84 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
-  // the largest tile that still gives every CU a tile: 256x256, else 256x128, else 128x128
+  // the largest tile that still gives every CU a tile: 256x256, else 256x128; then 128x128 while its
+  // tiles cover half the CUs, else 64x128 (column tiles stay 128 wide: the B swizzle spans 16 chunks)
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t cus = cu_count();
   auto tiles = [&](int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
   if (tiles(256, 256) >= cus) return launch_gemm<4, 4>(a, b, residual, c, m, n, k, s);
   if (tiles(256, 128) >= cus) return launch_gemm<4, 2>(a, b, residual, c, m, n, k, s);
-  return launch_gemm<2, 2>(a, b, residual, c, m, n, k, s);
+  if (tiles(128, 128) * 2 >= cus) return launch_gemm<2, 2>(a, b, residual, c, m, n, k, s);
+  return launch_gemm<1, 2>(a, b, residual, c, m, n, k, s);   // 64 x 128: twice the tiles of 128 x 128
+}
+
+namespace {
+
+// C = bf16(sum_s P[s] (+ R)), 4 consecutive elements per thread.
+__global__ __launch_bounds__(256) void splitk_finish(const float* __restrict__ P, int splits, int64_t mn,
+                                                     const uint16_t* __restrict__ R, uint16_t* __restrict__ C) {
+  const int64_t q = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (q >= mn) return;
+  f32x4v acc = *reinterpret_cast<const f32x4v*>(P + q);
+  for (int s = 1; s < splits; ++s) acc += *reinterpret_cast<const f32x4v*>(P + int64_t(s) * mn + q);
+  if (R) {
+    const u32x2 rr = *reinterpret_cast<const u32x2*>(R + q);
+    acc.x += bf16_lo(rr[0]);
+    acc.y += bf16_hi(rr[0]);
+    acc.z += bf16_lo(rr[1]);
+    acc.w += bf16_hi(rr[1]);
+  }
+  *reinterpret_cast<u32x2*>(C + q) = u32x2{pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w)};
+}
+
+// Split-K plan for a GEMM whose 128x128 tiles would fill at most a quarter of the CUs: S slices of kchunk
+// (a multiple of 64, at least 256) columns so that tiles * S roughly covers the chip once.
+bool split_plan(int64_t m, int64_t n, int64_t k, int* splits, int* kchunk) {
+  const int64_t cus = cu_count();
+  const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  if (k < 512 || tiles * 4 > cus) return false;   // a quarter of the CUs or more: 64x128 tiles instead
+  int64_t s = (cus + tiles - 1) / tiles;
+  if (s > k / 256) s = k / 256;
+  if (s < 2) return false;
+  int64_t kc = ((k + s - 1) / s + 63) / 64 * 64;
+  s = (k + kc - 1) / kc;
+  if (s < 2) return false;
+  *splits = int(s);
+  *kchunk = int(kc);
+  return true;
+}
+
+}  // namespace
+
+PTB_EXPORT size_t ptb_gemm_bf16_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  int s, kc;
+  if (m <= 0 || n <= 0 || k <= 0 || !split_plan(m, n, k, &s, &kc)) return 0;
+  return size_t(s) * size_t(m) * size_t(n) * sizeof(float);
+}
+
+PTB_EXPORT int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n,
+                                int64_t k, void* workspace, size_t workspace_bytes, void* stream) {
+  int splits, kchunk;
+  if (m <= 0 || n <= 0 || k <= 0 || k % 64 || n % 8 || !split_plan(m, n, k, &splits, &kchunk))
+    return ptb_gemm_bf16(a, b, residual, c, m, n, k, stream);   // no split for this shape (or it is refused there)
+  if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
+  if (!a || !b || !c || !workspace) return PTB_ERR_NULL;
+  if (workspace_bytes < ptb_gemm_bf16_workspace_bytes(m, n, k)) return PTB_ERR_WORKSPACE;
+  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || int64_t(128) * k * 2 >= (int64_t(1) << 32))
+    return PTB_ERR_UNSUPPORTED;
+  if (!aligned16(a) || !aligned16(b) || !aligned16(c) || !aligned16(workspace) || (residual && !aligned16(residual)))
+    return PTB_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t tm = (m + 127) / 128, tn = (n + 127) / 128;
+  const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
+  float* part = static_cast<float*>(workspace);
+  gemm_bf16_kernel<2, 2, false, kSplit><<<dim3(unsigned(tm * tn), unsigned(splits)), dim3(kThreads), 0, s>>>(
+      static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, nullptr, int(m), int(n), int(k),
+      int(tm), int(tn), none, part, kchunk);
+  const int64_t mn = m * n;
+  splitk_finish<<<dim3(unsigned((mn / 4 + 255) / 256)), dim3(256), 0, s>>>(
+      part, splits, mn, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(c));
+  return launch_status();
 }
 
 PTB_EXPORT int ptb_grouped_gemm_bf16(const void* a, const void* b, const int32_t* group, const int32_t* start,
@@ -378,9 +466,9 @@ PTB_EXPORT int ptb_grouped_gemm_bf16(const void* a, const void* b, const int32_t
   const int64_t tn = (n + 127) / 128, tm_bound = (a_rows + 127) / 128 + nprog;
   if (tm_bound * tn > 0x7fffffff) return PTB_ERR_GRID;
   const Groups gp{group, start, rows, int(nprog), int(ntab), int(nweights), int(a_rows), weight_stride};
-  gemm_bf16_kernel<2, 2, false, true><<<dim3(unsigned(tm_bound * tn)), dim3(kThreads), 0,
-                                        static_cast<hipStream_t>(stream)>>>(
+  gemm_bf16_kernel<2, 2, false, kGrouped><<<dim3(unsigned(tm_bound * tn)), dim3(kThreads), 0,
+                                            static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, static_cast<uint16_t*>(c), 0, int(n),
-      int(k), 0, int(tn), gp);
+      int(k), 0, int(tn), gp, nullptr, 0);
   return launch_status();
 }

@@ -135,8 +135,11 @@ def slice_add(x: torch.Tensor, first: int, count: int, s: float, out=None) -> to
     return y
 
 
-def gemm(a: torch.Tensor, b: torch.Tensor, residual: torch.Tensor | None = None, out=None) -> torch.Tensor:
-    """C = A[M,K] @ B[K,N] (+ residual[M,N]), bf16 operands, fp32 accumulation, bf16 C."""
+def gemm(a: torch.Tensor, b: torch.Tensor, residual: torch.Tensor | None = None, out=None,
+         workspace: torch.Tensor | None = None, split_k: bool = True) -> torch.Tensor:
+    """C = A[M,K] @ B[K,N] (+ residual[M,N]), bf16 operands, fp32 accumulation, bf16 C.  Shapes whose
+    output tiles would leave most CUs idle run split-K over a workspace (given, or allocated here);
+    split_k=False forces the single-pass kernel."""
     _need(a, "a", BF16, 2)
     _need(b, "b", BF16, 2)
     m, k = a.shape
@@ -150,7 +153,14 @@ def gemm(a: torch.Tensor, b: torch.Tensor, residual: torch.Tensor | None = None,
             raise ValueError("residual must be [M, N]")
         rp = residual.data_ptr()
     c = _out(out, (m, n), BF16, a)
-    _lib.call("ptb_gemm_bf16", a.data_ptr(), b.data_ptr(), rp, c.data_ptr(), m, n, k, _stream(a))
+    need = _lib.load().ptb_gemm_bf16_workspace_bytes(m, n, k) if split_k else 0
+    if need:
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=a.device)
+        _lib.call("ptb_gemm_bf16_ws", a.data_ptr(), b.data_ptr(), rp, c.data_ptr(), m, n, k, workspace.data_ptr(),
+                  workspace.numel() * workspace.element_size(), _stream(a))
+    else:
+        _lib.call("ptb_gemm_bf16", a.data_ptr(), b.data_ptr(), rp, c.data_ptr(), m, n, k, _stream(a))
     return c
 
 

@@ -110,3 +110,42 @@ def test_gemm_fp8(m, k, n):
     # outputs are ~N(0, 0.02^2 K): scale the absolute floor with them
     scale = float(want.float().abs().mean()) + 1e-6
     assert_close(c[rows], want, RTOL, ATOL * scale, f"gemm_fp8 {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,k,n,resid", [
+    (128, 2048, 128, False), (8, 2048, 768, False), (512, 2048, 128, True), (32, 3072, 768, False),
+    (1000, 4096, 264, True), (64, 768, 2048, False), (256, 12288, 512, True),
+])
+def test_split_k_gemm(m, k, n, resid):
+    """Shapes with few output tiles run split-K (fp32 partials, one finish pass): the same result as
+    the oracle, and as the single-pass kernel within the bf16 bound."""
+    assert _lib.load().ptb_gemm_bf16_workspace_bytes(m, n, k) > 0, "this shape is meant to split"
+    a = randn((m, k), 31, std=1 / 64)
+    b = randn((k, n), 32, std=1.0)
+    r = randn((m, n), 33) if resid else None
+    ad, bd, rd = a.to(DEV), b.to(DEV), None if r is None else r.to(DEV)
+    split = ops.gemm(ad, bd, rd).cpu()
+    single = ops.gemm(ad, bd, rd, split_k=False).cpu()
+    want = oracle.gemm(a, b, r)
+    scale = float(want.float().abs().mean())
+    assert_close(split, want, RTOL, 2e-2 * scale, f"split-K {m}x{k}x{n}")
+    assert_close(split, single, RTOL, 2e-2 * scale, f"split-K vs single pass {m}x{k}x{n}")
+
+
+def test_split_k_exact_on_small_integers():
+    """Small-integer operands make every partial and sum exact in fp32: split-K equals the oracle bit
+    for bit, whatever the slicing."""
+    g = torch.Generator().manual_seed(34)
+    a = torch.randint(-3, 4, (96, 4096), generator=g).to(torch.bfloat16)
+    b = torch.randint(-3, 4, (4096, 136), generator=g).to(torch.bfloat16)
+    assert _lib.load().ptb_gemm_bf16_workspace_bytes(96, 136, 4096) > 0
+    got = ops.gemm(a.to(DEV), b.to(DEV)).cpu()
+    assert bits_equal(got, oracle.gemm(a, b))
+
+
+@pytest.mark.parametrize("m,k,n,resid", [(2048, 768, 768, False), (1000, 768, 264, True), (768, 3072, 1024, False),
+                                         (4000, 384, 512, True)])
+def test_gemm_64x128_tiles(m, k, n, resid):
+    """Mid-size shapes whose 128x128 tiles leave CUs idle but too many to split run 64x128 tiles."""
+    c, want = run_gemm(m, k, n, 41, 1 / 32, 1 / 16, resid)
+    assert_close(c, want, RTOL, 2e-2 * float(want.float().abs().mean()), f"64x128 {m}x{k}x{n}")
