@@ -11,10 +11,13 @@
 //           meet in LDS and the slice's fp32 partials go to the workspace [splits, N].
 //   pass 2: y[n] = bf16(sum over splits (+ r1[n] + r2[n])), one rounding.
 // Decode attention (one query token, G query heads per kv head, S cached keys, D = 128):
-//   pass 1: workgroup (64-key chunk, kv head): scores t = (q.k) * scale*log2(e) with 16 lanes per
-//           key (one 256-byte row), the chunk's softmax in base 2 (m = chunk max, p = 2^(t-m),
-//           l = sum of fp32 p), acc = sum bf16(p) * v; (m, l, acc) to the workspace.
-//   pass 2: merge the chunks of a kv head: m = max m_c, o = sum acc_c 2^(m_c-m) / sum l_c 2^(m_c-m).
+//   pass 1: workgroup (key range, query rows of a kv head): teams of 256 threads each take a 64-key
+//           chunk per step (scores with 16 lanes per key, one 256-byte row, summed by DPP row
+//           moves; a running base-2 softmax; the next step's K and V in flight meanwhile) and meet
+//           in LDS.  A cache of at most four chunks (two for more than 3 rows a workgroup) is one
+//           workgroup per row group that writes o itself; a longer one leaves an (acc, m, l) record
+//           per range in the workspace.  Short caches give each query row its own workgroups.
+//   pass 2: workgroup (row group, query row): o = sum acc_r 2^(m_r-M) / sum l_r 2^(m_r-M), M = max m_r.
 #include <cmath>
 
 #include "ptb_common.h"
@@ -216,182 +219,332 @@ int launch_gemv(const void* x, const void* add, const float* ss, const void* g, 
 // decode attention
 
 constexpr int kD = 128;
-constexpr int kChunk = 64;       // keys per workgroup
-constexpr int kAttnThreads = 256;
+constexpr int kChunk = 64;          // keys per team step
+constexpr int kTeam = 256;          // threads per 64-key chunk
+constexpr int kMaxRecords = 256;    // key ranges per kv head that the merge pass combines
 
-// workspace per (kv head, chunk): m[G], l[G], acc[G][128]
-template <int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_decode_partial(const uint16_t* __restrict__ Q,
-                                                                    const uint16_t* __restrict__ Kc,
-                                                                    const uint16_t* __restrict__ Vc,
-                                                                    float* __restrict__ ws, int S, float c) {
-  __shared__ float qs[G][kD];
-  __shared__ float ts[G][kChunk];          // scores, then bf16-rounded p
-  __shared__ float red[4][G][kD];
-  __shared__ float stat[G][2];
-  const int chunk = blockIdx.x, kvh = blockIdx.y, nchunks = gridDim.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint16_t* q = Q + int64_t(kvh) * G * kD;
-  const uint16_t* kp = Kc + int64_t(kvh) * S * kD;
-  const uint16_t* vp = Vc + int64_t(kvh) * S * kD;
-  const int key0 = chunk * kChunk;
-  for (int i = tid; i < G * kD; i += kAttnThreads) qs[i / kD][i % kD] = bf16_to_f32(q[i]);
-  __syncthreads();
+// How a kv head's work is cut: its G query rows go to `gsplit` workgroup rows of G / gsplit each,
+// and its keys to `records` workgroups holding `teams` teams of 256 threads, each team taking one
+// 64-key chunk per step for `steps` steps.  A cache that the teams of one workgroup cover in one
+// step is a single pass (records = 1, the teams merged in LDS): four teams (1024 threads, 128 VGPRs
+// a lane) for up to 3 query rows, two for more, which measured faster than two teams over two
+// steps.  Longer caches take one chunk per workgroup, up to kMaxRecords workgroups a head, more
+// steps beyond that.
+struct DecodePlan {
+  int gsplit;                 // workgroups sharing a kv head's query rows (G / gsplit rows each)
+  int teams, steps, records;
+};
+DecodePlan decode_plan(int64_t seq, int64_t group) {
+  const int64_t chunks = (seq + kChunk - 1) / kChunk;
+  // Query rows per workgroup (measured on MI355X over 8 kv heads, G = 2..8): one for caches up to
+  // 1024 keys, where a workgroup's VALU work, not HBM, sets the time; two up to 8192 keys; all of
+  // them beyond, where re-reading K and V would cost HBM bandwidth.  The workgroups of one kv head
+  // read the same K and V, the second time mostly from L2 or the last-level cache.
+  const int rows = seq <= 1024 ? 1 : seq <= 8192 ? 2 : 8;
+  int gsplit = 1;
+  while (group / gsplit > rows && (group / gsplit) % 2 == 0) gsplit *= 2;
+  const int64_t g = group / gsplit;
+  const int most = g <= 3 ? 4 : 2;
+  if (chunks <= most) return {gsplit, chunks <= 1 ? 1 : chunks <= 2 ? 2 : 4, 1, 1};
+  const int64_t steps = (chunks + kMaxRecords - 1) / kMaxRecords;
+  return {gsplit, 1, int(steps), int((chunks + steps - 1) / steps)};
+}
 
-  // every K and V load of the chunk goes out first (16 x 16 bytes a lane, 64 KB a workgroup in
-  // flight): the kernel is bound by HBM latency x bandwidth, not by its few FMAs
-  // scores: 16 lanes per key (8 dims each), 4 keys per wave, 16 keys per pass
-  const int d8 = lane & 15;
-  const int kj = tid >> 4;   // PV: 16 lanes per key, key kj of each pass
-  u32x4 kreg[kChunk / 16], vreg[kChunk / 16];
+// One record per (kv head, key range): acc[G][128], m[G], l[G], padded to 16 bytes.
+constexpr int64_t record_floats(int64_t g) { return g * kD + ((2 * g + 3) & ~int64_t(3)); }
+
+// One 64-key step of K and V into registers: lane (kj = tid/16, d8 = tid%16 of its team) holds
+// dims 8*d8..+8 of keys kj, kj+16, kj+32, kj+48; keys past S repeat key S-1 (their scores are
+// masked), so an idle team's loads stay in bounds too.
+__device__ __forceinline__ void load_step(const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp, int key0,
+                                          int S, int kj, int d8, u32x4 (&kr)[kChunk / 16],
+                                          u32x4 (&vr)[kChunk / 16]) {
 #pragma unroll
   for (int pass = 0; pass < kChunk / 16; ++pass) {
-    const int key = min(key0 + pass * 16 + wave * 4 + (lane >> 4), S - 1);
-    kreg[pass] = *reinterpret_cast<const u32x4*>(kp + int64_t(key) * kD + 8 * d8);
+    const int key = min(key0 + pass * 16 + kj, S - 1);
+    kr[pass] = *reinterpret_cast<const u32x4*>(kp + int64_t(key) * kD + 8 * d8);
   }
 #pragma unroll
   for (int pass = 0; pass < kChunk / 16; ++pass) {
     const int key = min(key0 + pass * 16 + kj, S - 1);
-    vreg[pass] = *reinterpret_cast<const u32x4*>(vp + int64_t(key) * kD + 8 * d8);
+    vr[pass] = *reinterpret_cast<const u32x4*>(vp + int64_t(key) * kD + 8 * d8);
   }
+}
+
+// Workgroup (key range, kv head) of T teams.  Team t walks chunks (range*steps + s)*T + t: scores
+// t = (q.k) * scale*log2(e) with 16 lanes a key, a running base-2 softmax (m = running max, p =
+// 2^(t-m), l = l*2^(m_old-m) + sum of fp32 p) and acc = acc*2^(m_old-m) + sum bf16(p) * v, the next
+// step's K and V in flight meanwhile.  The teams then meet in LDS (weights 2^(m_t - M)); a head of
+// one range writes o = bf16(acc / l), otherwise the range's (acc, m, l) record goes to the workspace.
+template <int G, int T>
+__global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t* __restrict__ Q,
+                                                                 const uint16_t* __restrict__ Kc,
+                                                                 const uint16_t* __restrict__ Vc,
+                                                                 uint16_t* __restrict__ O, float* __restrict__ part,
+                                                                 int S, float c, int steps, int gsplit) {
+  constexpr int kRec = int(record_floats(G));
+  __shared__ float qs[G][kD];
+  __shared__ float ts[T][G][kChunk];      // scores, then bf16-rounded p
+  __shared__ float red[T][4][G][kD];
+  __shared__ float mrun[T][G], lrun[T][G], alpha[T][G], wt[T][G], mfin[G], lfin[G];
+  const int range = blockIdx.x, kvh = blockIdx.y, nrec = gridDim.x;
+  const int tid = threadIdx.x, team = tid / kTeam, ttid = tid % kTeam;
+  const int lane = tid & 63, wave = ttid >> 6, d8 = lane & 15, kj = ttid >> 4;
+  const uint16_t* q = Q + int64_t(kvh) * G * kD;                 // kvh: this workgroup's G query rows
+  const uint16_t* kp = Kc + int64_t(kvh / gsplit) * S * kD;      // of kv head kvh / gsplit
+  const uint16_t* vp = Vc + int64_t(kvh / gsplit) * S * kD;
+  const int first = range * steps * T + team;   // this team's chunk at step 0; + s*T at step s
+
+  // q's load goes out before the first step's K and V, so waiting for q does not wait for them:
+  // 16 bytes a lane, lanes past the G*16 vectors repeat the last one (the same value, and no
+  // branch for the load to sink into)
+  const int qi = min(tid, G * kD / 8 - 1);
+  const u32x4 qv = *reinterpret_cast<const u32x4*>(q + 8 * qi);
+  u32x4 kr[kChunk / 16], vr[kChunk / 16];
+  load_step(kp, vp, first * kChunk, S, kj, d8, kr, vr);
 #pragma unroll
-  for (int pass = 0; pass < kChunk / 16; ++pass) {
-    const int j = pass * 16 + wave * 4 + (lane >> 4);
-    float kf[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      kf[2 * e] = bf16_lo(kreg[pass][e]);
-      kf[2 * e + 1] = bf16_hi(kreg[pass][e]);
-    }
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-      float s = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s = __builtin_fmaf(qs[gi][8 * d8 + e], kf[e], s);
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
-      if (d8 == 0) ts[gi][j] = (key0 + j < S) ? s * c : -INFINITY;
-    }
+  for (int e = 0; e < 4; ++e) {
+    qs[0][8 * qi + 2 * e] = bf16_lo(qv[e]);
+    qs[0][8 * qi + 2 * e + 1] = bf16_hi(qv[e]);
+  }
+  if (ttid < G) {
+    mrun[team][ttid] = -INFINITY;
+    lrun[team][ttid] = 0.f;
   }
   __syncthreads();
-
-  // chunk softmax: 32 lanes per query head, 4 keys a lane
-  for (int gi = tid / 32; gi < G; gi += kAttnThreads / 32) {
-    const int l32 = tid & 31;
-    float mx = -INFINITY;
+  // one team: q in registers; several (up to 1024 threads, 128 VGPRs a lane): q read from LDS.
+  // Up to two teams: the next step's K and V load while this one computes.
+  constexpr bool kPrefetch = T <= 2;
+  float qf[T == 1 ? G : 1][8];
+  if constexpr (T == 1) {
 #pragma unroll
-    for (int e = 0; e < kChunk / 32; ++e) mx = fmaxf(mx, ts[gi][l32 + 32 * e]);
+    for (int gi = 0; gi < G; ++gi)
 #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 32));
-    float ls = 0.f;
-#pragma unroll
-    for (int e = 0; e < kChunk / 32; ++e) {
-      const float p = __builtin_amdgcn_exp2f(ts[gi][l32 + 32 * e] - mx);
-      ls += p;
-      ts[gi][l32 + 32 * e] = bf16_to_f32(f32_to_bf16(p));
-    }
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) ls += __shfl_xor(ls, off, 32);
-    if (l32 == 0) {
-      stat[gi][0] = mx;
-      stat[gi][1] = ls;
-    }
+      for (int e = 0; e < 8; ++e) qf[gi][e] = qs[gi][8 * d8 + e];
   }
-  __syncthreads();
-
-  // acc[g][d] = sum_j p[g][j] v[j][d]: lane owns 8 dims of every 16th key
   float acc[G][8];
 #pragma unroll
   for (int gi = 0; gi < G; ++gi)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[gi][e] = 0.f;
-#pragma unroll
-  for (int pass = 0; pass < kChunk / 16; ++pass) {
-    const int j = pass * 16 + kj;
-    float vf[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      vf[2 * e] = bf16_lo(vreg[pass][e]);
-      vf[2 * e + 1] = bf16_hi(vreg[pass][e]);
+
+  for (int s = 0; s < steps; ++s) {
+    const int key0 = (first + s * T) * kChunk;
+    if constexpr (!kPrefetch) {
+      if (s > 0) load_step(kp, vp, key0, S, kj, d8, kr, vr);
     }
+    u32x4 kc[kChunk / 16], vc[kChunk / 16];
+#pragma unroll
+    for (int pass = 0; pass < kChunk / 16; ++pass) {
+      kc[pass] = kr[pass];
+      vc[pass] = vr[pass];
+    }
+    if constexpr (kPrefetch) {
+      if (s + 1 < steps) load_step(kp, vp, key0 + T * kChunk, S, kj, d8, kr, vr);
+    }
+
+#pragma unroll
+    for (int pass = 0; pass < kChunk / 16; ++pass) {
+      const int j = pass * 16 + kj;
+      float kf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kf[2 * e] = bf16_lo(kc[pass][e]);
+        kf[2 * e + 1] = bf16_hi(kc[pass][e]);
+      }
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        float sc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sc = __builtin_fmaf(T == 1 ? qf[gi][e] : qs[gi][8 * d8 + e], kf[e], sc);
+        sc = row16_sum(sc);
+        if (d8 == 0) ts[team][gi][j] = (key0 + j < S) ? sc * c : -INFINITY;
+      }
+    }
+    __syncthreads();
+
+    // running softmax: 32 lanes per query head, 2 keys a lane; a chunk with no key left (an idle
+    // team) keeps m = -inf, l = 0 and adds nothing
+    for (int gi = ttid / 32; gi < G; gi += kTeam / 32) {
+      const int l32 = ttid & 31;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < kChunk / 32; ++e) mx = fmaxf(mx, ts[team][gi][l32 + 32 * e]);
+      mx = pair16_max(row16_max(mx));
+      const float mold = mrun[team][gi], mnew = fmaxf(mold, mx);
+      const float mref = mnew == -INFINITY ? 0.f : mnew;
+      float ls = 0.f;
+#pragma unroll
+      for (int e = 0; e < kChunk / 32; ++e) {
+        const float p = __builtin_amdgcn_exp2f(ts[team][gi][l32 + 32 * e] - mref);
+        ls += p;
+        ts[team][gi][l32 + 32 * e] = bf16_to_f32(f32_to_bf16(p));
+      }
+      ls = pair16_sum(row16_sum(ls));
+      if (l32 == 0) {
+        const float a = __builtin_amdgcn_exp2f(mold - mref);
+        alpha[team][gi] = a;
+        mrun[team][gi] = mnew;
+        lrun[team][gi] = __builtin_fmaf(lrun[team][gi], a, ls);
+      }
+    }
+    __syncthreads();
+
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
-      const float p = ts[gi][j];
+      const float a = alpha[team][gi];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[gi][e] = __builtin_fmaf(p, vf[e], acc[gi][e]);
+      for (int e = 0; e < 8; ++e) acc[gi][e] *= a;
     }
+#pragma unroll
+    for (int pass = 0; pass < kChunk / 16; ++pass) {
+      const int j = pass * 16 + kj;
+      float vf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vf[2 * e] = bf16_lo(vc[pass][e]);
+        vf[2 * e + 1] = bf16_hi(vc[pass][e]);
+      }
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        const float p = ts[team][gi][j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[gi][e] = __builtin_fmaf(p, vf[e], acc[gi][e]);
+      }
+    }
+    __syncthreads();   // ts and alpha are rewritten by the next step
   }
-  // lanes l, l^16, l^32, l^48 hold the same dims; then the four waves meet in LDS
+
+  // lanes l, l^16, l^32, l^48 hold the same dims; then each team's four waves meet in LDS
 #pragma unroll
   for (int gi = 0; gi < G; ++gi)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float a = acc[gi][e];
-      a += __shfl_xor(a, 16, kWave);
-      a += __shfl_xor(a, 32, kWave);
-      acc[gi][e] = a;
-    }
+    for (int e = 0; e < 8; ++e) acc[gi][e] = pair32_sum(pair16_sum(acc[gi][e]));
   if (lane < 16) {
 #pragma unroll
     for (int gi = 0; gi < G; ++gi)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) red[wave][gi][8 * d8 + e] = acc[gi][e];
+      for (int e = 0; e < 8; ++e) red[team][wave][gi][8 * d8 + e] = acc[gi][e];
+  }
+  if (tid < G) {   // the teams' weights: 2^(m_t - M), 0 for a team that saw no key
+    float mm = mrun[0][tid];
+#pragma unroll
+    for (int t = 1; t < T; ++t) mm = fmaxf(mm, mrun[t][tid]);
+    float ll = 0.f;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float w = T == 1 ? 1.f : __builtin_amdgcn_exp2f(mrun[t][tid] - mm);
+      wt[t][tid] = w;
+      ll = __builtin_fmaf(lrun[t][tid], w, ll);
+    }
+    mfin[tid] = mm;
+    lfin[tid] = ll;
   }
   __syncthreads();
-  float* out = ws + (int64_t(kvh) * nchunks + chunk) * (G * (kD + 2));
-  for (int i = tid; i < G * kD; i += kAttnThreads) {
+
+  float* rec = nrec > 1 ? part + (int64_t(kvh) * nrec + range) * kRec : nullptr;
+  for (int i = tid; i < G * kD; i += kTeam * T) {
     const int gi = i / kD, d = i % kD;
-    out[2 * G + i] = (red[0][gi][d] + red[1][gi][d]) + (red[2][gi][d] + red[3][gi][d]);
+    float o = 0.f;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      o = __builtin_fmaf(wt[t][gi], (red[t][0][gi][d] + red[t][1][gi][d]) + (red[t][2][gi][d] + red[t][3][gi][d]), o);
+    if (nrec == 1)
+      O[(int64_t(kvh) * G + gi) * kD + d] = f32_to_bf16(o / lfin[gi]);
+    else
+      rec[i] = o;
   }
-  if (tid < G) {
-    out[tid] = stat[tid][0];
-    out[G + tid] = stat[tid][1];
+  if (nrec > 1 && tid < G) {
+    rec[G * kD + tid] = mfin[tid];
+    rec[G * kD + G + tid] = lfin[tid];
   }
 }
 
-// One workgroup per (kv head, query head): the chunk maxima reduce across the workgroup first,
-// then each lane (one of the 128 dims) sums the chunks with independent loads.
+// Workgroup (kv head, query head): o = sum acc_r 2^(m_r-M) / sum l_r 2^(m_r-M), M = max m_r, over
+// the head's records.  The acc loads do not depend on the weights, so they go out with the (m, l)
+// loads: lane (r, o4) holds 4 dims of records r, r+8, ..., up to 16 of them in flight, and a lane
+// per record reads its m and l; one round trip covers up to 128 records.
 template <int G>
-__global__ __launch_bounds__(kD) void attn_decode_combine(const float* __restrict__ ws, uint16_t* __restrict__ O,
-                                                          int nchunks) {
-  __shared__ float red[2];
-  const int kvh = blockIdx.x, gi = blockIdx.y, d = threadIdx.x;
-  const float* base = ws + int64_t(kvh) * nchunks * (G * (kD + 2));
-  constexpr int stride = G * (kD + 2);
-  float m = -INFINITY;
-  for (int ch = d; ch < nchunks; ch += kD) m = fmaxf(m, base[int64_t(ch) * stride + gi]);
+__global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict__ part, uint16_t* __restrict__ O,
+                                                         int nrec) {
+  constexpr int kRec = int(record_floats(G));
+  constexpr int kR = 256 / (kD / 4);    // 8 lanes per 4 output dims
+  __shared__ float wl[kMaxRecords];
+  __shared__ float red[2][4];
+  __shared__ f32x4 msum[256];
+  const int kvh = blockIdx.x, gi = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* recs = part + int64_t(kvh) * nrec * kRec;
+  const int o4 = tid % (kD / 4), r = tid / (kD / 4);
+  const float* base = recs + gi * kD + 4 * o4;
+  f32x4 v[16];
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-  if ((d & 63) == 0) red[d >> 6] = m;
+  for (int u = 0; u < 16; ++u) v[u] = *reinterpret_cast<const f32x4*>(base + int64_t(min(r + u * kR, nrec - 1)) * kRec);
+  const int r0 = min(tid, nrec - 1);
+  const bool ok = tid < nrec;
+  const float m = ok ? recs[int64_t(r0) * kRec + G * kD + gi] : -INFINITY;
+  const float l = recs[int64_t(r0) * kRec + G * kD + G + gi];
+  const float mw = wave_absmax(m);
+  if (lane == 0) red[0][wave] = mw;
   __syncthreads();
-  m = fmaxf(red[0], red[1]);
-  float l[4] = {0.f, 0.f, 0.f, 0.f}, o[4] = {0.f, 0.f, 0.f, 0.f};
-  int ch = 0;
-  for (; ch + 3 < nchunks; ch += 4) {
+  const float mm = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  const float w = ok ? __builtin_amdgcn_exp2f(m - mm) : 0.f;
+  if (ok) wl[tid] = w;
+  const float lw = wave_sum(l * w);
+  if (lane == 0) red[1][wave] = lw;
+  __syncthreads();
+
+  f32x4 sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float* p = base + int64_t(ch + u) * stride;
-      const float w = __builtin_amdgcn_exp2f(p[gi] - m);
-      l[u] = __builtin_fmaf(p[G + gi], w, l[u]);
-      o[u] = __builtin_fmaf(p[2 * G + gi * kD + d], w, o[u]);
+  for (int u = 0; u < 16; ++u) {
+    const int s = r + u * kR;
+    const float ws = s < nrec ? wl[s] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum[e] = __builtin_fmaf(ws, v[u][e], sum[e]);
+  }
+  for (int s0 = r + 16 * kR; s0 < nrec; s0 += 16 * kR) {   // more than 128 records
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = *reinterpret_cast<const f32x4*>(base + int64_t(min(s0 + u * kR, nrec - 1)) * kRec);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int s = s0 + u * kR;
+      const float ws = s < nrec ? wl[s] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum[e] = __builtin_fmaf(ws, v[u][e], sum[e]);
     }
   }
-  for (; ch < nchunks; ++ch) {
-    const float* p = base + int64_t(ch) * stride;
-    const float w = __builtin_amdgcn_exp2f(p[gi] - m);
-    l[0] = __builtin_fmaf(p[G + gi], w, l[0]);
-    o[0] = __builtin_fmaf(p[2 * G + gi * kD + d], w, o[0]);
+  msum[tid] = sum;
+  __syncthreads();
+  if (tid < kD / 4) {
+    f32x4 t = msum[tid];
+#pragma unroll
+    for (int rr = 1; rr < kR; ++rr) t += msum[rr * (kD / 4) + tid];
+    const float lt = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    uint16_t* out = O + (int64_t(kvh) * G + gi) * kD + 4 * tid;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = f32_to_bf16(t[e] / lt);
   }
-  const float lt = (l[0] + l[1]) + (l[2] + l[3]), ot = (o[0] + o[1]) + (o[2] + o[3]);
-  O[(int64_t(kvh) * G + gi) * kD + d] = f32_to_bf16(ot / lt);
 }
 
+template <int G, int T>
+void launch_partial(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* part, int nkv,
+                    int seq, float c, const DecodePlan& p, hipStream_t s) {
+  attn_decode_partial<G, T><<<dim3(unsigned(p.records), unsigned(nkv * p.gsplit)), dim3(kTeam * T), 0, s>>>(
+      q, k, v, o, part, seq, c, p.steps, p.gsplit);
+}
+
+// G: query rows per workgroup (the kv head's group / p.gsplit)
 template <int G>
-void launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* ws, int nkv,
-                        int seq, float c, hipStream_t s) {
-  const int nchunks = (seq + kChunk - 1) / kChunk;
-  attn_decode_partial<G><<<dim3(unsigned(nchunks), unsigned(nkv)), dim3(kAttnThreads), 0, s>>>(q, k, v, ws, seq, c);
-  attn_decode_combine<G><<<dim3(unsigned(nkv), unsigned(G)), dim3(kD), 0, s>>>(ws, o, nchunks);
+void launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* part, int nkv,
+                        int seq, float c, const DecodePlan& p, hipStream_t s) {
+  if (p.teams == 1) {
+    launch_partial<G, 1>(q, k, v, o, part, nkv, seq, c, p, s);
+  } else if (p.teams == 2) {
+    launch_partial<G, 2>(q, k, v, o, part, nkv, seq, c, p, s);
+  } else {
+    if constexpr (G <= 3) launch_partial<G, 4>(q, k, v, o, part, nkv, seq, c, p, s);
+  }
+  if (p.records > 1)
+    attn_decode_merge<G><<<dim3(unsigned(nkv * p.gsplit), unsigned(G)), dim3(256), 0, s>>>(part, o, p.records);
 }
 
 }  // namespace
@@ -431,9 +584,10 @@ PTB_EXPORT int ptb_gemv_silu_bf16(const void* gate_up, const void* w, const void
 }
 
 PTB_EXPORT size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, int64_t seq) {
-  if (nkv <= 0 || group <= 0 || seq <= 0) return 0;
-  const int64_t nchunks = (seq + kChunk - 1) / kChunk;
-  return size_t(nkv * nchunks * group * (kD + 2)) * sizeof(float);
+  if (nkv <= 0 || group <= 0 || seq <= 0 || seq > 0x7fffffff) return 0;
+  const DecodePlan p = decode_plan(seq, group);
+  if (p.records == 1) return 0;
+  return size_t(nkv * p.gsplit * p.records * record_floats(group / p.gsplit)) * sizeof(float);
 }
 
 PTB_EXPORT int ptb_attn_decode_bf16(const void* q, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
@@ -441,26 +595,29 @@ PTB_EXPORT int ptb_attn_decode_bf16(const void* q, const void* k, const void* v,
                                     size_t workspace_bytes, void* stream) {
   if (nkv < 0 || group <= 0 || seq <= 0 || head_dim <= 0) return PTB_ERR_SHAPE;
   if (head_dim != kD) return PTB_ERR_UNSUPPORTED;
+  if (group != 1 && group != 2 && group != 3 && group != 4 && group != 6 && group != 8) return PTB_ERR_UNSUPPORTED;
   if (!std::isfinite(scale)) return PTB_ERR_UNSUPPORTED;
   if (nkv == 0) return PTB_OK;
   if (!q || !k || !v || !o) return PTB_ERR_NULL;
-  if (!aligned16(k) || !aligned16(v)) return PTB_ERR_ALIGN;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return PTB_ERR_ALIGN;
   if (nkv > 65535 || seq > 0x7fffffff || nkv * seq * kD >= (int64_t(1) << 40)) return PTB_ERR_GRID;
-  if (!workspace || workspace_bytes < ptb_attn_decode_workspace_bytes(nkv, group, seq)) return PTB_ERR_WORKSPACE;
-  if (reinterpret_cast<uintptr_t>(workspace) & 3u) return PTB_ERR_ALIGN;
+  const size_t need = ptb_attn_decode_workspace_bytes(nkv, group, seq);
+  if (need && (!workspace || workspace_bytes < need)) return PTB_ERR_WORKSPACE;
+  if (need && !aligned16(workspace)) return PTB_ERR_ALIGN;
   const float c = scale * 1.4426950408889634f;
   auto qp = static_cast<const uint16_t*>(q), kp = static_cast<const uint16_t*>(k), vp = static_cast<const uint16_t*>(v);
   auto op = static_cast<uint16_t*>(o);
-  auto ws = static_cast<float*>(workspace);
+  float* ws = need ? static_cast<float*>(workspace) : nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (group) {
-    case 1: launch_attn_decode<1>(qp, kp, vp, op, ws, int(nkv), int(seq), c, s); break;
-    case 2: launch_attn_decode<2>(qp, kp, vp, op, ws, int(nkv), int(seq), c, s); break;
-    case 3: launch_attn_decode<3>(qp, kp, vp, op, ws, int(nkv), int(seq), c, s); break;
-    case 4: launch_attn_decode<4>(qp, kp, vp, op, ws, int(nkv), int(seq), c, s); break;
-    case 6: launch_attn_decode<6>(qp, kp, vp, op, ws, int(nkv), int(seq), c, s); break;
-    case 8: launch_attn_decode<8>(qp, kp, vp, op, ws, int(nkv), int(seq), c, s); break;
-    default: return PTB_ERR_UNSUPPORTED;
+  const DecodePlan p = decode_plan(seq, group);
+  if (nkv * p.gsplit > 65535) return PTB_ERR_GRID;
+  switch (group / p.gsplit) {
+    case 1: launch_attn_decode<1>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
+    case 2: launch_attn_decode<2>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
+    case 3: launch_attn_decode<3>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
+    case 4: launch_attn_decode<4>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
+    case 6: launch_attn_decode<6>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
+    default: launch_attn_decode<8>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
   }
   return launch_status();
 }

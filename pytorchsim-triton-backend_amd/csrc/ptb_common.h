@@ -72,6 +72,48 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
   return __uint_as_float(__float_as_uint(v) | sign);
 }
 
+// Cross-lane steps on the VALU, with no LDS round trip (a __shfl_xor is a ds_bpermute).  DPP moves
+// within a 16-lane row: quad_perm [1,0,3,2] and [2,3,0,1] pair lanes l^1 and l^2; row_half_mirror
+// (l <-> 7-l within 8) and row_mirror (l <-> 15-l) then pair quads and half-rows, whose lanes hold
+// equal values by then, so every lane of the row ends with the full row result.  The permlane
+// swaps (gfx950) exchange rows between two registers; handed the same value twice, the two results
+// are v[l] and v[l^16] (or v[l^32]) in some order, and combining them with a commutative op gives
+// every lane the same pair result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f32<0xb1>(v);
+  v += dpp_f32<0x4e>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<0xb1>(v));
+  v = fmaxf(v, dpp_f32<0x4e>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  return v;
+}
+__device__ __forceinline__ float pair16_sum(float v) {   // v[l] + v[l ^ 16]
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair16_max(float v) {   // max(v[l], v[l ^ 16])
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_sum(float v) {   // v[l] + v[l ^ 32]
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair32_max(float v) {   // max(v[l], v[l ^ 32])
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // wave64 reductions through cross-lane shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

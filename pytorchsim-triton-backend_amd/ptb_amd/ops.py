@@ -304,7 +304,9 @@ def gemv_silu(gate_up: torch.Tensor, w: torch.Tensor, res_a: torch.Tensor | None
 
 def attention_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None, out=None,
                      workspace=None) -> torch.Tensor:
-    """One-token attention over a KV cache: q [NKV, G, D], k/v [NKV, S, D] bf16 -> o [NKV, G, D]."""
+    """One-token attention over a KV cache: q [NKV, G, D], k/v [NKV, S, D] bf16 -> o [NKV, G, D].
+    `workspace`: ``ptb_attn_decode_workspace_bytes`` bytes (none for a cache of at most 256 keys,
+    which is a single pass)."""
     _need(q, "q", BF16, 3)
     _need(k, "k", BF16, 3)
     _need(v, "v", BF16, 3)
@@ -314,9 +316,10 @@ def attention_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
     s = k.shape[1]
     o = _out(out, (nkv, g, d), BF16, q)
     need = _lib.load().ptb_attn_decode_workspace_bytes(nkv, g, s)
-    if workspace is None:
-        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     sc = default_scale(d) if scale is None else float(scale)
     _lib.call("ptb_attn_decode_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), nkv, g, s, d, sc,
-              workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(q))
+              workspace.data_ptr() if workspace is not None else None,
+              workspace.numel() * workspace.element_size() if workspace is not None else 0, _stream(q))
     return o

@@ -90,15 +90,43 @@ def test_attention_decode_ragged(nkv, g, s):
                 assert bits_equal(got[h, gi], v[h, 0])
 
 
+@pytest.mark.parametrize("nkv,g,s", [(2, 1, 20000), (1, 8, 20000), (1, 4, 16384), (2, 8, 64), (5, 3, 256),
+                                     (3, 8, 100), (3, 8, 250), (257, 1, 300), (2, 8, 9000), (2, 6, 3000),
+                                     (300, 8, 40)])
+def test_attention_decode_range_plans(nkv, g, s):
+    """Ranges of two 64-key steps (313 chunks, more than the 256 ranges a head may have) with 1 and
+    8 rows a workgroup, exactly 256 one-chunk ranges, one chunk in one pass, four teams in one pass
+    (G = 3), one row a workgroup in one pass with two and four teams (G = 8), many kv heads, all 8
+    rows in one workgroup past 8192 keys, 3 rows a workgroup (G = 6 halves to an odd count), and
+    2400 row workgroups (300 heads x 8)."""
+    q, k, v = randn((nkv, g, 128), 20), randn((nkv, s, 128), 21), randn((nkv, s, 128), 22)
+    got = ops.attention_decode(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
+    assert_close(got, oracle.attention_decode(q, k, v), RTOL, 2e-2, f"decode plan {nkv}x{g}x{s}")
+
+
+def test_attention_decode_workspace_reuse():
+    """One caller workspace serves consecutive calls of different shapes (each call's records
+    replace the last call's)."""
+    need = max(_lib.load().ptb_attn_decode_workspace_bytes(8, 4, 4096),
+               _lib.load().ptb_attn_decode_workspace_bytes(3, 2, 1000))
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    for nkv, g, s, seed in ((8, 4, 4096, 30), (3, 2, 1000, 33), (8, 4, 4096, 36), (8, 4, 1500, 39)):
+        q, k, v = randn((nkv, g, 128), seed), randn((nkv, s, 128), seed + 1), randn((nkv, s, 128), seed + 2)
+        got = ops.attention_decode(q.to(DEV), k.to(DEV), v.to(DEV), workspace=ws).cpu()
+        assert_close(got, oracle.attention_decode(q, k, v), RTOL, 2e-2, f"decode reuse {nkv}x{g}x{s}")
+
+
 def test_decode_refusals():
     q = torch.zeros((2, 5, 128), dtype=torch.bfloat16, device=DEV)
     k = torch.zeros((2, 64, 128), dtype=torch.bfloat16, device=DEV)
     with pytest.raises(_lib.UnsupportedError):
         ops.attention_decode(q, k, k)                                   # group 5 is not built
     q4 = torch.zeros((2, 4, 128), dtype=torch.bfloat16, device=DEV)
+    k4 = torch.zeros((2, 4096, 128), dtype=torch.bfloat16, device=DEV)   # several key ranges a head
     small = torch.empty(16, dtype=torch.uint8, device=DEV)
     with pytest.raises(_lib.PtbError) as e:
-        ops.attention_decode(q4, k, k, workspace=small)
+        ops.attention_decode(q4, k4, k4, workspace=small)
     assert e.value.status == _lib.PTB_ERR_WORKSPACE
     x = torch.zeros(64, dtype=torch.bfloat16, device=DEV)
     w = torch.zeros((64, 12), dtype=torch.bfloat16, device=DEV)
