@@ -239,10 +239,17 @@ DecodePlan decode_plan(int64_t seq, int64_t group) {
   // Query rows per workgroup (measured on MI355X over 8 kv heads, G = 2..8): one for caches up to
   // 1024 keys, where a workgroup's VALU work, not HBM, sets the time; two up to 8192 keys; all of
   // them beyond, where re-reading K and V would cost HBM bandwidth.  The workgroups of one kv head
-  // read the same K and V, the second time mostly from L2 or the last-level cache.
+  // read the same K and V, the second time mostly from L2 or the last-level cache.  G splits by
+  // factors of 2 and 3 (G = 3 and 6 reach one row).  A single pass of two steps measured slower
+  // than a second (merge) launch, so single passes are one step.
   const int rows = seq <= 1024 ? 1 : seq <= 8192 ? 2 : 8;
   int gsplit = 1;
-  while (group / gsplit > rows && (group / gsplit) % 2 == 0) gsplit *= 2;
+  for (;;) {
+    const int64_t g = group / gsplit;
+    if (g % 2 == 0 && g / 2 >= rows) gsplit *= 2;
+    else if (g % 3 == 0 && g / 3 >= rows) gsplit *= 3;
+    else break;
+  }
   const int64_t g = group / gsplit;
   const int most = g <= 3 ? 4 : 2;
   if (chunks <= most) return {gsplit, chunks <= 1 ? 1 : chunks <= 2 ? 2 : 4, 1, 1};

@@ -97,8 +97,8 @@ def test_attention_decode_range_plans(nkv, g, s):
     """Ranges of two 64-key steps (313 chunks, more than the 256 ranges a head may have) with 1 and
     8 rows a workgroup, exactly 256 one-chunk ranges, one chunk in one pass, four teams in one pass
     (G = 3), one row a workgroup in one pass with two and four teams (G = 8), many kv heads, all 8
-    rows in one workgroup past 8192 keys, 3 rows a workgroup (G = 6 halves to an odd count), and
-    2400 row workgroups (300 heads x 8)."""
+    rows in one workgroup past 8192 keys, G = 6 halved to 3 rows a workgroup (thirds would go below
+    two rows), and 2400 row workgroups (300 heads x 8)."""
     q, k, v = randn((nkv, g, 128), 20), randn((nkv, s, 128), 21), randn((nkv, s, 128), 22)
     got = ops.attention_decode(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
     assert_close(got, oracle.attention_decode(q, k, v), RTOL, 2e-2, f"decode plan {nkv}x{g}x{s}")
