@@ -115,7 +115,7 @@ __device__ __forceinline__ void softmax_step(WaveState& w, f32x16 (&sacc)[2], bf
   for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
     for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[t2][e]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  mx = pair32_max(mx);
   const float mt = mx * c;
   if (__builtin_amdgcn_ballot_w64(mt > w.m + kRescaleLog2)) {
     const float m_new = fmaxf(w.m, mt);
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   }
   if (!active) return;
 
-  const float l = w.l + __shfl_xor(w.l, 32, kWave);
+  const float l = pair32_sum(w.l);
   const float inv = 1.f / l;
   uint16_t* orow = op + int64_t(qi) * D;
 #pragma unroll

@@ -114,22 +114,36 @@ __device__ __forceinline__ float pair32_max(float v) {   // max(v[l], v[l ^ 32])
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// wave64 reductions through cross-lane shuffles.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+// v[l ^ 8] within a 16-lane row (row_ror:8: rotating a row by 8 lanes is the xor-8 exchange).
+__device__ __forceinline__ uint32_t xor8_u32(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x128, 0xf, 0xf, false));
 }
-__device__ __forceinline__ float wave_max_nan(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = max_nan(v, __shfl_xor(v, off, kWave));
-  return v;
+
+// wave64 reductions on the VALU (DPP within rows, then the two permlane swaps); every lane gets the
+// result.  All 64 lanes take part.
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+  v = op(v, dpp_f32<0xb1>(v));
+  v = op(v, dpp_f32<0x4e>(v));
+  v = op(v, dpp_f32<0x141>(v));
+  v = op(v, dpp_f32<0x140>(v));
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ __forceinline__ float wave_absmax(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
-}
+struct AddOp {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxNanOp {
+  __device__ float operator()(float a, float b) const { return max_nan(a, b); }
+};
+struct MaxOp {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+__device__ __forceinline__ float wave_sum(float v) { return wave_reduce(v, AddOp()); }
+__device__ __forceinline__ float wave_max_nan(float v) { return wave_reduce(v, MaxNanOp()); }
+__device__ __forceinline__ float wave_absmax(float v) { return wave_reduce(v, MaxOp()); }
 
 // Block reductions for blocks of NW waves; `red` is NW floats of LDS.  Every thread gets the result.
 template <int NW>

@@ -290,11 +290,10 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope(const uint16_t* __restric
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+  ss = row16_sum(ss);
   u32x4 pv;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) pv[q] = __shfl_xor(v[q], 8, kWave);
+  for (int q = 0; q < 4; ++q) pv[q] = xor8_u32(v[q]);
   if (!live) return;
   float pf[8], wf[8], pw[8];
   unpack8(pv, pf);
