@@ -152,8 +152,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows(const uint16_t* __restric
     if (in) {
       float f[8];
       unpack8(v[i], f);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mx = max_nan(mx, f[e]);
+      mx = max_nan(mx, max8_nan(f));
     }
   }
   mx = team_max<TPR>(mx, red);
@@ -194,8 +193,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_long(const uint16_t* __re
   for (int c = threadIdx.x; c < chunks; c += kBlock) {
     float f[8];
     unpack8(xr[c], f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) mx = max_nan(mx, f[e]);
+    mx = max_nan(mx, max8_nan(f));
   }
   mx = block_max_nan<kBlock / kWave>(mx, red);
   float s = 0.f;
@@ -343,8 +341,12 @@ __global__ __launch_bounds__(kBlock) void reduce_partial(const InT* __restrict__
   for (int64_t c = int64_t(blockIdx.x) * kBlock + threadIdx.x; c < chunks; c += stride) {
     float f[8];
     load8(x, c, f);
+    if constexpr (OP == PTB_REDUCE_SUM) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc = OP == PTB_REDUCE_SUM ? acc + f[e] : max_nan(acc, f[e]);
+      for (int e = 0; e < 8; ++e) acc += f[e];
+    } else {
+      acc = max_nan(acc, max8_nan(f));
+    }
   }
   if (blockIdx.x == 0) {
     for (int64_t i = (chunks << 3) + threadIdx.x; i < n; i += kBlock) {
@@ -355,6 +357,49 @@ __global__ __launch_bounds__(kBlock) void reduce_partial(const InT* __restrict__
   acc = OP == PTB_REDUCE_SUM ? block_sum<kBlock / kWave>(acc, red) : block_max_nan<kBlock / kWave>(acc, red);
   if (threadIdx.x == 0) part[blockIdx.x] = acc;
 }
+// Inputs of at most kSmallReduce elements: one workgroup (64..1024 threads, a thread per 8 chunks
+// of 8 elements) and one launch.  Each thread issues all its loads of a batch before it
+// accumulates (slots past the end load the last chunk again and are skipped), so a batch costs
+// one memory round trip.
+constexpr int kSmallThreads = 1024;
+constexpr int kSmallLoads = 8;
+constexpr int64_t kSmallReduce = 32768;   // measured: one CU's VALU work outgrows a second launch beyond
+template <int OP, typename InT>
+__global__ __launch_bounds__(kSmallThreads) void reduce_small(const InT* __restrict__ x, int64_t n,
+                                                               float* __restrict__ out) {
+  __shared__ float red[kSmallThreads / kWave];
+  const int chunks = int(n >> 3), nt = int(blockDim.x), tid = int(threadIdx.x);
+  float acc = OP == PTB_REDUCE_SUM ? 0.f : -INFINITY;
+  for (int base = 0; base < chunks; base += nt * kSmallLoads) {
+    float f[kSmallLoads][8];
+#pragma unroll
+    for (int i = 0; i < kSmallLoads; ++i) load8(x, min(base + i * nt + tid, chunks - 1), f[i]);
+#pragma unroll
+    for (int i = 0; i < kSmallLoads; ++i) {
+      if (base + i * nt + tid < chunks) {
+        if constexpr (OP == PTB_REDUCE_SUM) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc += f[i][e];
+        } else {
+          acc = max_nan(acc, max8_nan(f[i]));
+        }
+      }
+    }
+  }
+  for (int64_t i = (int64_t(chunks) << 3) + tid; i < n; i += nt) {
+    const float v = as_f32(x[i]);
+    acc = OP == PTB_REDUCE_SUM ? acc + v : max_nan(acc, v);
+  }
+  acc = OP == PTB_REDUCE_SUM ? wave_sum(acc) : wave_max_nan(acc);
+  if ((tid & 63) == 0) red[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) {
+    float t = red[0];
+    for (int w = 1; w < nt / kWave; ++w) t = OP == PTB_REDUCE_SUM ? t + red[w] : max_nan(t, red[w]);
+    out[0] = t;
+  }
+}
+
 template <int OP>
 __global__ __launch_bounds__(kBlock) void reduce_final(const float* __restrict__ part, int np,
                                                        float* __restrict__ out) {
@@ -544,6 +589,15 @@ int reduce_launch(const InT* x, float* out, int64_t n, int op, void* workspace, 
   if (!aligned16(x) || !aligned16(workspace)) return PTB_ERR_ALIGN;
   if (workspace_bytes < ptb_reduce_workspace_bytes(n)) return PTB_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n <= kSmallReduce) {
+    const int64_t per = (n / 8 + kSmallLoads - 1) / kSmallLoads;        // threads for one batch
+    const int nt = int(per <= kWave ? kWave : per >= kSmallThreads ? kSmallThreads : (per + kWave - 1) / kWave * kWave);
+    if (op == PTB_REDUCE_SUM)
+      reduce_small<PTB_REDUCE_SUM, InT><<<dim3(1), dim3(nt), 0, s>>>(x, n, out);
+    else
+      reduce_small<PTB_REDUCE_MAX, InT><<<dim3(1), dim3(nt), 0, s>>>(x, n, out);
+    return launch_status();
+  }
   const int g = grid_for(n / 8, int64_t(kBlock) * 8, kReduceBlocks);
   float* part = static_cast<float*>(workspace);
   if (op == PTB_REDUCE_SUM) {

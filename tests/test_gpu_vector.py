@@ -107,8 +107,11 @@ def test_qk_norm_rope(tokens, heads, tables, seed):
     check_bf16(got, oracle.qk_norm_rope(x, w, cos, sin, 1e-6), f"qk_norm_rope {tokens}x{heads}")
 
 
-@pytest.mark.parametrize("n,seed", [(12288 * 4096, 0), (1024 * 1024, 1), (8 * 128 + 5, 2), (3, 3)])
+@pytest.mark.parametrize("n,seed", [(12288 * 4096, 0), (1024 * 1024, 1), (8 * 128 + 5, 2), (3, 3),
+                                    (32768, 4), (32769, 5), (4096 + 8, 6), (16384, 7), (517, 8)])
 def test_reduce(n, seed):
+    """Two passes above 32768 elements, one workgroup of 64..512 threads at or below (skipped
+    slots, a tail of n % 8 elements)."""
     x = randn((n,), seed)
     xd = x.to(DEV)
     got_max = ops.reduce(xd, "max").cpu()
@@ -124,7 +127,7 @@ def test_reduce(n, seed):
     assert abs(gs - ws) <= 1e-5 * abs(ws), (gs, ws)
 
 
-@pytest.mark.parametrize("n,seed", [(8, 0), (1000003, 1), (4096 * 4096, 2)])
+@pytest.mark.parametrize("n,seed", [(8, 0), (1000003, 1), (4096 * 4096, 2), (30003, 3)])
 def test_reduce_fp32_input(n, seed):
     """fp32 elements (the MoE router's sum of its top-k weights is the 8-element case)."""
     x = torch.randn(n, generator=torch.Generator().manual_seed(seed)) + 0.5
@@ -134,8 +137,9 @@ def test_reduce_fp32_input(n, seed):
     assert abs(got - want) <= 1e-6 * float(x.abs().sum()) + 1e-6, (got, want)
 
 
-def test_reduce_max_nan():
-    x = randn((4096,), 9)
+@pytest.mark.parametrize("n", [4096, 1 << 20])
+def test_reduce_max_nan(n):
+    x = randn((n,), 9)
     x[1234] = float("nan")
     assert math.isnan(float(ops.reduce(x.to(DEV), "max")))
 
