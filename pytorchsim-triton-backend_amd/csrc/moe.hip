@@ -474,6 +474,89 @@ __global__ __launch_bounds__(kB) void topk_rows(const float* __restrict__ x, int
   }
 }
 
+// Top-k with k <= 64 of rows of at most 64*R elements: one wave per row with the row in registers
+// (lane l holds elements l, l + 64, ...), every load in flight at once, then k rounds of a wave
+// argmax over the elements not yet taken.  The 64-bit key (order-preserving bits of the value,
+// then the inverted position) makes a round's winner the largest value and, among equal values,
+// the lowest position: the same selection and order as the rank kernel above.  Taken and absent
+// elements hold key 0, below every present one.
+__device__ __forceinline__ uint32_t order_bits(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_order_bits(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o ^ 0x80000000u) : ~o);
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ void key_max(uint32_t& h, uint32_t& l, uint32_t oh, uint32_t ol) {
+  const bool b = (oh > h) | ((oh == h) & (ol > l));
+  h = b ? oh : h;
+  l = b ? ol : l;
+}
+// Wave-wide max of the 64-bit keys (h, l); every lane gets it.  The permlane swaps move h and l by
+// the same permutation, so each returned pair is one lane's key.
+__device__ __forceinline__ void wave_key_max(uint32_t& h, uint32_t& l) {
+  key_max(h, l, dpp_u32<0xb1>(h), dpp_u32<0xb1>(l));
+  key_max(h, l, dpp_u32<0x4e>(h), dpp_u32<0x4e>(l));
+  key_max(h, l, dpp_u32<0x141>(h), dpp_u32<0x141>(l));
+  key_max(h, l, dpp_u32<0x140>(h), dpp_u32<0x140>(l));
+  auto rh = __builtin_amdgcn_permlane16_swap(h, h, false, false);
+  auto rl = __builtin_amdgcn_permlane16_swap(l, l, false, false);
+  h = rh[0]; l = rl[0];
+  key_max(h, l, rh[1], rl[1]);
+  rh = __builtin_amdgcn_permlane32_swap(h, h, false, false);
+  rl = __builtin_amdgcn_permlane32_swap(l, l, false, false);
+  h = rh[0]; l = rl[0];
+  key_max(h, l, rh[1], rl[1]);
+}
+template <int R>
+__global__ __launch_bounds__(kB) void topk_rows_wave(const float* __restrict__ x, int64_t rows, int e, int k,
+                                                     bool largest, float* __restrict__ vals,
+                                                     int64_t* __restrict__ idx) {
+  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t row = int64_t(blockIdx.x) * kTopkRows + w;
+  if (row >= rows) return;   // a whole wave; no block barrier below
+  // smallest-k is largest-k of the negated values (negation reverses the order, keeps ties)
+  const float sgn = largest ? 1.0f : -1.0f;
+  const float* xr = x + row * e;
+  float raw[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) raw[r] = xr[min(lane + kWave * r, e - 1)];
+  uint32_t kh[R], kl[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool in = lane + kWave * r < e;
+    kh[r] = in ? order_bits(sgn * raw[r]) : 0u;
+    kl[r] = in ? ~uint32_t(lane + kWave * r) : 0u;
+  }
+  float outv = 0.f;
+  int outi = 0;
+  for (int n = 0; n < k; ++n) {
+    uint32_t bh = kh[0], bl = kl[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r) key_max(bh, bl, kh[r], kl[r]);
+    wave_key_max(bh, bl);
+    const int pos = int(~bl);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const bool taken = lane + kWave * r == pos;
+      kh[r] = taken ? 0u : kh[r];
+      kl[r] = taken ? 0u : kl[r];
+    }
+    if (lane == n) {
+      outv = sgn * from_order_bits(bh);
+      outi = pos;
+    }
+  }
+  if (lane < k) {
+    vals[row * k + lane] = outv;
+    idx[row * k + lane] = outi;
+  }
+}
+
 // ---------------------------------------------------------------- token <-> slot data movement
 // out[s, :] = x[floordiv(slot[s], k) (wrapped into [0, t)), :], 8 bf16 per thread.
 __global__ __launch_bounds__(kB) void gather_rows(const int64_t* __restrict__ slot, int64_t r, int64_t k,
@@ -798,8 +881,18 @@ PTB_EXPORT int ptb_topk_rows_f32(const float* x, int64_t rows, int64_t e, int64_
   if (e > kTopkMax || k > e) return PTB_ERR_UNSUPPORTED;
   const int64_t blocks = (rows + kTopkRows - 1) / kTopkRows;
   if (blocks > 0x7fffffff) return PTB_ERR_GRID;
-  topk_rows<<<dim3(unsigned(blocks)), kB, 0, static_cast<hipStream_t>(stream)>>>(x, rows, int(e), int(k), largest != 0,
-                                                                               values, indices);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int ei = int(e), ki = int(k);
+  const bool lg = largest != 0;
+  if (k <= kWave) {   // the row in registers, k wave-argmax rounds
+    if (e <= 64) topk_rows_wave<1><<<dim3(unsigned(blocks)), kB, 0, s>>>(x, rows, ei, ki, lg, values, indices);
+    else if (e <= 128) topk_rows_wave<2><<<dim3(unsigned(blocks)), kB, 0, s>>>(x, rows, ei, ki, lg, values, indices);
+    else if (e <= 256) topk_rows_wave<4><<<dim3(unsigned(blocks)), kB, 0, s>>>(x, rows, ei, ki, lg, values, indices);
+    else if (e <= 512) topk_rows_wave<8><<<dim3(unsigned(blocks)), kB, 0, s>>>(x, rows, ei, ki, lg, values, indices);
+    else topk_rows_wave<16><<<dim3(unsigned(blocks)), kB, 0, s>>>(x, rows, ei, ki, lg, values, indices);
+  } else {
+    topk_rows<<<dim3(unsigned(blocks)), kB, 0, s>>>(x, rows, ei, ki, lg, values, indices);
+  }
   return launch_status();
 }
 

@@ -89,8 +89,11 @@ def test_sort_rows(rows, e, kind, desc):
 
 
 @pytest.mark.parametrize("rows,e,k,largest", [(1024, 128, 8, True), (1, 128, 8, True), (4096, 128, 8, True),
-                                              (100, 1000, 5, False), (7, 64, 64, True)])
+                                              (100, 1000, 5, False), (7, 64, 64, True), (3, 100, 65, True),
+                                              (5, 33, 8, False), (2, 300, 16, True), (9, 1024, 64, False)])
 def test_topk_rows(rows, e, k, largest):
+    """Rows in registers with wave-argmax rounds (k <= 64, 1 to 16 values a lane, ragged e) and the
+    LDS rank kernel (k = 65)."""
     x = torch.randn(rows * e, generator=gen(rows + k))
     x[3::17] = x[::17][: x[3::17].numel()]     # repeated values: ties by lowest position
     v, i = torch.empty(rows * k, device=DEV), torch.empty(rows * k, dtype=I64, device=DEV)
