@@ -304,6 +304,17 @@ int ptb_rms_broadcast_bf16(const void* x, const void* a, const float* ss, const 
 int ptb_grouped_gemm_bf16(const void* a, const void* b, const int32_t* group, const int32_t* start,
                           const int32_t* rows, void* c, int64_t nprog, int64_t ntab, int64_t a_rows,
                           int64_t nweights, int64_t k, int64_t n, int64_t weight_stride, void* stream);
+/* The same grouped GEMM with a caller workspace of ptb_grouped_gemm_workspace_bytes(nprog, a_rows,
+ * k, n) bytes (16-byte aligned), non-zero when a_rows <= 16: a split-K GEMV pass over each
+ * program's weight (every weight row read once per 4 rows of A) and a pass that sums the slices,
+ * rounding once.  Same results contract and argument checks as ptb_grouped_gemm_bf16, which it
+ * calls when the workspace query is 0 or the workspace is missing or short.
+ * Replaces: the same grouped_mm kernels, at the decode shapes (layer_layer_decode_1x<S>_bf16/20, 22) */
+size_t ptb_grouped_gemm_workspace_bytes(int64_t nprog, int64_t a_rows, int64_t k, int64_t n);
+int ptb_grouped_gemm_bf16_ws(const void* a, const void* b, const int32_t* group, const int32_t* start,
+                             const int32_t* rows, void* c, int64_t nprog, int64_t ntab, int64_t a_rows,
+                             int64_t nweights, int64_t k, int64_t n, int64_t weight_stride, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

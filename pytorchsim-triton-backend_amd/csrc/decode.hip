@@ -216,6 +216,128 @@ int launch_gemv(const void* x, const void* add, const float* ss, const void* g, 
 }
 
 // ---------------------------------------------------------------------------------------------
+// grouped GEMV: the grouped GEMM when A has at most kGgMaxRows rows (the decode MoE: one token's k
+// experts, a row each).  For each program p with g = group[p]: C[start[g] + i] = A[start[g] + i] @
+// B[g] for i < rows[g].  Pass 1: workgroup (512-column block, 64-row K slice, program); as soon as
+// g is known every lane issues its 16 weight loads of the slice (the slice stays in registers, read
+// once however many rows the group has), then reads start/rows and A's slice into LDS, kGgRows rows
+// at a time; fp32 partials per (program, slice, row).  Pass 2 sums the slices and rounds.
+
+constexpr int kGgRows = 4;       // A rows a pass of FMAs over the register-held slice serves
+constexpr int kGgMaxRows = 16;   // A rows at most: no program can have more
+constexpr int kGgKb = 64;        // K rows per slice: 16 per wave, one 16-byte load each per lane
+
+// Table checks as the MFMA path makes them: group in [0, ntab) and below nweights; rows > 0,
+// start >= 0, start + rows <= a_rows.  An entry failing them is an empty program.
+__device__ __forceinline__ bool gg_weight(int g, int ntab, int nweights) { return g >= 0 && g < ntab && g < nweights; }
+__device__ __forceinline__ bool gg_rows(int s0, int nr, int a_rows) {
+  return nr > 0 && s0 >= 0 && int64_t(s0) + nr <= a_rows;
+}
+
+__global__ __launch_bounds__(kGemvThreads) void ggemv_partial(const uint16_t* __restrict__ A,
+                                                              const uint16_t* __restrict__ B,
+                                                              const int32_t* __restrict__ grp,
+                                                              const int32_t* gstart, const int32_t* grows, int ntab,
+                                                              int nweights, int a_rows, int64_t sbg, int K, int N,
+                                                              int splits, float* __restrict__ part) {
+  __shared__ float xs[kGgRows][kGgKb];
+  __shared__ float red[4][kGgRows][kColBlock];
+  const int p = blockIdx.z, split = blockIdx.y, n0 = blockIdx.x * kColBlock;
+  const int g = grp[p];
+  if (!gg_weight(g, ntab, nweights)) return;   // uniform
+  const int k0 = split * kGgKb, krows = min(K - k0, kGgKb);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = min(n0 + 8 * lane, N - 8);    // lanes past N repeat the last columns (not stored)
+  // rows wave, wave + 4, ... of the slice; rows past K repeat the slice's last row (weight 0 below)
+  const uint16_t* wp = B + int64_t(g) * sbg + int64_t(k0) * N + col;
+  u32x4 v[kGgKb / 4];
+#pragma unroll
+  for (int u = 0; u < kGgKb / 4; ++u)
+    v[u] = *reinterpret_cast<const u32x4*>(wp + int64_t(min(wave + 4 * u, krows - 1)) * N);
+  // the first pass below runs even for an empty row range (it then stores nothing): an exit or a
+  // guarded loop would let the compiler move the weight loads after the table reads and wait for
+  // those first
+  const int s0r = gstart[g], nr0 = grows[g];
+  const bool has_rows = gg_rows(s0r, nr0, a_rows);
+  const int nr = has_rows ? nr0 : 0, s0 = has_rows ? s0r : 0;
+  int i0 = 0;
+  do {
+    const int rb = min(kGgRows, nr - i0);   // <= 0 for an empty range: no A row read, nothing stored
+    for (int t = threadIdx.x; t < kGgRows * kGgKb; t += kGemvThreads) {
+      const int r = t / kGgKb, kk = t % kGgKb;
+      xs[r][kk] = (r < rb && kk < krows) ? bf16_to_f32(A[int64_t(s0 + i0 + r) * K + k0 + kk]) : 0.f;
+    }
+    __syncthreads();
+    // the weights' unpacking stays here, after A's loads went out (hoisted out of the loop it
+    // would wait for every weight load before A's loads)
+#pragma unroll
+    for (int u = 0; u < kGgKb / 4; ++u) __asm__ volatile("" : "+v"(v[u]));
+    float acc[kGgRows][8];
+#pragma unroll
+    for (int r = 0; r < kGgRows; ++r)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[r][c] = 0.f;
+#pragma unroll
+    for (int u = 0; u < kGgKb / 4; ++u)
+#pragma unroll
+      for (int r = 0; r < kGgRows; ++r) {
+        const float xv = xs[r][wave + 4 * u];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          acc[r][2 * c] = __builtin_fmaf(xv, bf16_lo(v[u][c]), acc[r][2 * c]);
+          acc[r][2 * c + 1] = __builtin_fmaf(xv, bf16_hi(v[u][c]), acc[r][2 * c + 1]);
+        }
+      }
+#pragma unroll
+    for (int r = 0; r < kGgRows; ++r)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) red[wave][r][8 * lane + c] = acc[r][c];
+    __syncthreads();
+    for (int t = threadIdx.x; t < kGgRows * kColBlock; t += kGemvThreads) {
+      const int r = t / kColBlock, c = t - r * kColBlock, n = n0 + c;
+      if (r < rb && n < N)
+        part[((int64_t(p) * splits + split) * a_rows + i0 + r) * N + n] =
+            (red[0][r][c] + red[1][r][c]) + (red[2][r][c] + red[3][r][c]);
+    }
+    __syncthreads();   // xs and red are refilled by the next rows
+    i0 += kGgRows;
+  } while (i0 < nr);
+}
+
+// Workgroup (program, 64 columns): C[start + i, n] = bf16(sum over slices) for the program's rows i;
+// 4 slice groups of 64 lanes, each lane 8 slices in flight.
+constexpr int kGgFinCols = 64;
+__global__ __launch_bounds__(256) void ggemv_finish(const float* __restrict__ part, const int32_t* __restrict__ grp,
+                                                    const int32_t* __restrict__ gstart,
+                                                    const int32_t* __restrict__ grows, int ntab, int nweights,
+                                                    int a_rows, int splits, int N, uint16_t* __restrict__ C) {
+  __shared__ float red[4][kGgFinCols];
+  const int p = blockIdx.y;
+  const int g = grp[p];
+  if (!gg_weight(g, ntab, nweights)) return;   // uniform
+  const int s0 = gstart[g], nr = grows[g];
+  if (!gg_rows(s0, nr, a_rows)) return;        // uniform
+  const int c = threadIdx.x % kGgFinCols, sg = threadIdx.x / kGgFinCols;
+  const int n = blockIdx.x * kGgFinCols + c;
+  const int64_t sstride = int64_t(a_rows) * N;
+  for (int i = 0; i < nr; ++i) {
+    const float* base = part + (int64_t(p) * splits * a_rows + i) * N + min(n, N - 1);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int sp0 = sg; sp0 < splits; sp0 += 32) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int sp = sp0 + 4 * u;
+        acc[u] += sp < splits ? base[int64_t(min(sp, splits - 1)) * sstride] : 0.f;
+      }
+    }
+    red[sg][c] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    __syncthreads();
+    if (sg == 0 && n < N) C[int64_t(s0 + i) * N + n] = f32_to_bf16((red[0][c] + red[1][c]) + (red[2][c] + red[3][c]));
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // decode attention
 
 constexpr int kD = 128;
@@ -626,5 +748,39 @@ PTB_EXPORT int ptb_attn_decode_bf16(const void* q, const void* k, const void* v,
     case 6: launch_attn_decode<6>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
     default: launch_attn_decode<8>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
   }
+  return launch_status();
+}
+
+PTB_EXPORT size_t ptb_grouped_gemm_workspace_bytes(int64_t nprog, int64_t a_rows, int64_t k, int64_t n) {
+  if (nprog <= 0 || a_rows <= 0 || a_rows > kGgMaxRows || k <= 0 || n < 8 || nprog > 65535) return 0;
+  const int64_t splits = (k + kGgKb - 1) / kGgKb;
+  return size_t(nprog * splits * a_rows * n) * sizeof(float);
+}
+
+PTB_EXPORT int ptb_grouped_gemm_bf16_ws(const void* a, const void* b, const int32_t* group, const int32_t* start,
+                                        const int32_t* rows, void* c, int64_t nprog, int64_t ntab, int64_t a_rows,
+                                        int64_t nweights, int64_t k, int64_t n, int64_t weight_stride,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  const size_t need = ptb_grouped_gemm_workspace_bytes(nprog, a_rows, k, n);
+  // the MFMA path for more rows (or no workspace); it also owns the argument checks below
+  if (need == 0 || !workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
+    return ptb_grouped_gemm_bf16(a, b, group, start, rows, c, nprog, ntab, a_rows, nweights, k, n, weight_stride,
+                                 stream);
+  if (ntab < 0 || nweights < 0) return PTB_ERR_SHAPE;
+  if (!a || !b || !group || !start || !rows || !c) return PTB_ERR_NULL;
+  if (k % 64 || n % 8 || nprog > 256) return PTB_ERR_UNSUPPORTED;
+  if (weight_stride < k * n || ntab > 0x7fffffff || nweights > 0x7fffffff || k > 0x7fffffff || n > 0x7fffffff)
+    return PTB_ERR_SHAPE;
+  if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (weight_stride % 8)) return PTB_ERR_ALIGN;
+  const int splits = int((k + kGgKb - 1) / kGgKb);
+  if (splits > 65535) return PTB_ERR_GRID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  ggemv_partial<<<dim3(unsigned((n + kColBlock - 1) / kColBlock), unsigned(splits), unsigned(nprog)),
+                  dim3(kGemvThreads), 0, s>>>(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), group,
+                                              start, rows, int(ntab), int(nweights), int(a_rows), weight_stride, int(k),
+                                              int(n), splits, part);
+  ggemv_finish<<<dim3(unsigned((n + kGgFinCols - 1) / kGgFinCols), unsigned(nprog)), dim3(256), 0, s>>>(
+      part, group, start, rows, int(ntab), int(nweights), int(a_rows), splits, int(n), static_cast<uint16_t*>(c));
   return launch_status();
 }

@@ -119,6 +119,9 @@ SIGNATURES = {
     "ptb_rms_broadcast_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_f32, _vp]),
     "ptb_grouped_gemm_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_i64, _vp]),
+    "ptb_grouped_gemm_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "ptb_grouped_gemm_bf16_ws": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                          _c_i64, _vp, _c_size, _vp]),
     "ptb_attn_decode_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "ptb_attn_decode_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _vp, _c_size,
                                       _vp]),

@@ -252,9 +252,11 @@ def rms_broadcast(x, a, ss, w, out, eps: float = 1e-6) -> torch.Tensor:
     return out
 
 
-def grouped_gemm(a, b, group, start, rows, c, k: int, n: int, weight_stride: int) -> torch.Tensor:
+def grouped_gemm(a, b, group, start, rows, c, k: int, n: int, weight_stride: int, workspace=None,
+                 gemv: bool = True) -> torch.Tensor:
     """For each program p: C[start[g] + i, :] = A[start[g] + i, :] @ B[g] (bf16, fp32 accumulation)
-    for i < rows[g], g = group[p]; B[g] is row-major [k, n] at b + g * weight_stride."""
+    for i < rows[g], g = group[p]; B[g] is row-major [k, n] at b + g * weight_stride.  With at most
+    16 rows in A (and `gemv`), the split-K GEMV form (its workspace allocated here unless given)."""
     _need(a, "a", BF16)
     _need(b, "b", BF16)
     _need(c, "c", BF16)
@@ -263,7 +265,14 @@ def grouped_gemm(a, b, group, start, rows, c, k: int, n: int, weight_stride: int
     _numel(rows, start.numel(), "rows")
     if a.numel() % k or c.numel() != (a.numel() // k) * n:
         raise ValueError("a must be [R, k] and c [R, n]")
-    _lib.call("ptb_grouped_gemm_bf16", a.data_ptr(), b.data_ptr(), group.data_ptr(), start.data_ptr(), rows.data_ptr(),
-              c.data_ptr(), group.numel(), start.numel(), a.numel() // k, b.numel() // weight_stride, k, n,
-              weight_stride, _stream(a))
+    args = (a.data_ptr(), b.data_ptr(), group.data_ptr(), start.data_ptr(), rows.data_ptr(), c.data_ptr(),
+            group.numel(), start.numel(), a.numel() // k, b.numel() // weight_stride, k, n, weight_stride)
+    need = _lib.load().ptb_grouped_gemm_workspace_bytes(group.numel(), a.numel() // k, k, n) if gemv else 0
+    if need:
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=a.device)
+        _lib.call("ptb_grouped_gemm_bf16_ws", *args, workspace.data_ptr(),
+                  workspace.numel() * workspace.element_size(), _stream(a))
+    else:
+        _lib.call("ptb_grouped_gemm_bf16", *args, _stream(a))
     return c

@@ -197,8 +197,11 @@ def _tables(ti, e):
 
 
 @pytest.mark.parametrize("t,k_dim,n,skew", [(1024, 2048, 1536, False), (1024, 768, 2048, True), (1, 2048, 1536, False),
-                                            (200, 512, 256, True)])
+                                            (200, 512, 256, True), (1, 768, 2048, False), (2, 2048, 1536, True),
+                                            (2, 128, 520, False)])
 def test_grouped_gemm(t, k_dim, n, skew):
+    """MFMA tiles for many rows; at most 16 rows (t <= 2 with top-8) the split-K GEMV form, with
+    one row a group at decode and ragged groups of up to 2 rows when skewed."""
     e, k = 128, 8
     _, ti = _routing(t, e, k, t + n, skew)
     group, starts, rows = _tables(ti, e)
@@ -227,6 +230,26 @@ def test_grouped_gemm_skips_tables_outside_a():
     want[:16] = (a.reshape(64, k_dim)[:16].double() @ b.reshape(2, k_dim, n)[0].double()).to(F32).to(BF16)
     close_scaled(c.cpu(), want.reshape(-1), "grouped gemm with bad tables")
     assert torch.equal(c.cpu().reshape(64, n)[16:], c0.reshape(64, n)[16:])
+
+
+@pytest.mark.parametrize("gemv", [True, False])
+def test_grouped_gemm_few_rows_tables(gemv):
+    """Sixteen rows of A (the GEMV form when allowed): a group of 6 rows (two passes of 4 over the
+    weight slice), a group listed by two programs, entries past A's rows, past the weights and
+    negative, and rows no program covers keep C's values; both forms give the same result."""
+    k_dim, n = 256, 136
+    a = torch.randn(16 * k_dim, generator=gen(20)).to(BF16)
+    b = (torch.randn(3 * k_dim * n, generator=gen(21)) / 8).to(BF16)
+    group = torch.tensor([0, 1, 1, 2, 3, -1, 4], dtype=I32)
+    starts = torch.tensor([0, 6, 14, 9, 0], dtype=I32)
+    rows = torch.tensor([6, 3, 3, 2, 0], dtype=I32)   # group 2 runs past row 16; group 3 has no weight
+    c0 = torch.randn(16 * n, generator=gen(22)).to(BF16)
+    c = c0.to(DEV)
+    moe.grouped_gemm(a.to(DEV), b.to(DEV), group.to(DEV), starts.to(DEV), rows.to(DEV), c, k_dim, n, k_dim * n,
+                     gemv=gemv)
+    want = oracle.grouped_mm(a, b, group, starts, rows, k_dim, n, k_dim * n, c=c0)
+    close_scaled(c.cpu(), want, f"grouped gemm few rows gemv={gemv}")
+    assert torch.equal(c.cpu().reshape(16, n)[9:], c0.reshape(16, n)[9:])
 
 
 def test_moe_layer_chain_matches_the_oracle():
