@@ -58,20 +58,23 @@ __global__ __launch_bounds__(kB) void cast_i64_i32(const int64_t* __restrict__ x
 // ---------------------------------------------------------------- single-block scans
 constexpr int kScanThreads = 1024, kScanPer = 8, kScanMax = kScanThreads * kScanPer;
 
-// Inclusive scan of the block's per-thread totals (int64) in LDS; returns this thread's exclusive
-// prefix.  All kScanThreads threads call it.
+// Exclusive prefix of the per-thread totals (int64) over the block: an inclusive scan within each
+// wave (shift-up shuffles), then every wave adds the totals of the waves before it (one LDS pass,
+// two barriers).  All kScanThreads threads call it; `s` holds at least one int64 per wave.
 __device__ __forceinline__ int64_t block_exclusive_scan(int64_t t, int64_t* s) {
-  s[threadIdx.x] = t;
-  __syncthreads();
-  for (int off = 1; off < kScanThreads; off <<= 1) {
-    const int64_t add = threadIdx.x >= off ? s[threadIdx.x - off] : 0;
-    __syncthreads();
-    s[threadIdx.x] += add;
-    __syncthreads();
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int64_t v = t;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t u = __shfl_up(v, off, 64);
+    v += lane >= off ? u : 0;
   }
-  const int64_t incl = s[threadIdx.x];
+  if (lane == 63) s[w] = v;
   __syncthreads();
-  return incl - t;
+  int64_t before = 0;
+  for (int i = 0; i < w; ++i) before += s[i];
+  __syncthreads();   // s is reused by the caller's next scan
+  return before + v - t;
 }
 
 template <typename InT, typename OutT>
@@ -221,6 +224,31 @@ __device__ __forceinline__ void store_sorted(void* v, int64_t* idx, int64_t at, 
 }
 __device__ __forceinline__ bool key_less(int64_t ka, int32_t ia, int64_t kb, int32_t ib) {
   return (ka < kb) | ((ka == kb) & (ia < ib));   // bitwise: no short-circuit branches
+}
+
+// Rows of at most kRankSortMax keys: one workgroup per row, a key per thread in LDS; the stable
+// position of key i is the number of keys ordered before it (smaller, or equal at a lower
+// position), counted in one pass over the row's keys (the bitonic network's log^2 stages of
+// barriers cost more than these few hundred compares).
+constexpr int kRankSortMax = 256;
+__global__ __launch_bounds__(kRankSortMax) void sort_rank(const void* __restrict__ x, int e, bool is_f32, bool desc,
+                                                          void* __restrict__ v, int64_t* __restrict__ idx) {
+  __shared__ int64_t ks[kRankSortMax];
+  const int64_t row = blockIdx.x;
+  const int i = threadIdx.x;
+  const void* xr = is_f32 ? static_cast<const void*>(static_cast<const float*>(x) + row * e)
+                          : static_cast<const void*>(static_cast<const int64_t*>(x) + row * e);
+  const int64_t k = sort_key(xr, i < e ? i : e - 1, is_f32, desc);
+  ks[i] = k;
+  __syncthreads();
+  if (i >= e) return;
+  int rank = 0;
+#pragma unroll 8
+  for (int j = 0; j < e; ++j) {
+    const int64_t o = ks[j];
+    rank += int((o < k) | ((o == k) & (j < i)));
+  }
+  store_sorted(static_cast<uint8_t*>(v) + row * e * (is_f32 ? 4 : 8), idx + row * e, rank, k, i, is_f32, desc);
 }
 
 constexpr int kSortChunk = 8192;   // elements one workgroup sorts in LDS (96 KB)
@@ -628,10 +656,28 @@ __global__ __launch_bounds__(kB) void combine_rows(const int64_t* __restrict__ i
 
 // ---------------------------------------------------------------- small row / elementwise kernels
 // out[r, j] = bf16(x[r, j] / sum_j x[r, j]) (normalize) or out[r] = sum_j x[r, j] (row sum), fp32 x.
+// Rows of up to 16 values: every load of the row in flight at once (slots past k reload the row's
+// last value and add nothing), the sum in the same order as the plain loop.
 __global__ __launch_bounds__(kB) void normalize_rows(const float* __restrict__ x, int64_t rows, int k,
                                                      uint16_t* __restrict__ out_bf16, float* __restrict__ out_sum) {
   const int64_t r = int64_t(blockIdx.x) * kB + threadIdx.x;
   if (r >= rows) return;
+  if (k <= 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = x[r * k + (j < k ? j : k - 1)];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s += j < k ? v[j] : 0.f;
+    if (out_sum) {
+      out_sum[r] = s;
+      return;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < k) out_bf16[r * k + j] = f32_to_bf16(v[j] / s);
+    return;
+  }
   float s = 0.f;
   for (int j = 0; j < k; ++j) s += x[r * k + j];
   if (out_sum) {
@@ -846,6 +892,11 @@ PTB_EXPORT int ptb_sort_rows(const void* x, int key_dtype, void* values, int64_t
   if (e > (int64_t(1) << 30) || rows > 65535) return PTB_ERR_UNSUPPORTED;
   const bool f32 = key_dtype == PTB_DTYPE_F32, desc = descending != 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (e <= kRankSortMax) {
+    sort_rank<<<dim3(unsigned(rows)), dim3(unsigned((e + kWave - 1) / kWave * kWave)), 0, s>>>(x, int(e), f32, desc,
+                                                                                             values, indices);
+    return launch_status();
+  }
   if (e <= kSortChunk) {
     int p = 1;
     while (p < e) p <<= 1;

@@ -69,8 +69,11 @@ def test_expert_count_and_rank(r, e, lo, hi):
 
 @pytest.mark.parametrize("rows,e,kind,desc", [(1, 8192, "int", False), (1, 8, "int", False), (1, 32768, "int", False),
                                               (3, 12345, "int", False), (2, 1000, "float", True), (1, 20000, "float", False),
-                                              (4, 4096, "float", True), (1, 1, "int", False)])
+                                              (4, 4096, "float", True), (1, 1, "int", False), (5, 256, "float", False),
+                                              (3, 200, "int", True), (2, 257, "int", False), (7, 63, "float", True)])
 def test_sort_rows(rows, e, kind, desc):
+    """The rank sort (rows of at most 256 keys), one bitonic workgroup (up to 8192), chunks plus merge
+    passes beyond; ties, signed zeros, NaN and infinities keep the reference's order."""
     g = gen(rows * 7 + e)
     if kind == "int":
         x = torch.randint(0, 128, (rows * e,), generator=g, dtype=I64)          # many ties: stability matters
