@@ -406,7 +406,9 @@ __global__ __launch_bounds__(256) void splitk_finish(const float* __restrict__ P
 bool split_plan(int64_t m, int64_t n, int64_t k, int* splits, int* kchunk) {
   const int64_t cus = cu_count();
   const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-  if (k < 512 || tiles * 4 > cus) return false;   // a quarter of the CUs or more: 64x128 tiles instead
+  // measured over the bundle's GEMM shapes: below K = 1024 one pass over K (about 7 us) beats
+  // partials plus the finish launch; slices under 256 deep cost more in pipeline fill than they save
+  if (k < 1024 || tiles * 4 > cus) return false;   // a quarter of the CUs or more: 64x128 tiles instead
   int64_t s = (cus + tiles - 1) / tiles;
   if (s > k / 256) s = k / 256;
   if (s < 2) return false;

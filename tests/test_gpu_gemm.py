@@ -114,7 +114,7 @@ def test_gemm_fp8(m, k, n):
 
 @pytest.mark.parametrize("m,k,n,resid", [
     (128, 2048, 128, False), (8, 2048, 768, False), (512, 2048, 128, True), (32, 3072, 768, False),
-    (1000, 4096, 264, True), (64, 768, 2048, False), (256, 12288, 512, True),
+    (1000, 4096, 264, True), (64, 1024, 2048, False), (256, 12288, 512, True),
 ])
 def test_split_k_gemm(m, k, n, resid):
     """Shapes with few output tiles run split-K (fp32 partials, one finish pass): the same result as
@@ -130,6 +130,17 @@ def test_split_k_gemm(m, k, n, resid):
     scale = float(want.float().abs().mean())
     assert_close(split, want, RTOL, 2e-2 * scale, f"split-K {m}x{k}x{n}")
     assert_close(split, single, RTOL, 2e-2 * scale, f"split-K vs single pass {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(64, 768, 2048), (256, 960, 768)])
+def test_no_split_below_1024(m, k, n):
+    """Below K = 1024 a single pass over K is faster than partials plus a finish: no workspace is
+    asked for, and the result matches the oracle."""
+    assert _lib.load().ptb_gemm_bf16_workspace_bytes(m, n, k) == 0
+    a, b = randn((m, k), 35, std=1 / 32), randn((k, n), 36)
+    got = ops.gemm(a.to(DEV), b.to(DEV)).cpu()
+    want = oracle.gemm(a, b)
+    assert_close(got, want, RTOL, 2e-2 * float(want.float().abs().mean()), f"no split {m}x{k}x{n}")
 
 
 def test_split_k_exact_on_small_integers():
