@@ -385,12 +385,26 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
 namespace {
 
 // C = bf16(sum_s P[s] (+ R)), 4 consecutive elements per thread.
+// Eight slices' loads go out before any is added (a plain loop waits for each in turn); the sum
+// keeps the slice order, P_0 + P_1 + ... .
 __global__ __launch_bounds__(256) void splitk_finish(const float* __restrict__ P, int splits, int64_t mn,
                                                      const uint16_t* __restrict__ R, uint16_t* __restrict__ C) {
   const int64_t q = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (q >= mn) return;
-  f32x4v acc = *reinterpret_cast<const f32x4v*>(P + q);
-  for (int s = 1; s < splits; ++s) acc += *reinterpret_cast<const f32x4v*>(P + int64_t(s) * mn + q);
+  f32x4v acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    f32x4v v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int sl = s0 + u < splits ? s0 + u : splits - 1;
+      v[u] = *reinterpret_cast<const f32x4v*>(P + int64_t(sl) * mn + q);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int sl = s0 + u;
+      acc = sl == 0 ? v[u] : (sl < splits ? acc + v[u] : acc);
+    }
+  }
   if (R) {
     const u32x2 rr = *reinterpret_cast<const u32x2*>(R + q);
     acc.x += bf16_lo(rr[0]);
