@@ -159,8 +159,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __r
   }
 }
 
-// 16 columns a workgroup, 16 split groups of 16 lanes: each lane sums every 16th split with its
-// loads independent (the partials come from L2 or another XCD: latency, not bandwidth, bounds this)
+// 16 columns a workgroup, 16 split groups of 16 lanes: each lane sums every 16th split, eight of
+// its loads in flight before the first add (the partials come from L2 or another XCD: latency,
+// not bandwidth, bounds this; up to 128 splits cost one round trip)
 constexpr int kFinCols = 16;
 __global__ __launch_bounds__(256) void gemv_finish(const float* __restrict__ part, int splits, int N,
                                                    const uint16_t* __restrict__ r1, const uint16_t* __restrict__ r2,
@@ -168,16 +169,20 @@ __global__ __launch_bounds__(256) void gemv_finish(const float* __restrict__ par
   __shared__ float red[16][kFinCols];
   const int c = threadIdx.x % kFinCols, sg = threadIdx.x / kFinCols;
   const int n = blockIdx.x * kFinCols + c;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float acc = 0.f;
   if (n < N) {
-    int sp = sg;
-    for (; sp + 48 < splits; sp += 64) {
+    for (int sp0 = sg; sp0 < splits; sp0 += 128) {
+      float v[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc[u] += part[int64_t(sp + 16 * u) * N + n];
+      for (int u = 0; u < 8; ++u) {
+        const int sp = sp0 + 16 * u;
+        v[u] = part[int64_t(sp < splits ? sp : splits - 1) * N + n];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += sp0 + 16 * u < splits ? v[u] : 0.f;
     }
-    for (; sp < splits; sp += 16) acc[0] += part[int64_t(sp) * N + n];
   }
-  red[sg][c] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  red[sg][c] = acc;
   __syncthreads();
   if (sg == 0 && n < N) {
     float s = 0.f;
