@@ -117,13 +117,23 @@ int ptb_gemm_bf16(const void* a, const void* b, const void* residual, void* c, i
                   int64_t k, void* stream);
 
 /* The same GEMM with a caller workspace for split-K: when the 128x128 output tiles would fill at
- * most a quarter of the CUs (and K >= 512), K is cut into slices multiplied by separate workgroups into
+ * most a quarter of the CUs (and K >= 1024), K is cut into slices multiplied by separate workgroups into
  * fp32 partials that a finish pass sums (+ residual) and rounds once.  ptb_gemm_bf16_workspace_bytes
  * is 0 for shapes that do not split; then ptb_gemm_bf16_ws is ptb_gemm_bf16.
  * Replaces: the same kernels as ptb_gemm_bf16 (the small M x N gemm_<M>x<K>x<N>_bf16 shapes). */
 size_t ptb_gemm_bf16_workspace_bytes(int64_t m, int64_t n, int64_t k);
 int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n, int64_t k,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* The gate_up GEMM with the SwiGLU gate fused into its epilogue: for A [m, k] and B [k, 2*inter]
+ * (gate columns [0, inter), up columns [inter, 2*inter)), C [m, inter] = bf16( silu(g) * u ) with
+ * g, u = bf16(A . B[:, j]) and bf16(A . B[:, inter + j]) and silu(g) = g / (1 + e^-g), fp32 --
+ * bit for bit what ptb_gemm_bf16 followed by ptb_silu_mul_bf16 give, without the [m, 2*inter]
+ * intermediate.  k % 64 == 0, inter % 128 == 0.
+ * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/09_..._fused__to_copy_add_mean_mm_mul_pow_rsqrt_5ojlpnva's
+ *           gate_up product together with 10_..._fused__to_copy_mul_silu_slice_ktzl5s2h (the pair
+ *           ptb_amd.qwen3's prefill layer launches back to back; the bundle's manifests keep them apart). */
+int ptb_gemm_swiglu_bf16(const void* a, const void* b, void* c, int64_t m, int64_t inter, int64_t k, void* stream);
 
 /* Per-row dynamic e4m3 quantisation of bf16 activations: scale[r] = max_c |x[r,c]| / 448,
  * xq[r,c] = e4m3fn(x[r,c] / scale[r]) (round to nearest even; an all-zero row gets scale 1).

@@ -80,7 +80,12 @@ constexpr int kMaxPrograms = 256;
 
 // Split-K mode: workgroup (tile, blockIdx.y = s) multiplies K columns [s*kchunk, s*kchunk + kchunk)
 // and stores its fp32 partial tile at part + s*M*N; splitk_finish sums the partials.
-enum { kPlain = 0, kGrouped = 1, kSplit = 2 };
+// SwiGLU mode (the gate_up GEMM with silu(gate) * up fused into its epilogue): B is [K, 2*I] with
+// gate columns [0, I) and up columns [I, 2I); a 256x256 workgroup tile's B columns alternate in
+// 32-wide blocks between gate and up columns of the same 128 output columns, so each wave's
+// accumulator pairs (j even: gate, j + 1: up) cover the same outputs and the epilogue stores
+// bf16(silu(bf16(gate)) * bf16(up)), as a separate silu_mul would compute it from the bf16 GEMM.
+enum { kPlain = 0, kGrouped = 1, kSplit = 2, kSwiGLU = 3 };
 
 template <int WM, int WN, bool RESID, int MODE>
 __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_kernel(
@@ -154,7 +159,7 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     const int tm = first_m + (pid % width) % gsize;
     const int tn = (pid % width) / gsize;
     m0 = tm * BM;
-    n0 = tn * BN;
+    n0 = MODE == kSwiGLU ? tn * (BN / 2) : tn * BN;   // SwiGLU: the output (and gate) column base
   }
 
   const int tid = threadIdx.x;
@@ -179,7 +184,12 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   for (int t = 0; t < Sh::kDmaB; ++t) {
     const int k = Sh::kBRowsPerKB * (wave * Sh::kDmaB + t) + lane / Sh::kBSlots;
     const int bchunk = (lane % Sh::kBSlots) ^ (4 * (k & 3));
-    b_voff[t] = uint32_t(k * N + bchunk * 8) * 2u;
+    int bcol = bchunk * 8;
+    if constexpr (MODE == kSwiGLU) {   // 32-wide block b: gate (b even) or up (b odd) of pair b / 2
+      const int b = bchunk >> 2;
+      bcol = ((b & 1) ? N / 2 : 0) + 32 * (b >> 1) + 8 * (bchunk & 3);
+    }
+    b_voff[t] = uint32_t(k * N + bcol) * 2u;
   }
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
   // t-th of this wave's DMA instructions of stage kt (A first, then B)
@@ -299,6 +309,33 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     }
   }
   wait_vmcnt<0>();
+
+  if constexpr (MODE == kSwiGLU) {
+    // pair jp of this wave: gate acc[i][2jp], up acc[i][2jp+1] -> output columns
+    // n0 + 32*(wn*WN/2 + jp) + 8*(r/4) + 4*(lane/32) + r%4 of C [M, N/2]
+    const int Nout = N / 2;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int row = m0 + wm * (BM / 2) + i * 32 + fr;
+      if (row >= M) continue;
+#pragma unroll
+      for (int jp = 0; jp < WN / 2; ++jp) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = n0 + 32 * (wn * (WN / 2) + jp) + 8 * g + 4 * h;
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float gv = bf16_to_f32(f32_to_bf16(acc[i][2 * jp][4 * g + e]));
+            const float uv = bf16_to_f32(f32_to_bf16(acc[i][2 * jp + 1][4 * g + e]));
+            o[e] = (gv / (__builtin_amdgcn_exp2f(-gv * 1.4426950408889634f) + 1.0f)) * uv;
+          }
+          *reinterpret_cast<u32x2*>(C + int64_t(row) * Nout + col) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        }
+      }
+    }
+    return;
+  }
 
   // ---- epilogue: accumulator (i, j, r) of lane -> C row m0 + wm*BM/2 + i*32 + lane%32,
   //      column n0 + wn*BN/2 + j*32 + 8*(r/4) + 4*(lane/32) + r%4: 4 consecutive columns per r/4
@@ -464,6 +501,26 @@ PTB_EXPORT int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residu
   const int64_t mn = m * n;
   splitk_finish<<<dim3(unsigned((mn / 4 + 255) / 256)), dim3(256), 0, s>>>(
       part, splits, mn, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(c));
+  return launch_status();
+}
+
+PTB_EXPORT int ptb_gemm_swiglu_bf16(const void* a, const void* b, void* c, int64_t m, int64_t inter, int64_t k,
+                                    void* stream) {
+  if (m < 0 || inter < 0 || k < 0) return PTB_ERR_SHAPE;
+  if (m == 0 || inter == 0) return PTB_OK;
+  if (!a || !b || !c) return PTB_ERR_NULL;
+  if (k == 0 || k % 64 || inter % 128) return PTB_ERR_UNSUPPORTED;
+  const int64_t n = 2 * inter;
+  if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
+  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || int64_t(256) * k * 2 >= (int64_t(1) << 32))
+    return PTB_ERR_UNSUPPORTED;
+  if (!aligned16(a) || !aligned16(b) || !aligned16(c)) return PTB_ERR_ALIGN;
+  const int64_t tm = (m + 255) / 256, tn = inter / 128;
+  if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
+  const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
+  gemm_bf16_kernel<4, 4, false, kSwiGLU><<<dim3(unsigned(tm * tn)), dim3(kThreads), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, static_cast<uint16_t*>(c), int(m),
+      int(n), int(k), int(tm), int(tn), none, nullptr, 0);
   return launch_status();
 }
 

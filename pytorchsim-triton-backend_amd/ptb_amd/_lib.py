@@ -89,6 +89,7 @@ SIGNATURES = {
     "ptb_gemm_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "ptb_gemm_bf16_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "ptb_gemm_bf16_ws": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_size, _vp]),
+    "ptb_gemm_swiglu_bf16": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "ptb_quant_rows_e4m3": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp]),
     "ptb_quant_weight_e4m3": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp]),
     "ptb_gemm_fp8_scaled": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),

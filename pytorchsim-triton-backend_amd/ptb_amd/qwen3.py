@@ -12,6 +12,9 @@ HIP stream:
   K00 rmsnorm(h, w_post)          K09 gu = hn Wgu        K10 a = silu(g) * u
   K11 y = a Wd + h
 
+K09 and K10 run as one kernel (``ops.gemm_swiglu``: the gate_up GEMM with silu(g) * u in its
+epilogue, bit for bit the pair's result), so the [T, 2*I] gate_up product never goes to HBM.
+
 (The data flow is read from each kernel's index arithmetic; the reference times these kernels
 separately and never runs the layer end to end, validation/gemm/simulate_shapes.py:279-302.)
 """
@@ -116,7 +119,7 @@ class Qwen3Layer:
                 "qh": e(c.heads, tokens, c.head_dim), "kh": e(c.kv_heads, tokens, c.head_dim),
                 "vh": e(c.kv_heads, tokens, c.head_dim), "oh": e(c.heads, tokens, c.head_dim),
                 "o": e(tokens, c.heads, c.head_dim), "h": e(tokens, c.hidden), "hn": e(tokens, c.hidden),
-                "gu": e(tokens, 2 * c.intermediate), "a": e(tokens, c.intermediate), "y": e(tokens, c.hidden),
+                "a": e(tokens, c.intermediate), "y": e(tokens, c.hidden),
             }
         return self._bufs[key]
 
@@ -151,8 +154,7 @@ class Qwen3Layer:
         ops.transpose_heads(b["oh"], out=b["o"])                                            # K07
         ops.gemm(b["o"].view(t, c.heads * c.head_dim), w["wo"], residual=x, out=b["h"])     # K08
         ops.rmsnorm(b["h"], w["w_post"], c.eps, out=b["hn"])                                # K00
-        ops.gemm(b["hn"], w["wgu"], out=b["gu"])                                            # K09
-        ops.silu_mul(b["gu"], out=b["a"])                                                   # K10
+        ops.gemm_swiglu(b["hn"], w["wgu"], out=b["a"])                                      # K09 + K10
         ops.gemm(b["a"], w["wd"], residual=b["h"], out=y)                                   # K11
         return y
 

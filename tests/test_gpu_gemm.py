@@ -160,3 +160,27 @@ def test_gemm_64x128_tiles(m, k, n, resid):
     """Mid-size shapes whose 128x128 tiles leave CUs idle but too many to split run 64x128 tiles."""
     c, want = run_gemm(m, k, n, 41, 1 / 32, 1 / 16, resid)
     assert_close(c, want, RTOL, 2e-2 * float(want.float().abs().mean()), f"64x128 {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,k,inter", [(2048, 4096, 12288), (300, 512, 256), (64, 128, 128), (1000, 1024, 384)])
+def test_gemm_swiglu_fused(m, k, inter):
+    """The gate_up GEMM with silu(g) * u in its epilogue equals the two launches it replaces bit for
+    bit (same accumulation per output, the same roundings and formula), and the oracle within the
+    bf16 bound; rows past a 256-row tile's end (m = 300, 1000) are not stored."""
+    a = randn((m, k), 41, std=1 / 16)
+    b = randn((k, 2 * inter), 42, std=1 / 4)
+    ad, bd = a.to(DEV), b.to(DEV)
+    fused = ops.gemm_swiglu(ad, bd).cpu()
+    pair = ops.silu_mul(ops.gemm(ad, bd, split_k=False)).cpu()
+    assert bits_equal(fused, pair)
+    if m * k * inter <= 300 * 512 * 256:
+        want = oracle.silu_mul(oracle.gemm(a, b))
+        assert_close(fused, want, RTOL, 2e-2 * float(want.float().abs().mean()), f"swiglu {m}x{k}x{inter}")
+
+
+def test_gemm_swiglu_refusals():
+    a = torch.zeros((64, 128), dtype=torch.bfloat16, device=DEV)
+    b = torch.zeros((128, 2 * 192), dtype=torch.bfloat16, device=DEV)     # inter = 192: not a multiple of 128
+    with pytest.raises(_lib.UnsupportedError):
+        ops.gemm_swiglu(a, b)
+
