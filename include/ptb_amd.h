@@ -163,6 +163,14 @@ int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* wq_t, const
 int ptb_flash_attn_fwd_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
                             int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale,
                             int causal, void* stream);
+/* The same attention with O written token-major, o [batch, seq, hq, 128] (row t of batch b holds
+ * every query head's output for token t), the layout the layer's output projection reads: the
+ * separate head transpose after attention is not needed.
+ * Replaces: 06__prefill_kernel together with 07_..._fused_clone_select_transpose_ei42assc of
+ *           qwen3_8b_layer_prefill_2048x2048_bf16 (attention, then O -> [T, 32, 128]). */
+int ptb_flash_attn_fwd_tokens_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
+                                   int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale, int causal,
+                                   void* stream);
 
 /* ---- single-token (decode) path: qwen3_8b_layer_decode_1x<S>_bf16 and attention_decode_* ---- */
 

@@ -162,7 +162,8 @@ __device__ __forceinline__ void pv_step(WaveState& w, const bf16x8 (&pf)[2][2], 
 template <int WAVES>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-    uint16_t* __restrict__ O, int S, int hq, int hkv, int nkv, int nt, float c, int negate, int causal) {
+    uint16_t* __restrict__ O, int S, int hq, int hkv, int nkv, int nt, float c, int negate, int causal,
+    int o_tokens) {
   constexpr int BQ = 32 * WAVES;               // query rows per workgroup
   constexpr int kDmaT = 16 / WAVES;            // DMA instructions per wave per 16 KB tile
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
@@ -288,7 +289,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
   const float l = pair32_sum(w.l);
   const float inv = 1.f / l;
-  uint16_t* orow = op + int64_t(qi) * D;
+  // O [batch*hq, S, D] (head-major), or with o_tokens O [batch, S, hq, D] (token-major)
+  uint16_t* orow = o_tokens ? O + ((int64_t(b) * S + qi) * hq + (kvh * G + g)) * D : op + int64_t(qi) * D;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -302,9 +304,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
 }  // namespace
 
-PTB_EXPORT int ptb_flash_attn_fwd_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
-                                       int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale,
-                                       int causal, void* stream) {
+static int flash_launch(const void* q, const void* k, const void* v, void* o, int64_t batch, int64_t hq, int64_t hkv,
+                        int64_t seq, int64_t head_dim, float scale, int causal, int o_tokens, void* stream) {
   if (batch < 0 || hq <= 0 || hkv <= 0 || seq < 0 || head_dim <= 0) return PTB_ERR_SHAPE;
   if (hq % hkv) return PTB_ERR_SHAPE;
   if (head_dim != D) return PTB_ERR_UNSUPPORTED;
@@ -331,10 +332,22 @@ PTB_EXPORT int ptb_flash_attn_fwd_bf16(const void* q, const void* k, const void*
   if (wide)
     flash_fwd_kernel<8><<<dim3(unsigned(total)), dim3(512), 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv),
                                                                    int(nkv), int(nt), c, scale < 0.f ? 1 : 0,
-                                                                   causal ? 1 : 0);
+                                                                   causal ? 1 : 0, o_tokens);
   else
     flash_fwd_kernel<4><<<dim3(unsigned(total)), dim3(256), 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv),
                                                                    int(nkv), int(nt), c, scale < 0.f ? 1 : 0,
-                                                                   causal ? 1 : 0);
+                                                                   causal ? 1 : 0, o_tokens);
   return launch_status();
+}
+
+PTB_EXPORT int ptb_flash_attn_fwd_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
+                                       int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale,
+                                       int causal, void* stream) {
+  return flash_launch(q, k, v, o, batch, hq, hkv, seq, head_dim, scale, causal, 0, stream);
+}
+
+PTB_EXPORT int ptb_flash_attn_fwd_tokens_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
+                                              int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale,
+                                              int causal, void* stream) {
+  return flash_launch(q, k, v, o, batch, hq, hkv, seq, head_dim, scale, causal, 1, stream);
 }

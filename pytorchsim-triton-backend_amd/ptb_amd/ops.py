@@ -225,8 +225,9 @@ def default_scale(head_dim: int) -> float:
 
 
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, hq: int, hkv: int, causal: bool = True,
-                    scale: float | None = None, out=None) -> torch.Tensor:
-    """Flash-attention forward over head-major q [B*hq, S, D], k/v [B*hkv, S, D] -> o like q."""
+                    scale: float | None = None, out=None, tokens_out: bool = False) -> torch.Tensor:
+    """Flash-attention forward over head-major q [B*hq, S, D], k/v [B*hkv, S, D] -> o like q, or with
+    `tokens_out` o [B, S, hq, D] (token-major, no separate head transpose)."""
     for t, name in ((q, "q"), (k, "k"), (v, "v")):
         _need(t, name, BF16, 3)
     bhq, s, d = q.shape
@@ -235,10 +236,10 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, hq: int, 
     batch = bhq // hq
     if tuple(k.shape) != (batch * hkv, s, d) or tuple(v.shape) != (batch * hkv, s, d):
         raise ValueError("k and v must be [B*hkv, S, D] matching q")
-    o = _out(out, tuple(q.shape), BF16, q)
+    o = _out(out, (batch, s, hq, d) if tokens_out else tuple(q.shape), BF16, q)
     sc = default_scale(d) if scale is None else float(scale)
-    _lib.call("ptb_flash_attn_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), batch, hq, hkv, s,
-              d, sc, 1 if causal else 0, _stream(q))
+    _lib.call("ptb_flash_attn_fwd_tokens_bf16" if tokens_out else "ptb_flash_attn_fwd_bf16", q.data_ptr(),
+              k.data_ptr(), v.data_ptr(), o.data_ptr(), batch, hq, hkv, s, d, sc, 1 if causal else 0, _stream(q))
     return o
 
 

@@ -13,7 +13,8 @@ HIP stream:
   K11 y = a Wd + h
 
 K09 and K10 run as one kernel (``ops.gemm_swiglu``: the gate_up GEMM with silu(g) * u in its
-epilogue, bit for bit the pair's result), so the [T, 2*I] gate_up product never goes to HBM.
+epilogue, bit for bit the pair's result), so the [T, 2*I] gate_up product never goes to HBM, and
+K06 writes O token-major, [T, 32, 128], so K07's transpose is not launched.
 
 (The data flow is read from each kernel's index arithmetic; the reference times these kernels
 separately and never runs the layer end to end, validation/gemm/simulate_shapes.py:279-302.)
@@ -117,7 +118,7 @@ class Qwen3Layer:
             self._bufs[key] = {
                 "xn": e(tokens, c.hidden), "q": e(tokens, qd), "k": e(tokens, kd), "v": e(tokens, kd),
                 "qh": e(c.heads, tokens, c.head_dim), "kh": e(c.kv_heads, tokens, c.head_dim),
-                "vh": e(c.kv_heads, tokens, c.head_dim), "oh": e(c.heads, tokens, c.head_dim),
+                "vh": e(c.kv_heads, tokens, c.head_dim),
                 "o": e(tokens, c.heads, c.head_dim), "h": e(tokens, c.hidden), "hn": e(tokens, c.hidden),
                 "a": e(tokens, c.intermediate), "y": e(tokens, c.hidden),
             }
@@ -150,8 +151,8 @@ class Qwen3Layer:
         main.wait_event(ev[1])
         main.wait_event(ev[2])
         ops.flash_attention(b["qh"], b["kh"], b["vh"], c.heads, c.kv_heads, True,
-                            1.0 / math.sqrt(c.head_dim), out=b["oh"])                       # K06
-        ops.transpose_heads(b["oh"], out=b["o"])                                            # K07
+                            1.0 / math.sqrt(c.head_dim), out=b["o"].view(1, t, c.heads, c.head_dim),
+                            tokens_out=True)                                                # K06 + K07
         ops.gemm(b["o"].view(t, c.heads * c.head_dim), w["wo"], residual=x, out=b["h"])     # K08
         ops.rmsnorm(b["h"], w["w_post"], c.eps, out=b["hn"])                                # K00
         ops.gemm_swiglu(b["hn"], w["wgu"], out=b["a"])                                      # K09 + K10

@@ -62,6 +62,19 @@ def test_flash_constant_v():
     assert (o - 0.75).abs().max() <= 0.75 * 2 ** -7
 
 
+@pytest.mark.parametrize("batch,hq,hkv,s", [(1, 32, 8, 2048), (2, 4, 2, 384), (1, 8, 8, 128)])
+def test_flash_tokens_out_is_the_transposed_output(batch, hq, hkv, s):
+    """The token-major output ([B, S, hq, D]) holds exactly the head-major output's values,
+    transposed: the same kernel, only the store address differs."""
+    q = randn((batch * hq, s, 128), 51).to(DEV)
+    k = randn((batch * hkv, s, 128), 52).to(DEV)
+    v = randn((batch * hkv, s, 128), 53).to(DEV)
+    heads = ops.flash_attention(q, k, v, hq, hkv, True).cpu()
+    tokens = ops.flash_attention(q, k, v, hq, hkv, True, tokens_out=True).cpu()
+    assert tokens.shape == (batch, s, hq, 128)
+    assert bits_equal(tokens, heads.view(batch, hq, s, 128).transpose(1, 2).contiguous())
+
+
 def test_flash_refuses_bad_shapes():
     q = torch.zeros((4, 100, 128), dtype=torch.bfloat16, device=DEV)
     with pytest.raises(_lib.UnsupportedError):
