@@ -185,6 +185,8 @@ int ptb_sumsq_bf16(const void* x, const void* y, float* out, int64_t n, void* st
  *   ptb_gemv_bf16:          xp = x.
  *     Replaces decode 04_..._fused_add_select_transpose_view_vumxrjnr_triton.py:17-42 (o-projection).
  *   ptb_gemv_rmsnorm_bf16:  xp = ((x + add) * rsqrt(ss[0]/k + eps)) * g, all fp32; add may be NULL.
+ *     ss may be NULL: then every workgroup forms sum((x + add)^2) over k itself (x, add 16-byte
+ *     aligned), which saves the ptb_sumsq_bf16 launch a decode step otherwise makes before it.
  *     Replaces decode 01_..._fused__to_copy_add_mean_mm_mul_pow_rsqrt_ddfn4f75_triton.py:17-55 (q-projection)
  *     and 06_..._5gopcdje_triton.py:17-57 (gate/up projection after the post-attention norm).
  *   ptb_gemv_silu_bf16:     xp = silu(gate_up[k']) * gate_up[k + k'] (gate_up holds 2k values);

@@ -114,7 +114,31 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __r
   const int k0 = split * kb;
   const int rows = min(K - k0, kb);
   float r = 0.f;
-  if constexpr (MODE == kRms) r = 1.f / sqrtf(ss[0] / float(K) + eps);
+  if constexpr (MODE == kRms) {
+    float sv;
+    if (ss) {
+      sv = ss[0];
+    } else {   // no sum of squares given: every workgroup forms sum (x + add)^2 over K itself (from L2)
+      float t = 0.f;
+      const int k8 = K / 8;
+      for (int i = threadIdx.x; i < k8; i += kGemvThreads) {
+        const u32x4 a = reinterpret_cast<const u32x4*>(x)[i];
+        const u32x4 b = add ? reinterpret_cast<const u32x4*>(add)[i] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float lo = bf16_lo(a[c]) + bf16_lo(b[c]), hi = bf16_hi(a[c]) + bf16_hi(b[c]);
+          t = __builtin_fmaf(lo, lo, t);
+          t = __builtin_fmaf(hi, hi, t);
+        }
+      }
+      for (int i = k8 * 8 + threadIdx.x; i < K; i += kGemvThreads) {
+        const float v = bf16_to_f32(x[i]) + (add ? bf16_to_f32(add[i]) : 0.f);
+        t = __builtin_fmaf(v, v, t);
+      }
+      sv = block_sum<kGemvThreads / kWave>(t, &red[0][0]);
+    }
+    r = 1.f / sqrtf(sv / float(K) + eps);
+  }
   for (int i = threadIdx.x; i < rows; i += kGemvThreads) xs[i] = prologue<MODE>(x, add, g, r, k0 + i, K);
   __syncthreads();
 
@@ -199,7 +223,8 @@ int launch_gemv(const void* x, const void* add, const float* ss, const void* g, 
                 void* stream) {
   if (k < 0 || n < 0) return PTB_ERR_SHAPE;
   if (n == 0) return PTB_OK;
-  if (!x || !w || !y || (MODE == kRms && (!ss || !g))) return PTB_ERR_NULL;
+  if (!x || !w || !y || (MODE == kRms && !g)) return PTB_ERR_NULL;
+  if (MODE == kRms && !ss && (!aligned16(x) || (add && !aligned16(add)))) return PTB_ERR_ALIGN;
   if (k == 0) return PTB_ERR_UNSUPPORTED;
   if (k > 0x7fffffff || n > 0x7fffffff || k * n >= (int64_t(1) << 40)) return PTB_ERR_SHAPE;
   if (n % 8) return PTB_ERR_UNSUPPORTED;

@@ -280,9 +280,11 @@ def gemv(x: torch.Tensor, w: torch.Tensor, out=None, workspace=None) -> torch.Te
 
 def gemv_rmsnorm(x: torch.Tensor, ss: torch.Tensor, g: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None = None,
                  eps: float = 1e-6, out=None, workspace=None) -> torch.Tensor:
-    """y = bf16( (((x + add) * rsqrt(ss/K + eps)) * g) @ W ), the normalised vector kept in fp32."""
+    """y = bf16( (((x + add) * rsqrt(ss/K + eps)) * g) @ W ), the normalised vector kept in fp32.
+    ss=None: the kernel forms sum((x + add)^2) itself (no separate sumsq launch)."""
     _need(x, "x", BF16)
-    _need(ss, "ss", F32)
+    if ss is not None:
+        _need(ss, "ss", F32)
     _need(g, "g", BF16)
     if add is not None:
         _need(add, "add", BF16)
@@ -291,7 +293,8 @@ def gemv_rmsnorm(x: torch.Tensor, ss: torch.Tensor, g: torch.Tensor, w: torch.Te
     if g.numel() != x.numel():
         raise ValueError("g must match x")
     k, n, y, ws, wsb = _gemv_args(x.numel(), w, out, x, workspace)
-    _lib.call("ptb_gemv_rmsnorm_bf16", x.data_ptr(), add.data_ptr() if add is not None else None, ss.data_ptr(),
+    _lib.call("ptb_gemv_rmsnorm_bf16", x.data_ptr(), add.data_ptr() if add is not None else None,
+              ss.data_ptr() if ss is not None else None,
               g.data_ptr(), float(eps), w.data_ptr(), y.data_ptr(), k, n, ws.data_ptr(), wsb, _stream(x))
     return y
 

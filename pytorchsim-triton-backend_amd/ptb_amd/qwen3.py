@@ -208,16 +208,15 @@ class Qwen3DecodeLayer:
         c, w = self.cfg, self.w
         b = self.buffers(kcache.shape[1], x.device)
         y = b["y"] if out is None else out
-        ops.sumsq(x, out=b["ss"])                                                              # K00
-        ops.gemv_rmsnorm(x, b["ss"], w["w_in"], w["wq"], eps=c.eps, out=b["q"], workspace=b["ws"])  # K01
+        # K00's sum of squares is formed inside K01's (and K05's inside K06's) workgroups
+        ops.gemv_rmsnorm(x, None, w["w_in"], w["wq"], eps=c.eps, out=b["q"], workspace=b["ws"])  # K00 + K01
         ops.qk_norm_rope(b["q"].view(1, c.heads, c.head_dim), w["w_qn"], cos.view(1, c.head_dim),
                          sin.view(1, c.head_dim), c.eps, out=b["qh"])                          # K02
         ops.attention_decode(b["qh"].view(c.kv_heads, c.heads // c.kv_heads, c.head_dim), kcache, vcache,
                              1.0 / math.sqrt(c.head_dim), out=b["o"], workspace=b["attn_ws"])  # K03
         ops.gemv(b["o"].view(-1), w["wo"], out=b["a"], workspace=b["ws"])                      # K04
-        ops.sumsq(x, b["a"], out=b["ss2"])                                                     # K05
-        ops.gemv_rmsnorm(x, b["ss2"], w["w_post"], w["wgu"], add=b["a"], eps=c.eps, out=b["gu"],
-                         workspace=b["ws"])                                                    # K06
+        ops.gemv_rmsnorm(x, None, w["w_post"], w["wgu"], add=b["a"], eps=c.eps, out=b["gu"],
+                         workspace=b["ws"])                                                    # K05 + K06
         ops.gemv_silu(b["gu"], w["wd"], x, b["a"], out=y, workspace=b["ws"])                   # K07
         return y
 

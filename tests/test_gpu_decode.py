@@ -45,6 +45,11 @@ def test_gemv_plain_and_rmsnorm(k, n):
     ss1 = oracle.sumsq(x)
     got = ops.gemv_rmsnorm(xd, ss1.to(DEV), gd, wd, eps=1e-6).cpu()
     close_scaled(got, oracle.gemv_rmsnorm(x, ss1, g, w, eps=1e-6), f"gemv_rmsnorm {k}x{n}")
+    # no sum of squares passed: the workgroups form it themselves (with and without the add)
+    got = ops.gemv_rmsnorm(xd, None, gd, wd, add=ad, eps=1e-6).cpu()
+    close_scaled(got, oracle.gemv_rmsnorm(x, ss, g, w, add=a, eps=1e-6), f"gemv_rmsnorm own ss+add {k}x{n}")
+    got = ops.gemv_rmsnorm(xd, None, gd, wd, eps=1e-6).cpu()
+    close_scaled(got, oracle.gemv_rmsnorm(x, ss1, g, w, eps=1e-6), f"gemv_rmsnorm own ss {k}x{n}")
 
 
 @pytest.mark.parametrize("k,n", [(12288, 4096), (64, 8), (777, 264)])
