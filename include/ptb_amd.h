@@ -214,6 +214,18 @@ int ptb_attn_decode_bf16(const void* q, const void* k, const void* v, void* o, i
                          int64_t seq, int64_t head_dim, float scale, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* Decode attention with the query's per-head RMSNorm and rotate-half RoPE done in its prologue:
+ * q is the q projection's raw output [nkv, group, 128]; each workgroup normalizes (qnorm_w [128]
+ * bf16, eps) and rotates (cos_t / sin_t [128] fp32 of the token's position) its own query rows,
+ * rounding them to bf16 exactly as ptb_qk_norm_rope_bf16 does, then attends as
+ * ptb_attn_decode_bf16 (same workspace).  qnorm_w, cos_t, sin_t 16-byte aligned.
+ * Replaces: qwen3_8b_layer_decode_1x<S>_bf16/02__decode_kernel (q-norm + RoPE) together with
+ *           qwen3_8b_layer_decode_1x<S>_bf16/03__decode_kernel (attention). */
+int ptb_attn_decode_qnorm_rope_bf16(const void* q, const void* qnorm_w, const float* cos_t, const float* sin_t,
+                                    float eps, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
+                                    int64_t seq, int64_t head_dim, float scale, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
 /* ---- Qwen3-30B-A3B mixture-of-experts layer (validation/pytorchsim/layer_op_* and layer_layer_*).
  * Paths below are relative to validation/pytorchsim/; LOP_<op> = layer_op_<op>_1024x0_bf16 and
  * LL = layer_layer_prefill_1024x1024_bf16 (other token counts differ only in sizes).  Index

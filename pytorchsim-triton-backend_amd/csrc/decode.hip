@@ -440,7 +440,10 @@ __global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t*
                                                                  const uint16_t* __restrict__ Kc,
                                                                  const uint16_t* __restrict__ Vc,
                                                                  uint16_t* __restrict__ O, float* __restrict__ part,
-                                                                 int S, float c, int steps, int gsplit) {
+                                                                 int S, float c, int steps, int gsplit,
+                                                                 const uint16_t* __restrict__ qw,
+                                                                 const float* __restrict__ qcos,
+                                                                 const float* __restrict__ qsin, float qeps) {
   constexpr int kRec = int(record_floats(G));
   __shared__ float qs[G][kD];
   __shared__ float ts[T][G][kChunk];      // scores, then bf16-rounded p
@@ -459,12 +462,60 @@ __global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t*
   // branch for the load to sink into)
   const int qi = min(tid, G * kD / 8 - 1);
   const u32x4 qv = *reinterpret_cast<const u32x4*>(q + 8 * qi);
+  // fused q-norm + RoPE (qw given): lane qi holds dims 8*(qi%16).. of head qi/16, as the q/k-norm
+  // kernel lays them out; its weights and the token's cos/sin are read here too
+  const int qc = qi & 15;
+  u32x4 wv = {0u, 0u, 0u, 0u}, wp = {0u, 0u, 0u, 0u};
+  f32x4v cs0 = {0.f, 0.f, 0.f, 0.f}, cs1 = cs0, sn0 = cs0, sn1 = cs0;
+  if (qw) {
+    wv = reinterpret_cast<const u32x4*>(qw)[qc];
+    wp = reinterpret_cast<const u32x4*>(qw)[qc ^ 8];
+    cs0 = reinterpret_cast<const f32x4v*>(qcos + 8 * qc)[0];
+    cs1 = reinterpret_cast<const f32x4v*>(qcos + 8 * qc)[1];
+    sn0 = reinterpret_cast<const f32x4v*>(qsin + 8 * qc)[0];
+    sn1 = reinterpret_cast<const f32x4v*>(qsin + 8 * qc)[1];
+  }
   u32x4 kr[kChunk / 16], vr[kChunk / 16];
   load_step(kp, vp, first * kChunk, S, kj, d8, kr, vr);
+  float qf8[8];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    qs[0][8 * qi + 2 * e] = bf16_lo(qv[e]);
-    qs[0][8 * qi + 2 * e + 1] = bf16_hi(qv[e]);
+    qf8[2 * e] = bf16_lo(qv[e]);
+    qf8[2 * e + 1] = bf16_hi(qv[e]);
+  }
+  if (qw) {   // the q/k-norm kernel's arithmetic, rounded to bf16 as its output is
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(qf8[e], qf8[e], ss);
+    ss = row16_sum(ss);
+    float pf[8], wf[8], pw[8];
+    u32x4 pv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pv[e] = xor8_u32(qv[e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      pf[2 * e] = bf16_lo(pv[e]);
+      pf[2 * e + 1] = bf16_hi(pv[e]);
+      wf[2 * e] = bf16_lo(wv[e]);
+      wf[2 * e + 1] = bf16_hi(wv[e]);
+      pw[2 * e] = bf16_lo(wp[e]);
+      pw[2 * e + 1] = bf16_hi(wp[e]);
+    }
+    const float r = 1.0f / sqrtf(ss / float(kD) + qeps);
+    const float cs[8] = {cs0.x, cs0.y, cs0.z, cs0.w, cs1.x, cs1.y, cs1.z, cs1.w};
+    const float sn[8] = {sn0.x, sn0.y, sn0.z, sn0.w, sn1.x, sn1.y, sn1.z, sn1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = (qf8[e] * r) * wf[e];
+      const float pp = (pf[e] * r) * pw[e];
+      const float rot = qc < 8 ? -pp : pp;
+      qf8[e] = bf16_to_f32(f32_to_bf16(fmaf(a, cs[e], rot * sn[e])));
+    }
+  }
+  // lanes past the G*16 vectors hold repeats (whose norms are not their head's): they do not store
+  if (tid < G * kD / 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qs[0][8 * qi + e] = qf8[e];
   }
   if (ttid < G) {
     mrun[team][ttid] = -INFINITY;
@@ -684,23 +735,32 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
   }
 }
 
+// q-norm + RoPE fused into the prologue when qw is given (per-head weights [128], the token's
+// cos / sin [128]): q is then the projection's raw output
+struct QNorm {
+  const uint16_t* w;
+  const float* cos;
+  const float* sin;
+  float eps;
+};
+
 template <int G, int T>
 void launch_partial(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* part, int nkv,
-                    int seq, float c, const DecodePlan& p, hipStream_t s) {
+                    int seq, float c, const DecodePlan& p, const QNorm& qn, hipStream_t s) {
   attn_decode_partial<G, T><<<dim3(unsigned(p.records), unsigned(nkv * p.gsplit)), dim3(kTeam * T), 0, s>>>(
-      q, k, v, o, part, seq, c, p.steps, p.gsplit);
+      q, k, v, o, part, seq, c, p.steps, p.gsplit, qn.w, qn.cos, qn.sin, qn.eps);
 }
 
 // G: query rows per workgroup (the kv head's group / p.gsplit)
 template <int G>
 void launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* part, int nkv,
-                        int seq, float c, const DecodePlan& p, hipStream_t s) {
+                        int seq, float c, const DecodePlan& p, const QNorm& qn, hipStream_t s) {
   if (p.teams == 1) {
-    launch_partial<G, 1>(q, k, v, o, part, nkv, seq, c, p, s);
+    launch_partial<G, 1>(q, k, v, o, part, nkv, seq, c, p, qn, s);
   } else if (p.teams == 2) {
-    launch_partial<G, 2>(q, k, v, o, part, nkv, seq, c, p, s);
+    launch_partial<G, 2>(q, k, v, o, part, nkv, seq, c, p, qn, s);
   } else {
-    if constexpr (G <= 3) launch_partial<G, 4>(q, k, v, o, part, nkv, seq, c, p, s);
+    if constexpr (G <= 3) launch_partial<G, 4>(q, k, v, o, part, nkv, seq, c, p, qn, s);
   }
   if (p.records > 1)
     attn_decode_merge<G><<<dim3(unsigned(nkv * p.gsplit), unsigned(G)), dim3(256), 0, s>>>(part, o, p.records);
@@ -749,9 +809,9 @@ PTB_EXPORT size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, in
   return size_t(nkv * p.gsplit * p.records * record_floats(group / p.gsplit)) * sizeof(float);
 }
 
-PTB_EXPORT int ptb_attn_decode_bf16(const void* q, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
-                                    int64_t seq, int64_t head_dim, float scale, void* workspace,
-                                    size_t workspace_bytes, void* stream) {
+static int attn_decode_entry(const void* q, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
+                             int64_t seq, int64_t head_dim, float scale, const QNorm& qn, void* workspace,
+                             size_t workspace_bytes, void* stream) {
   if (nkv < 0 || group <= 0 || seq <= 0 || head_dim <= 0) return PTB_ERR_SHAPE;
   if (head_dim != kD) return PTB_ERR_UNSUPPORTED;
   if (group != 1 && group != 2 && group != 3 && group != 4 && group != 6 && group != 8) return PTB_ERR_UNSUPPORTED;
@@ -771,14 +831,32 @@ PTB_EXPORT int ptb_attn_decode_bf16(const void* q, const void* k, const void* v,
   const DecodePlan p = decode_plan(seq, group);
   if (nkv * p.gsplit > 65535) return PTB_ERR_GRID;
   switch (group / p.gsplit) {
-    case 1: launch_attn_decode<1>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
-    case 2: launch_attn_decode<2>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
-    case 3: launch_attn_decode<3>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
-    case 4: launch_attn_decode<4>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
-    case 6: launch_attn_decode<6>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
-    default: launch_attn_decode<8>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, s); break;
+    case 1: launch_attn_decode<1>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
+    case 2: launch_attn_decode<2>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
+    case 3: launch_attn_decode<3>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
+    case 4: launch_attn_decode<4>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
+    case 6: launch_attn_decode<6>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
+    default: launch_attn_decode<8>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
   }
   return launch_status();
+}
+
+PTB_EXPORT int ptb_attn_decode_bf16(const void* q, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
+                                    int64_t seq, int64_t head_dim, float scale, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  return attn_decode_entry(q, k, v, o, nkv, group, seq, head_dim, scale, QNorm{nullptr, nullptr, nullptr, 0.f},
+                           workspace, workspace_bytes, stream);
+}
+
+PTB_EXPORT int ptb_attn_decode_qnorm_rope_bf16(const void* q, const void* qnorm_w, const float* cos_t,
+                                               const float* sin_t, float eps, const void* k, const void* v, void* o,
+                                               int64_t nkv, int64_t group, int64_t seq, int64_t head_dim, float scale,
+                                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (!qnorm_w || !cos_t || !sin_t) return PTB_ERR_NULL;
+  if (!aligned16(qnorm_w) || !aligned16(cos_t) || !aligned16(sin_t)) return PTB_ERR_ALIGN;
+  return attn_decode_entry(q, k, v, o, nkv, group, seq, head_dim, scale,
+                           QNorm{static_cast<const uint16_t*>(qnorm_w), cos_t, sin_t, eps}, workspace,
+                           workspace_bytes, stream);
 }
 
 PTB_EXPORT size_t ptb_grouped_gemm_workspace_bytes(int64_t nprog, int64_t a_rows, int64_t k, int64_t n) {

@@ -287,7 +287,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope(const uint16_t* __restric
   unpack8(v, f);
   float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+  for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
   ss = row16_sum(ss);
   u32x4 pv;
 #pragma unroll
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope(const uint16_t* __restric
     const float a = (f[e] * r) * wf[e];
     const float p = (pf[e] * r) * pw[e];
     const float rot = first_half ? -p : p;
-    o[e] = a * cs[e] + rot * sn[e];
+    o[e] = fmaf(a, cs[e], rot * sn[e]);   // explicit fma: the fused decode-attention prologue matches
   }
   reinterpret_cast<u32x4*>(out + (h * tokens + t) * D)[c] = pack8(o);
 }

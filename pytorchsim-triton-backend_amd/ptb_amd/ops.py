@@ -321,10 +321,12 @@ def gemv_silu(gate_up: torch.Tensor, w: torch.Tensor, res_a: torch.Tensor | None
 
 
 def attention_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None, out=None,
-                     workspace=None) -> torch.Tensor:
+                     workspace=None, qnorm=None) -> torch.Tensor:
     """One-token attention over a KV cache: q [NKV, G, D], k/v [NKV, S, D] bf16 -> o [NKV, G, D].
     `workspace`: ``ptb_attn_decode_workspace_bytes`` bytes (none for a cache of at most 256 keys,
-    which is a single pass)."""
+    which is a single pass).  `qnorm` = (w [D] bf16, cos [D] fp32, sin [D] fp32, eps): q is then the
+    raw projection, normalized and rotated in the kernel's prologue exactly as :func:`qk_norm_rope`
+    would (one launch instead of two)."""
     _need(q, "q", BF16, 3)
     _need(k, "k", BF16, 3)
     _need(v, "v", BF16, 3)
@@ -337,7 +339,18 @@ def attention_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
     if workspace is None and need:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     sc = default_scale(d) if scale is None else float(scale)
-    _lib.call("ptb_attn_decode_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), nkv, g, s, d, sc,
-              workspace.data_ptr() if workspace is not None else None,
-              workspace.numel() * workspace.element_size() if workspace is not None else 0, _stream(q))
+    wsp = workspace.data_ptr() if workspace is not None else None
+    wsb = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    if qnorm is None:
+        _lib.call("ptb_attn_decode_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), nkv, g, s, d, sc,
+                  wsp, wsb, _stream(q))
+        return o
+    w, cos, sin, eps = qnorm
+    _need(w, "qnorm w", BF16, 1)
+    _need(cos, "cos", F32)
+    _need(sin, "sin", F32)
+    if w.numel() != d or cos.numel() != d or sin.numel() != d:
+        raise ValueError("qnorm w, cos and sin must hold D elements")
+    _lib.call("ptb_attn_decode_qnorm_rope_bf16", q.data_ptr(), w.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+              float(eps), k.data_ptr(), v.data_ptr(), o.data_ptr(), nkv, g, s, d, sc, wsp, wsb, _stream(q))
     return o

@@ -194,7 +194,7 @@ class Qwen3DecodeLayer:
                 return torch.empty(*shape, dtype=dtype, device=device)
 
             self._bufs[key] = {
-                "ss": e(1, dtype=torch.float32), "q": e(c.heads * c.head_dim), "qh": e(c.heads, 1, c.head_dim),
+                "ss": e(1, dtype=torch.float32), "q": e(c.heads * c.head_dim),
                 "o": e(c.kv_heads, c.heads // c.kv_heads, c.head_dim), "a": e(c.hidden),
                 "ss2": e(1, dtype=torch.float32), "gu": e(2 * c.intermediate), "y": e(c.hidden),
                 "ws": e(max(gemv_ws, 4), dtype=torch.uint8), "attn_ws": e(max(attn_ws, 4), dtype=torch.uint8),
@@ -210,10 +210,10 @@ class Qwen3DecodeLayer:
         y = b["y"] if out is None else out
         # K00's sum of squares is formed inside K01's (and K05's inside K06's) workgroups
         ops.gemv_rmsnorm(x, None, w["w_in"], w["wq"], eps=c.eps, out=b["q"], workspace=b["ws"])  # K00 + K01
-        ops.qk_norm_rope(b["q"].view(1, c.heads, c.head_dim), w["w_qn"], cos.view(1, c.head_dim),
-                         sin.view(1, c.head_dim), c.eps, out=b["qh"])                          # K02
-        ops.attention_decode(b["qh"].view(c.kv_heads, c.heads // c.kv_heads, c.head_dim), kcache, vcache,
-                             1.0 / math.sqrt(c.head_dim), out=b["o"], workspace=b["attn_ws"])  # K03
+        # K02's q-norm + RoPE runs in K03's prologue: each attention workgroup rotates its own q rows
+        ops.attention_decode(b["q"].view(c.kv_heads, c.heads // c.kv_heads, c.head_dim), kcache, vcache,
+                             1.0 / math.sqrt(c.head_dim), out=b["o"], workspace=b["attn_ws"],
+                             qnorm=(w["w_qn"], cos, sin, c.eps))                                 # K02 + K03
         ops.gemv(b["o"].view(-1), w["wo"], out=b["a"], workspace=b["ws"])                      # K04
         ops.gemv_rmsnorm(x, None, w["w_post"], w["wgu"], add=b["a"], eps=c.eps, out=b["gu"],
                          workspace=b["ws"])                                                    # K05 + K06

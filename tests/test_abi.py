@@ -65,6 +65,10 @@ def test_null_pointers_refused(lib):
     assert lib.ptb_gemm_bf16(P16, None, None, P16, 4, 64, 64, None) == _lib.PTB_ERR_NULL
     assert lib.ptb_softmax_rows_bf16(P16, None, 4, 64, None) == _lib.PTB_ERR_NULL
     assert lib.ptb_gemm_fp8_scaled(P16, P16, P16, None, P16, 4, 16, 128, None) == _lib.PTB_ERR_NULL
+    assert lib.ptb_attn_decode_qnorm_rope_bf16(P16, None, P16, P16, 1e-6, P16, P16, P16, 8, 4, 64, 128, 0.1,
+                                               None, 0, None) == _lib.PTB_ERR_NULL
+    assert lib.ptb_attn_decode_qnorm_rope_bf16(P16, P16 + 2, P16, P16, 1e-6, P16, P16, P16, 8, 4, 64, 128, 0.1,
+                                               None, 0, None) == _lib.PTB_ERR_ALIGN
 
 
 def test_shape_and_alignment_refused(lib):

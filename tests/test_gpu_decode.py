@@ -109,6 +109,27 @@ def test_attention_decode_range_plans(nkv, g, s):
     assert_close(got, oracle.attention_decode(q, k, v), RTOL, 2e-2, f"decode plan {nkv}x{g}x{s}")
 
 
+@pytest.mark.parametrize("nkv,g,s", [(8, 4, 1024), (8, 4, 4096), (2, 8, 9000), (3, 1, 100), (1, 3, 20000),
+                                     (4, 6, 600), (2, 2, 300)])
+def test_attention_decode_fused_qnorm_rope(nkv, g, s):
+    """q-norm + RoPE in the attention prologue gives the same bits as qk_norm_rope followed by
+    attention_decode (both round the rotated q to bf16 with the same fp32 arithmetic), over the
+    one-pass, team and range plans; and it matches the oracle's pair."""
+    qraw = randn((nkv * g, 128), 40)
+    w = randn((128,), 41, std=0.1, mean=1.0)
+    cos_t, sin_t = oracle.rope_tables(s + 1, 128, 1.0e6)
+    cos, sin = cos_t[s], sin_t[s]
+    k, v = randn((nkv, s, 128), 42), randn((nkv, s, 128), 43)
+    qd, wd, cd, sd, kd, vd = (t.to(DEV) for t in (qraw, w, cos, sin, k, v))
+    qh = ops.qk_norm_rope(qd.view(1, nkv * g, 128), wd, cd.view(1, 128), sd.view(1, 128), 1e-6)
+    pair = ops.attention_decode(qh.view(nkv, g, 128), kd, vd).cpu()
+    fused = ops.attention_decode(qd.view(nkv, g, 128), kd, vd, qnorm=(wd, cd, sd, 1e-6)).cpu()
+    assert bits_equal(fused, pair), f"fused q-norm differs from the pair {nkv}x{g}x{s}"
+    qo = oracle.qk_norm_rope(qraw.view(1, nkv * g, 128), w, cos.view(1, 128), sin.view(1, 128), 1e-6)
+    want = oracle.attention_decode(qo.view(nkv, g, 128), k, v)
+    assert_close(fused, want, RTOL, 2e-2, f"fused decode vs oracle {nkv}x{g}x{s}")
+
+
 def test_attention_decode_workspace_reuse():
     """One caller workspace serves consecutive calls of different shapes (each call's records
     replace the last call's)."""
