@@ -76,6 +76,10 @@ int ptb_silu_mul_bf16(const void* gate_up, void* out, int64_t rows, int64_t inte
  * [H,T,D] -> [T,H,D] replaces 07_..._ei42assc_triton.py:17-27. */
 int ptb_transpose_heads_bf16(const void* x, void* y, int64_t d0, int64_t d1, int64_t inner,
                              void* stream);
+/* The same with x's rows of d1*inner elements ld elements apart (ld >= d1*inner, ld % 8 == 0): reads
+ * the v part of a fused [T, q|k|v] projection output in place.  Replaces the same launch as above. */
+int ptb_transpose_heads_ld_bf16(const void* x, int64_t ld, void* y, int64_t d0, int64_t d1, int64_t inner,
+                                void* stream);
 
 /* Per-(token, head) RMSNorm (eps) with weight w[head_dim], then rotate-half RoPE with fp32
  * cos/sin [tokens, head_dim], stored head-major: out[h, t, :].  x is [tokens, heads, head_dim].
@@ -85,6 +89,11 @@ int ptb_transpose_heads_bf16(const void* x, void* y, int64_t d0, int64_t d1, int
 int ptb_qk_norm_rope_bf16(const void* x, const void* w, const float* cos_t, const float* sin_t,
                           void* out, int64_t tokens, int64_t heads, int64_t head_dim, float eps,
                           void* stream);
+/* The same with token t's heads starting at x + t*ld (ld >= heads*head_dim, ld % 8 == 0): reads the
+ * q or k part of a fused [T, q|k|v] projection output in place.  Replaces the same launches. */
+int ptb_qk_norm_rope_ld_bf16(const void* x, int64_t ld, const void* w, const float* cos_t, const float* sin_t,
+                             void* out, int64_t tokens, int64_t heads, int64_t head_dim, float eps,
+                             void* stream);
 
 /* Whole-tensor reduction to one fp32: PTB_REDUCE_SUM (fp32 accumulation) or PTB_REDUCE_MAX
  * (NaN-propagating).  workspace must hold ptb_reduce_workspace_bytes(n) bytes.

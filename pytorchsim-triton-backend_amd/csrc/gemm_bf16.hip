@@ -409,11 +409,13 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
   // the largest tile that still gives every CU a tile: 256x256, else 256x128; then 128x128 while its
-  // tiles cover half the CUs, else 64x128 (column tiles stay 128 wide: the B swizzle spans 16 chunks)
+  // tiles cover half the CUs, else 64x128 (column tiles stay 128 wide: the B swizzle spans 16 chunks).
+  // 256x256 also where 256x128 tiles would need a second round on the CUs: a 256x256 workgroup
+  // moves ~1.4x the flops per CU of a 256x128 one, so one round of it beats two of the smaller.
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t cus = cu_count();
   auto tiles = [&](int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
-  if (tiles(256, 256) >= cus) return launch_gemm<4, 4>(a, b, residual, c, m, n, k, s);
+  if (tiles(256, 256) >= cus || tiles(256, 128) > cus) return launch_gemm<4, 4>(a, b, residual, c, m, n, k, s);
   if (tiles(256, 128) >= cus) return launch_gemm<4, 2>(a, b, residual, c, m, n, k, s);
   if (tiles(128, 128) * 2 >= cus) return launch_gemm<2, 2>(a, b, residual, c, m, n, k, s);
   return launch_gemm<1, 2>(a, b, residual, c, m, n, k, s);   // 64 x 128: twice the tiles of 128 x 128

@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kBlock) void silu_mul(const uint16_t* __restrict__ 
 
 // ---------------------------------------------------------------- head transpose
 __global__ __launch_bounds__(kBlock) void transpose_heads(const u32x4* __restrict__ x, u32x4* __restrict__ y,
-                                                          int64_t d0, int64_t d1, int64_t ic,
+                                                          int64_t d0, int64_t d1, int64_t ic, int64_t xa,
                                                           int64_t total) {
   const int64_t stride = int64_t(gridDim.x) * kBlock;
   int64_t idx = int64_t(blockIdx.x) * kBlock + threadIdx.x;
@@ -257,10 +257,10 @@ __global__ __launch_bounds__(kBlock) void transpose_heads(const u32x4* __restric
   for (int i = 0; i < kPer; ++i) {
     id[i] = idx + i * stride;
     if (id[i] < total) {
-      // output chunk id -> (b, a, c) of y[d1, d0, ic]; source x[a, b, c]
+      // output chunk id -> (b, a, c) of y[d1, d0, ic]; source x[a, b, c], xa chunks between a rows
       const int64_t c = id[i] % ic, ba = id[i] / ic;
       const int64_t a = ba % d0, b = ba / d0;
-      v[i] = x[(a * d1 + b) * ic + c];
+      v[i] = x[a * xa + b * ic + c];
     }
   }
 #pragma unroll
@@ -276,13 +276,14 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope(const uint16_t* __restric
                                                        const float* __restrict__ cos_t,
                                                        const float* __restrict__ sin_t,
                                                        uint16_t* __restrict__ out, int64_t tokens,
-                                                       int heads, float eps) {
+                                                       int heads, int64_t ld, float eps) {
   constexpr int D = 128;
   const int64_t row = int64_t(blockIdx.x) * (kBlock / 16) + threadIdx.x / 16;  // = t * heads + h
   const int c = threadIdx.x % 16;
   const bool live = row < tokens * heads;
   const int64_t rr = live ? row : 0;
-  const u32x4 v = reinterpret_cast<const u32x4*>(x + rr * D)[c];
+  const int64_t t = rr / heads, h = rr - t * heads;   // token t's heads start ld elements apart
+  const u32x4 v = reinterpret_cast<const u32x4*>(x + t * ld + h * D)[c];
   float f[8];
   unpack8(v, f);
   float ss = 0.f;
@@ -299,7 +300,6 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope(const uint16_t* __restric
   unpack8(reinterpret_cast<const u32x4*>(w)[c], wf);
   unpack8(reinterpret_cast<const u32x4*>(w)[pc], pw);
   const float r = 1.0f / sqrtf(ss / float(D) + eps);
-  const int64_t t = rr / heads, h = rr - t * heads;
   const f32x4v* cp = reinterpret_cast<const f32x4v*>(cos_t + t * D + c * 8);
   const f32x4v* sp = reinterpret_cast<const f32x4v*>(sin_t + t * D + c * 8);
   const f32x4v c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
@@ -541,23 +541,32 @@ PTB_EXPORT int ptb_silu_mul_bf16(const void* gate_up, void* out, int64_t rows, i
   return launch_status();
 }
 
-PTB_EXPORT int ptb_transpose_heads_bf16(const void* x, void* y, int64_t d0, int64_t d1, int64_t inner,
-                                        void* stream) {
+PTB_EXPORT int ptb_transpose_heads_ld_bf16(const void* x, int64_t ld, void* y, int64_t d0, int64_t d1,
+                                           int64_t inner, void* stream) {
   if (d0 < 0 || d1 < 0 || inner <= 0) return PTB_ERR_SHAPE;
   if (d0 == 0 || d1 == 0) return PTB_OK;
+  if (ld < d1 * inner) return PTB_ERR_SHAPE;
   if (!x || !y) return PTB_ERR_NULL;
-  if (inner % 8 || !aligned16(x) || !aligned16(y)) return PTB_ERR_ALIGN;
+  if (inner % 8 || ld % 8 || !aligned16(x) || !aligned16(y)) return PTB_ERR_ALIGN;
   const int64_t total = d0 * d1 * (inner / 8);
   const int g = grid_for(total, int64_t(kBlock) * kPer, 1 << 20);
   transpose_heads<<<dim3(g), dim3(kBlock), 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const u32x4*>(x), static_cast<u32x4*>(y), d0, d1, inner / 8, total);
+      static_cast<const u32x4*>(x), static_cast<u32x4*>(y), d0, d1, inner / 8, ld / 8, total);
   return launch_status();
 }
 
-PTB_EXPORT int ptb_qk_norm_rope_bf16(const void* x, const void* w, const float* cos_t, const float* sin_t,
-                                     void* out, int64_t tokens, int64_t heads, int64_t head_dim, float eps,
-                                     void* stream) {
+PTB_EXPORT int ptb_transpose_heads_bf16(const void* x, void* y, int64_t d0, int64_t d1, int64_t inner,
+                                        void* stream) {
+  if (d0 < 0 || d1 < 0 || inner <= 0) return PTB_ERR_SHAPE;
+  return ptb_transpose_heads_ld_bf16(x, d1 * inner, y, d0, d1, inner, stream);
+}
+
+PTB_EXPORT int ptb_qk_norm_rope_ld_bf16(const void* x, int64_t ld, const void* w, const float* cos_t,
+                                        const float* sin_t, void* out, int64_t tokens, int64_t heads,
+                                        int64_t head_dim, float eps, void* stream) {
   if (tokens < 0 || heads <= 0 || head_dim <= 0) return PTB_ERR_SHAPE;
+  if (ld < heads * head_dim) return PTB_ERR_SHAPE;
+  if (ld % 8) return PTB_ERR_ALIGN;
   if (head_dim != 128) return PTB_ERR_UNSUPPORTED;
   if (tokens == 0) return PTB_OK;
   if (!x || !w || !cos_t || !sin_t || !out) return PTB_ERR_NULL;
@@ -569,8 +578,15 @@ PTB_EXPORT int ptb_qk_norm_rope_bf16(const void* x, const void* w, const float* 
   if (blocks > 0x7fffffff || heads > 0x7fffffff) return PTB_ERR_GRID;
   qk_norm_rope<<<dim3(unsigned(blocks)), dim3(kBlock), 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), cos_t, sin_t,
-      static_cast<uint16_t*>(out), tokens, int(heads), eps);
+      static_cast<uint16_t*>(out), tokens, int(heads), ld, eps);
   return launch_status();
+}
+
+PTB_EXPORT int ptb_qk_norm_rope_bf16(const void* x, const void* w, const float* cos_t, const float* sin_t,
+                                     void* out, int64_t tokens, int64_t heads, int64_t head_dim, float eps,
+                                     void* stream) {
+  if (tokens < 0 || heads <= 0 || head_dim <= 0) return PTB_ERR_SHAPE;
+  return ptb_qk_norm_rope_ld_bf16(x, heads * head_dim, w, cos_t, sin_t, out, tokens, heads, head_dim, eps, stream);
 }
 
 PTB_EXPORT size_t ptb_reduce_workspace_bytes(int64_t n) {

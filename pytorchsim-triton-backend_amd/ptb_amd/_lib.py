@@ -81,6 +81,8 @@ SIGNATURES = {
     "ptb_silu_mul_bf16": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "ptb_transpose_heads_bf16": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "ptb_qk_norm_rope_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_f32, _vp]),
+    "ptb_transpose_heads_ld_bf16": (_c_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _vp]),
+    "ptb_qk_norm_rope_ld_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_f32, _vp]),
     "ptb_reduce_workspace_bytes": (_c_size, [_c_i64]),
     "ptb_reduce_bf16": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _c_size, _vp]),
     "ptb_reduce_f32": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _c_size, _vp]),

@@ -79,19 +79,37 @@ def silu_mul(gate_up: torch.Tensor, out=None) -> torch.Tensor:
     return y
 
 
+def _row_ld(x: torch.Tensor, name: str):
+    """A bf16 [A, B, D] tensor whose [B, D] rows are each contiguous (a column slice of a wider
+    [A, L] matrix is one): None when x is contiguous, else the elements between consecutive rows."""
+    if not isinstance(x, torch.Tensor) or x.is_contiguous():
+        _need(x, name, BF16, 3)
+        return None
+    if x.device.type != "cuda" or x.dtype != BF16 or x.dim() != 3:
+        raise ValueError(f"{name} must be a 3-D bf16 GPU tensor")
+    a, b, d = x.shape
+    if x.stride(2) != 1 or x.stride(1) != d or x.stride(0) < b * d:
+        raise ValueError(f"{name} must have contiguous [B, D] rows (strides (ld, D, 1)), got {x.stride()}")
+    return x.stride(0)
+
+
 def transpose_heads(x: torch.Tensor, out=None) -> torch.Tensor:
-    """[A, B, D] -> [B, A, D] (exact)."""
-    _need(x, "x", BF16, 3)
+    """[A, B, D] -> [B, A, D] (exact).  x may be a column slice of a wider matrix (rows ld apart)."""
+    ld = _row_ld(x, "x")
     a, b, d = x.shape
     y = _out(out, (b, a, d), BF16, x)
-    _lib.call("ptb_transpose_heads_bf16", x.data_ptr(), y.data_ptr(), a, b, d, _stream(x))
+    if ld is None:
+        _lib.call("ptb_transpose_heads_bf16", x.data_ptr(), y.data_ptr(), a, b, d, _stream(x))
+    else:
+        _lib.call("ptb_transpose_heads_ld_bf16", x.data_ptr(), ld, y.data_ptr(), a, b, d, _stream(x))
     return y
 
 
 def qk_norm_rope(x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float = 1e-6,
                  out=None) -> torch.Tensor:
-    """x [T, H, D] -> per-head RMSNorm(w) + rotate-half RoPE -> [H, T, D]."""
-    _need(x, "x", BF16, 3)
+    """x [T, H, D] -> per-head RMSNorm(w) + rotate-half RoPE -> [H, T, D].  x may be a column slice
+    of a wider matrix (token rows ld apart), as the q or k part of a fused q|k|v projection."""
+    ld = _row_ld(x, "x")
     _need(w, "w", BF16, 1)
     _need(cos, "cos", F32, 2)
     _need(sin, "sin", F32, 2)
@@ -99,8 +117,12 @@ def qk_norm_rope(x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch
     if w.numel() != d or tuple(cos.shape) != (t, d) or tuple(sin.shape) != (t, d):
         raise ValueError("w must be [D] and cos/sin [T, D]")
     y = _out(out, (h, t, d), BF16, x)
-    _lib.call("ptb_qk_norm_rope_bf16", x.data_ptr(), w.data_ptr(), cos.data_ptr(), sin.data_ptr(), y.data_ptr(),
-              t, h, d, float(eps), _stream(x))
+    if ld is None:
+        _lib.call("ptb_qk_norm_rope_bf16", x.data_ptr(), w.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                  y.data_ptr(), t, h, d, float(eps), _stream(x))
+    else:
+        _lib.call("ptb_qk_norm_rope_ld_bf16", x.data_ptr(), ld, w.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                  y.data_ptr(), t, h, d, float(eps), _stream(x))
     return y
 
 

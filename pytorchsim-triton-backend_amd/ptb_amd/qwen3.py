@@ -2,9 +2,7 @@
 
 The launch sequence is the reference bundle's: validation/pytorchsim/qwen3_8b_layer_prefill_2048x2048_bf16/
 manifest.json lists 14 launches of 12 kernels, 00,01,02,03,04,03,05,06,07,08,00,09,10,11, and
-:meth:`Qwen3Layer.forward` issues them in that order, the k branch (K03, K04) and the v branch
-(K03, K05) on two side streams that fork after K00 and join before K06, the rest on the current
-HIP stream:
+:meth:`Qwen3Layer.forward` computes them in that order on the current HIP stream:
 
   K00 rmsnorm(x, w_in)            K01 q = xn Wq          K02 q-norm + RoPE -> [32,T,128]
   K03 k = xn Wk                   K04 k-norm + RoPE      K03 v = xn Wv      K05 v -> [8,T,128]
@@ -12,7 +10,10 @@ HIP stream:
   K00 rmsnorm(h, w_post)          K09 gu = hn Wgu        K10 a = silu(g) * u
   K11 y = a Wd + h
 
-K09 and K10 run as one kernel (``ops.gemm_swiglu``: the gate_up GEMM with silu(g) * u in its
+K01 and the two K03 launches run as one GEMM over the concatenated weight [hidden, q|k|v] (one round
+of 256x256 tiles fills the chip; the separate k and v GEMMs have 128 tiles each and leave half the
+CUs idle), and K02, K04 and K05 read their column slices of its [T, q|k|v] output in place (the
+same per-element arithmetic as the separate products).  K09 and K10 run as one kernel (``ops.gemm_swiglu``: the gate_up GEMM with silu(g) * u in its
 epilogue, bit for bit the pair's result), so the [T, 2*I] gate_up product never goes to HBM, and
 K06 writes O token-major, [T, 32, 128], so K07's transpose is not launched.
 
@@ -89,21 +90,16 @@ class Qwen3Layer:
         self.cfg = cfg
         self._tables = {}
         self._bufs = {}
-        self._streams = {}
+        # the q, k and v projections run as one GEMM over [hidden, q|k|v] (a copy made once): one
+        # round of 256x256 tiles on the chip instead of three GEMMs whose k and v parts leave most
+        # CUs idle
+        self.wqkv = torch.cat([weights["wq"], weights["wk"], weights["wv"]], dim=1).contiguous()
 
     def tables(self, tokens: int, device):
         key = (tokens, str(device))
         if key not in self._tables:
             self._tables[key] = rope_tables(tokens, self.cfg.head_dim, self.cfg.rope_theta, device)
         return self._tables[key]
-
-    def side_streams(self, device):
-        """Two side streams (default priority) and three events for the k/v branches, per device."""
-        key = str(device)
-        if key not in self._streams:
-            self._streams[key] = (torch.cuda.Stream(device), torch.cuda.Stream(device),
-                                  [torch.cuda.Event() for _ in range(3)])
-        return self._streams[key]
 
     def buffers(self, tokens: int, device) -> dict:
         """Activation buffers for one forward at this length, allocated once and reused."""
@@ -116,7 +112,7 @@ class Qwen3Layer:
                 return torch.empty(*shape, dtype=BF16, device=device)
 
             self._bufs[key] = {
-                "xn": e(tokens, c.hidden), "q": e(tokens, qd), "k": e(tokens, kd), "v": e(tokens, kd),
+                "xn": e(tokens, c.hidden), "qkv": e(tokens, qd + 2 * kd),
                 "qh": e(c.heads, tokens, c.head_dim), "kh": e(c.kv_heads, tokens, c.head_dim),
                 "vh": e(c.kv_heads, tokens, c.head_dim),
                 "o": e(tokens, c.heads, c.head_dim), "h": e(tokens, c.hidden), "hn": e(tokens, c.hidden),
@@ -131,25 +127,15 @@ class Qwen3Layer:
         b = self.buffers(t, x.device)
         y = b["y"] if out is None else out
         ops.rmsnorm(x, w["w_in"], c.eps, out=b["xn"])                                       # K00
-        # the q, k and v branches are independent: k and v run on side streams, so their small
-        # GEMMs share the chip with q's instead of each leaving most CUs idle
-        main = torch.cuda.current_stream(x.device)
-        sk, sv, ev = self.side_streams(x.device)
-        ev[0].record(main)
-        with torch.cuda.stream(sk):
-            sk.wait_event(ev[0])
-            ops.gemm(b["xn"], w["wk"], out=b["k"])                                          # K03
-            ops.qk_norm_rope(b["k"].view(t, c.kv_heads, c.head_dim), w["w_kn"], cos, sin, c.eps, out=b["kh"])  # K04
-            ev[1].record(sk)
-        with torch.cuda.stream(sv):
-            sv.wait_event(ev[0])
-            ops.gemm(b["xn"], w["wv"], out=b["v"])                                          # K03
-            ops.transpose_heads(b["v"].view(t, c.kv_heads, c.head_dim), out=b["vh"])       # K05
-            ev[2].record(sv)
-        ops.gemm(b["xn"], w["wq"], out=b["q"])                                              # K01
-        ops.qk_norm_rope(b["q"].view(t, c.heads, c.head_dim), w["w_qn"], cos, sin, c.eps, out=b["qh"])   # K02
-        main.wait_event(ev[1])
-        main.wait_event(ev[2])
+        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        qkv = b["qkv"]
+        ops.gemm(b["xn"], self.wqkv, out=qkv)                                              # K01 + K03
+        # the norms and the v transpose read their column slices of [T, q|k|v] in place
+        ops.qk_norm_rope(qkv[:, :qd].view(t, c.heads, c.head_dim), w["w_qn"], cos, sin, c.eps,
+                         out=b["qh"])                                                        # K02
+        ops.qk_norm_rope(qkv[:, qd:qd + kd].view(t, c.kv_heads, c.head_dim), w["w_kn"], cos, sin, c.eps,
+                         out=b["kh"])                                                        # K04
+        ops.transpose_heads(qkv[:, qd + kd:].view(t, c.kv_heads, c.head_dim), out=b["vh"])   # K05
         ops.flash_attention(b["qh"], b["kh"], b["vh"], c.heads, c.kv_heads, True,
                             1.0 / math.sqrt(c.head_dim), out=b["o"].view(1, t, c.heads, c.head_dim),
                             tokens_out=True)                                                # K06 + K07

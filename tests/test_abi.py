@@ -82,6 +82,9 @@ def test_shape_and_alignment_refused(lib):
     assert lib.ptb_gemm_fp8_scaled(P16, P16, P16, P16, P16, 4, 16, 64, None) == _lib.PTB_ERR_UNSUPPORTED
     assert lib.ptb_qk_norm_rope_bf16(P16, P16, P16, P16, P16, 4, 2, 64, 1e-6, None) == _lib.PTB_ERR_UNSUPPORTED
     assert lib.ptb_transpose_heads_bf16(P16, P16, 2, 3, 4, None) == _lib.PTB_ERR_ALIGN
+    assert lib.ptb_transpose_heads_ld_bf16(P16, 100, P16, 2, 3, 128, None) == _lib.PTB_ERR_SHAPE   # ld < 3*128
+    assert lib.ptb_qk_norm_rope_ld_bf16(P16, 4000, P16, P16, P16, P16, 4, 32, 128, 1e-6, None) == _lib.PTB_ERR_SHAPE
+    assert lib.ptb_qk_norm_rope_ld_bf16(P16, 4100, P16, P16, P16, P16, 4, 32, 128, 1e-6, None) == _lib.PTB_ERR_ALIGN
     assert lib.ptb_reduce_bf16(P16, P16, 64, 5, P16, 4096, None) == _lib.PTB_ERR_DTYPE
     assert lib.ptb_reduce_bf16(P16, P16, 64, 0, P16, 4, None) == _lib.PTB_ERR_WORKSPACE
 

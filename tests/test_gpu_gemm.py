@@ -41,6 +41,7 @@ def run_gemm(m, k, n, seed, std_a, std_b, resid=False):
     (2048, 4096, 1024, False),    # L2048/03 k/v_proj
     (2048, 4096, 4096, True),     # L2048/08 o_proj + residual
     (2048, 12288, 4096, True),    # L2048/11 down + residual
+    (2048, 4096, 6144, False),    # fused q|k|v projection: 256x256 tiles (256x128 would take two rounds)
 ])
 def test_gemm_layer_shapes(m, k, n, resid):
     std = 1.0 / 64.0

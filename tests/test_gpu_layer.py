@@ -32,7 +32,10 @@ def test_layer_matches_oracle_small():
 
 def test_layer_full_size_is_its_launch_chain():
     """T = S = 2048: the layer's forward is exactly the 14-launch chain, so
-    re-running the chain op by op gives bit-identical output (deterministic kernels)."""
+    re-running the chain op by op gives bit-identical output (deterministic kernels).  The forward's
+    fused q|k|v GEMM (256x256 tiles) and its strided norm / transpose reads give the bits of the
+    separate q, k, v products (other tile shapes): every tile issues the same MFMA over K in the
+    same order."""
     cfg = qwen3.QWEN3_8B
     t = 2048
     w = {k: v.to(DEV) for k, v in qwen3.random_weights(cfg, seed=0).items()}

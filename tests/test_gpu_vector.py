@@ -90,6 +90,25 @@ def test_transpose_heads_exact(shape):
     assert bits_equal(got, oracle.transpose_heads(x))
 
 
+@pytest.mark.parametrize("tokens,cols", [(2048, (4096, 1024, 1024)), (5, (384, 128, 256)), (1, (128, 128, 128))])
+def test_row_strided_slices_exact(tokens, cols):
+    """q-norm + RoPE and the head transpose over column slices of a [T, q|k|v] matrix (rows ld
+    apart) give the bits of the same calls on contiguous copies of the slices."""
+    qd, kd, vd = cols
+    qkv = randn((tokens, qd + kd + vd), 50).to(DEV)
+    w = randn((128,), 51, std=0.1, mean=1.0).to(DEV)
+    cos, sin = (t.to(DEV) for t in oracle.rope_tables(tokens, 128, 1.0e6))
+    for lo, width in ((0, qd), (qd, kd)):
+        sl = qkv[:, lo:lo + width].view(tokens, width // 128, 128)
+        assert not sl.is_contiguous() or tokens == 1
+        got = ops.qk_norm_rope(sl, w, cos, sin, 1e-6)
+        assert bits_equal(got, ops.qk_norm_rope(sl.contiguous(), w, cos, sin, 1e-6))
+    sl = qkv[:, qd + kd:].view(tokens, vd // 128, 128)
+    assert bits_equal(ops.transpose_heads(sl), ops.transpose_heads(sl.contiguous()))
+    with pytest.raises(ValueError):   # rows must be contiguous inside
+        ops.transpose_heads(qkv.view(tokens, -1, 128)[:, :, :64])
+
+
 @pytest.mark.parametrize("tokens,heads,tables,seed", [
     (2048, 32, "bundle", 0),   # L2048/02: cos/sin drawn by the spec's make_inputs (randn)
     (2048, 8, "rope", 1),      # L2048/04 with real theta=1e6 tables
