@@ -456,9 +456,30 @@ __global__ __launch_bounds__(256) void splitk_finish(const float* __restrict__ P
 
 // Split-K plan for a GEMM whose 128x128 tiles would fill at most a quarter of the CUs: S slices of kchunk
 // (a multiple of 64, at least 256) columns so that tiles * S roughly covers the chip once.
-bool split_plan(int64_t m, int64_t n, int64_t k, int* splits, int* kchunk) {
+// Wide form (*wide = true, 256x256 tiles): where 256x256 tiles fill at most half the CUs and one
+// round of smaller tiles would be chosen instead, S = CUs / tiles slices of at least kWideMinChunk
+// columns give every CU a 256x256 workgroup (~1.4x the flops per CU of a 256x128 one), at the cost
+// of the fp32 partials and the finish pass.  Measured: 2048x12288x4096 (+ residual) 205 -> 198 us in
+// two 6144-deep slices, but 2048x4096x4096 79 -> 95 us in two of 2048, hence the depth floor.
+constexpr int64_t kWideMinChunk = 6144;
+
+bool split_plan(int64_t m, int64_t n, int64_t k, int* splits, int* kchunk, bool* wide) {
   const int64_t cus = cu_count();
   const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  *wide = false;
+  const int64_t t44 = ((m + 255) / 256) * ((n + 255) / 256), t42 = ((m + 255) / 256) * ((n + 127) / 128);
+  if (tiles * 4 > cus && t44 * 2 <= cus && t42 <= cus) {
+    int64_t s = cus / t44;
+    if (s > k / kWideMinChunk) s = k / kWideMinChunk;
+    if (s < 2 || t44 * s * 4 < cus * 3) return false;   // the slices must still fill 3/4 of the CUs
+    const int64_t kc = ((k + s - 1) / s + 63) / 64 * 64;
+    s = (k + kc - 1) / kc;
+    if (s < 2) return false;
+    *splits = int(s);
+    *kchunk = int(kc);
+    *wide = true;
+    return true;
+  }
   // measured over the bundle's GEMM shapes: below K = 1024 one pass over K (about 7 us) beats
   // partials plus the finish launch; slices under 256 deep cost more in pipeline fill than they save
   if (k < 1024 || tiles * 4 > cus) return false;   // a quarter of the CUs or more: 64x128 tiles instead
@@ -477,29 +498,38 @@ bool split_plan(int64_t m, int64_t n, int64_t k, int* splits, int* kchunk) {
 
 PTB_EXPORT size_t ptb_gemm_bf16_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   int s, kc;
-  if (m <= 0 || n <= 0 || k <= 0 || !split_plan(m, n, k, &s, &kc)) return 0;
+  bool wide;
+  if (m <= 0 || n <= 0 || k <= 0 || !split_plan(m, n, k, &s, &kc, &wide)) return 0;
   return size_t(s) * size_t(m) * size_t(n) * sizeof(float);
 }
 
 PTB_EXPORT int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n,
                                 int64_t k, void* workspace, size_t workspace_bytes, void* stream) {
   int splits, kchunk;
-  if (m <= 0 || n <= 0 || k <= 0 || k % 64 || n % 8 || !split_plan(m, n, k, &splits, &kchunk))
+  bool wide;
+  if (m <= 0 || n <= 0 || k <= 0 || k % 64 || n % 8 || !split_plan(m, n, k, &splits, &kchunk, &wide))
     return ptb_gemm_bf16(a, b, residual, c, m, n, k, stream);   // no split for this shape (or it is refused there)
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
   if (!a || !b || !c || !workspace) return PTB_ERR_NULL;
   if (workspace_bytes < ptb_gemm_bf16_workspace_bytes(m, n, k)) return PTB_ERR_WORKSPACE;
-  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || int64_t(128) * k * 2 >= (int64_t(1) << 32))
+  const int64_t bt = wide ? 256 : 128;   // tile rows and columns
+  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || bt * k * 2 >= (int64_t(1) << 32))
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || !aligned16(workspace) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t tm = (m + 127) / 128, tn = (n + 127) / 128;
+  const int64_t tm = (m + bt - 1) / bt, tn = (n + bt - 1) / bt;
   const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
   float* part = static_cast<float*>(workspace);
-  gemm_bf16_kernel<2, 2, false, kSplit><<<dim3(unsigned(tm * tn), unsigned(splits)), dim3(kThreads), 0, s>>>(
-      static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, nullptr, int(m), int(n), int(k),
-      int(tm), int(tn), none, part, kchunk);
+  const dim3 grid(unsigned(tm * tn), unsigned(splits));
+  if (wide)
+    gemm_bf16_kernel<4, 4, false, kSplit><<<grid, dim3(kThreads), 0, s>>>(
+        static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, nullptr, int(m), int(n), int(k),
+        int(tm), int(tn), none, part, kchunk);
+  else
+    gemm_bf16_kernel<2, 2, false, kSplit><<<grid, dim3(kThreads), 0, s>>>(
+        static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, nullptr, int(m), int(n), int(k),
+        int(tm), int(tn), none, part, kchunk);
   const int64_t mn = m * n;
   splitk_finish<<<dim3(unsigned((mn / 4 + 255) / 256)), dim3(256), 0, s>>>(
       part, splits, mn, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(c));

@@ -44,9 +44,10 @@ def test_layer_full_size_is_its_launch_chain():
     y = layer(x).clone()
     cos, sin = qwen3.rope_tables(t, device=DEV)
     xn = ops.rmsnorm(x, w["w_in"])
-    qh = ops.qk_norm_rope(ops.gemm(xn, w["wq"]).view(t, 32, 128), w["w_qn"], cos, sin)
-    kh = ops.qk_norm_rope(ops.gemm(xn, w["wk"]).view(t, 8, 128), w["w_kn"], cos, sin)
-    vh = ops.transpose_heads(ops.gemm(xn, w["wv"]).view(t, 8, 128))
+    # the q, k, v products single-pass, as the columns of the layer's fused q|k|v GEMM are
+    qh = ops.qk_norm_rope(ops.gemm(xn, w["wq"], split_k=False).view(t, 32, 128), w["w_qn"], cos, sin)
+    kh = ops.qk_norm_rope(ops.gemm(xn, w["wk"], split_k=False).view(t, 8, 128), w["w_kn"], cos, sin)
+    vh = ops.transpose_heads(ops.gemm(xn, w["wv"], split_k=False).view(t, 8, 128))
     o = ops.transpose_heads(ops.flash_attention(qh, kh, vh, 32, 8, True))
     h = ops.gemm(o.view(t, 4096), w["wo"], residual=x)
     a = ops.silu_mul(ops.gemm(ops.rmsnorm(h, w["w_post"]), w["wgu"]))
