@@ -42,6 +42,11 @@ extern "C" {
 #define PTB_DTYPE_F32 1
 #define PTB_DTYPE_I32 2
 #define PTB_DTYPE_I64 3
+#define PTB_DTYPE_E4M3 4
+
+#define PTB_ROLE_IN 0
+#define PTB_ROLE_OUT 1
+#define PTB_ROLE_INOUT 2
 
 #define PTB_REDUCE_SUM 0
 #define PTB_REDUCE_MAX 1
@@ -57,6 +62,14 @@ const char* ptb_status_string(int status);
 int ptb_rmsnorm_bf16(const void* x, const void* w, int w_dtype, void* y, int64_t rows, int64_t cols,
                      float eps, void* stream);
 
+/* fp32 RMSNorm over rows: y = (x * rsqrt(sum_c x^2 / cols + eps)) * w, fp32 in and out (no
+ * rounding below fp32).  x, w, y 16-byte aligned, cols % 4 == 0.
+ * Replaces: tests/cases/workloads/rmsnorm.py:44-54 (the row arm, output o). */
+int ptb_rmsnorm_f32(const float* x, const float* w, float* y, int64_t rows, int64_t cols, float eps, void* stream);
+/* The column arm of the same case: c[j] = rsqrt(sum_i x[i,j]^2 / rows + eps), fp32.
+ * Replaces: tests/cases/workloads/rmsnorm.py:56-57 (output c). */
+int ptb_col_rms_f32(const float* x, float* c, int64_t rows, int64_t cols, float eps, void* stream);
+
 /* Row softmax: y = bf16( exp(x - max) / sum(exp(x - max)) ), max NaN-propagating, fp32 math.
  * Replaces: validation/pytorchsim/vector_softmax_2048x6144_bf16/00_..._sa7wwqqf/..._triton.py:17-68 */
 int ptb_softmax_rows_bf16(const void* x, void* y, int64_t rows, int64_t cols, void* stream);
@@ -66,6 +79,22 @@ int ptb_softmax_rows_bf16(const void* x, void* y, int64_t rows, int64_t cols, vo
  * Replaces: validation/pytorchsim/layer_layer_decode_1x1024_bf16/16_..._qslpdpud/
  *           pytorchsim_triton_compiler_fused__softmax__to_copy_qslpdpud_triton.py:17-45 */
 int ptb_softmax_rows_bf16_f32(const void* x, void* y, int64_t rows, int64_t cols, void* stream);
+
+/* fp32 row softmax: y = exp(x - max) / sum(exp(x - max)), fp32 in and out, max NaN-propagating.
+ * x, y 16-byte aligned, cols % 4 == 0.
+ * Replaces: tests/cases/workloads/softmax.py:46-55 (rtol 1e-5, atol 1e-6 at :84). */
+int ptb_softmax_rows_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
+
+/* fp32 SiLU gate: out[t,j] = (g / (1 + exp(-g))) * u, g = gu[t, j], u = gu[t, inter + j], all fp32.
+ * inter % 4 == 0, pointers 16-byte aligned.  The elementwise half of tests/cases/workloads/swiglu.py
+ * (silu(gate) * up at :61-62); ptb_swiglu_f32 is the whole case. */
+int ptb_silu_mul_f32(const float* gate_up, float* out, int64_t rows, int64_t inter, void* stream);
+
+/* fp32 SwiGLU block: o[m,n] = silu(g) * u with g = (x . wg)[m,n], u = (x . wu)[m,n], x [m,k],
+ * wg / wu [k,n] row-major, fp32 operands and accumulation, silu(g) = g / (1 + exp(-g)).
+ * Replaces: tests/cases/workloads/swiglu.py:44-62 (rtol = atol = 1e-3 at :100). */
+int ptb_swiglu_f32(const float* x, const float* wg, const float* wu, float* o, int64_t m, int64_t n, int64_t k,
+                   void* stream);
 
 /* SiLU gate: out[t,j] = bf16( (g / (1 + exp(-g))) * u ), g = gu[t, j], u = gu[t, inter + j].
  * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/10_..._ktzl5s2h/..._triton.py:17-36 */
@@ -163,6 +192,7 @@ int ptb_quant_weight_e4m3(const float* w, void* wq_t, float* scale, int64_t k, i
  *            tests/cases/workloads/int8_dequant_matmul.py:59-69 (scale epilogue). */
 int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* wq_t, const float* sw, void* c,
                         int64_t m, int64_t n, int64_t k, void* stream);
+
 
 /* Flash-attention forward, head-major layout: q/o [batch*hq, seq, head_dim], k/v [batch*hkv, seq,
  * head_dim]; q head h reads kv head h / (hq / hkv).  Online softmax in fp32 with P rounded to bf16
@@ -356,6 +386,76 @@ int ptb_grouped_gemm_bf16_ws(const void* a, const void* b, const int32_t* group,
                              const int32_t* rows, void* c, int64_t nprog, int64_t ntab, int64_t a_rows,
                              int64_t nweights, int64_t k, int64_t n, int64_t weight_stride, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/* ---- spec-driven entry points: one per kernel family ----
+ * The reference's generated driver calls a lowered kernel as
+ *   <kernel>(1, &desc_0, ..., 1, &desc_n, scalars..., gx, gy, gz, pidx, pidy, pidz)
+ * once per program, desc_i being a memref descriptor {allocated, aligned, offset, size, stride} per
+ * tensor in spec order (reference: pytorchsim_triton_compiler/codegen/wrapper.py:37-51 declaration,
+ * :140-146 descriptor, :126-277 main, program loop :254-265).  Each ptb_<family>_args entry takes
+ * the same in one call: `args` the tensors in spec order as ptb_tensor descriptors, `ints` / `floats`
+ * the family's integer and floating-point parameters in the order listed per entry (the kernel's
+ * runtime scalars and the constexprs its compile baked in), and `grid` the launch grid.
+ * Sizes come from the descriptors and must agree with the parameters (PTB_ERR_SHAPE otherwise, as
+ * a wrong count `nargs` / `nints` / `nfloats`).  Every family runs its programs along x.  Where the
+ * last int is `programs`, it is the program bound the kernel was compiled for (kernel.json's
+ * grid_bound, else the spec's grid), the programs splitting the rows (or outputs) evenly; the other
+ * families' bound follows from their shape.  A grid with gy or gz != 1, gx < 1 or gx past the bound
+ * is refused with PTB_ERR_GRID (contract/kernel_object.py:93-107 refuse_grid_past_bound).  A grid
+ * below the bound runs the programs it covers where they are blocks of whole rows (rmsnorm,
+ * softmax, silu_mul, and flash_attn over whole batches); elsewhere it is PTB_ERR_UNSUPPORTED.  A
+ * tensor must be flat (stride 1 when size > 1), and a written tensor must not have role
+ * PTB_ROLE_IN. */
+typedef struct ptb_tensor {
+  void* allocated;  /* allocation base (not read) */
+  void* aligned;    /* element 0 sits at aligned + offset * itemsize */
+  int64_t offset;   /* in elements */
+  int64_t size;     /* elements */
+  int64_t stride;   /* 1 */
+  int32_t dtype;    /* PTB_DTYPE_* */
+  int32_t role;     /* PTB_ROLE_* */
+} ptb_tensor;
+
+/* args [x, w, y] (L2048/00's in_ptr0, in_ptr1, out_ptr1), x/y bf16 with w bf16 or fp32, or all
+ * fp32; ints [rows (xnumel), cols (r0_numel), programs]; floats [eps].
+ * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/00_..._gwdq6qer_triton.py:17-60 and
+ *           tests/cases/workloads/rmsnorm.py:44-54 */
+int ptb_rmsnorm_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                     int nfloats, const int32_t grid[3], void* stream);
+/* args [x, y]: bf16 -> bf16, bf16 -> fp32 or fp32 -> fp32; ints [rows, cols, programs].
+ * Replaces: vector_softmax_<R>x<C>_bf16/00_..._triton.py:17-68, layer_layer_decode_1x1024_bf16/16
+ *           (fp32 out), tests/cases/workloads/softmax.py:46-55 */
+int ptb_softmax_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                     int nfloats, const int32_t grid[3], void* stream);
+/* args [gate_up, out] (bf16 or fp32); ints [rows, inter, programs].
+ * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/10_..._ktzl5s2h_triton.py:17-36 */
+int ptb_silu_mul_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                      int nfloats, const int32_t grid[3], void* stream);
+/* args [A, B, C] or, with the residual epilogue, [R, A, B, C] (bf16); ints [M, N, K, programs]
+ * (only the whole grid runs: a partial grid's tiles follow the caller's template order).
+ * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/01_..._ckb6aiys_triton.py:18-97 (and 03, 09),
+ *           08_..._utuycvlm_triton.py:18-99, 11_..._fjjozd2g_triton.py:18-66, gemm_<M>x<K>x<N>_bf16 */
+int ptb_gemm_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                  int nfloats, const int32_t grid[3], void* stream);
+/* args [q, k, v, o] head-major bf16; ints [batch, HQ, HKV (HQ / G), S, D, CAUSAL]; floats [SCALE];
+ * one program per (batch, query head).
+ * Replaces: attention_prefill_<HQ>x<HKV>x<S>_bf16/00__prefill_kernel/_prefill_kernel_triton.py:4-44 */
+int ptb_flash_attn_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                        int nfloats, const int32_t grid[3], void* stream);
+/* args [q, k, v, o] (+ a workspace descriptor of ptb_attn_decode_workspace_bytes bytes when
+ * S > 256); ints [HKV, G, S, D]; floats [SCALE]; one program per kv head (only the whole grid).
+ * Replaces: attention_decode_<HQ>x8x<S>_bf16/00__decode_kernel/_decode_kernel_triton.py:4-29 */
+int ptb_attn_decode_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                         int nfloats, const int32_t grid[3], void* stream);
+/* args [x, w, cos, sin, out] (L2048/02's in_ptr0..3, out_ptr2); ints [tokens, heads, head_dim,
+ * programs]; floats [eps]; only the whole grid.
+ * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/02_..._mmis7ufj_triton.py:17-98 (and 04) */
+int ptb_qk_norm_rope_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                          int nfloats, const int32_t grid[3], void* stream);
+/* args [x, y]; ints [d0, d1, inner, programs]: y[b, a, :] = x[a, b, :]; only the whole grid.
+ * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/05_..._ff5nvvqz_triton.py:17-27 and 07_..._ei42assc */
+int ptb_transpose_heads_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints,
+                             const double* floats, int nfloats, const int32_t grid[3], void* stream);
 
 #ifdef __cplusplus
 }

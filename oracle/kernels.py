@@ -23,6 +23,7 @@ __all__ = [
     "add_scalar", "gemm", "quant_rows_e4m3", "quant_weight_e4m3", "gemm_fp8", "flash_attention",
     "rope_tables", "qwen3_layer", "E4M3_MAX",
     "slice_add", "sumsq", "gemv", "gemv_rmsnorm", "gemv_silu", "attention_decode", "qwen3_decode_layer",
+    "rmsnorm_f32", "col_rms_f32", "silu_mul_f32", "swiglu_f32",
 ]
 
 E4M3_MAX = 448.0
@@ -36,6 +37,38 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor
     s = (xf * xf).sum(dim=-1, keepdim=True)
     r = torch.rsqrt(s / float(x.shape[-1]) + eps)
     return ((xf * r) * w.float()).to(BF16)
+
+
+def rmsnorm_f32(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """tests/cases/workloads/rmsnorm.py:44-54, the row arm of the fp32 case: ms = sum(x*x) / N (:51),
+    y = x * rsqrt(ms + EPS) (:52), o = y * w (:54); everything fp32, nothing rounded below it."""
+    xf = x.float()
+    ms = (xf * xf).sum(dim=-1, keepdim=True) / float(x.shape[-1])
+    return (xf * torch.rsqrt(ms + eps)) * w.float()
+
+
+def col_rms_f32(x: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """tests/cases/workloads/rmsnorm.py:56-57, the column arm: rsqrt(sum_i x[i,j]^2 / rows + EPS)."""
+    xf = x.float()
+    return torch.rsqrt((xf * xf).sum(dim=0) / float(x.shape[0]) + eps)
+
+
+def silu_mul_f32(gu: torch.Tensor) -> torch.Tensor:
+    """The elementwise half of tests/cases/workloads/swiglu.py (:61-62): gate / (1 + exp(-gate)) * up
+    in fp32, gate | up side by side as in the bf16 kernel's [T, 2I] layout."""
+    inter = gu.shape[-1] // 2
+    g = gu[..., :inter].float()
+    u = gu[..., inter:].float()
+    return (g / (1.0 + torch.exp(-g))) * u
+
+
+def swiglu_f32(x: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor) -> torch.Tensor:
+    """tests/cases/workloads/swiglu.py:44-62: gate = x @ wg and up = x @ wu with fp32 accumulation
+    (:52-58; the products are summed in fp64 and rounded once to fp32, the exact value every fp32
+    order approximates), then gate / (1 + exp(-gate)) * up in fp32 (:61-62)."""
+    g = (x.double() @ wg.double()).float()
+    u = (x.double() @ wu.double()).float()
+    return (g / (1.0 + torch.exp(-g))) * u
 
 
 def softmax_rows(x: torch.Tensor, out_dtype=BF16) -> torch.Tensor:

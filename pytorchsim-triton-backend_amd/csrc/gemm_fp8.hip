@@ -6,39 +6,43 @@
 //   gemm_fp8     : C[m,n] = bf16( (sum_k Aq[m,k] * Wt[n,k]) * sa[m] * sw[n] ), fp32 accumulation
 //
 // The GEMM uses v_mfma_f32_32x32x64_f8f6f4 (both operands e4m3, no block scales): a 256xBN
-// workgroup tile (BN = 256, or 128 when 256x256 tiles would leave CUs idle), K step 64, 4 waves in
-// a 2x2 arrangement, each wave 128 x BN/2 as 32x32 accumulators.  Both operands are K-contiguous
-// rows of 64 bytes per K step; they move HBM -> LDS with buffer_load_dwordx4 ... lds into a ring of
-// four stages, three K steps ahead of the matrix cores.  Within a row the four 16-byte chunks are
-// XOR-swizzled by (row >> 2) & 3, so the two 128-bit fragment reads per lane are bank-conflict
-// free.  Each K step issues half of its MFMAs, passes the barrier that publishes the next stage,
-// then issues the other half with the next stage's DMA and fragment reads folded in between them.
-// MFMAs take W as the first operand, so accumulators hold C^T blocks and each lane stores 4
-// consecutive columns of a row of C at once.
+// workgroup tile (BN = 256, or 128 when 256x256 tiles would leave CUs idle), 4 waves in a 2x2
+// arrangement, each wave 128 x BN/2 as 32x32 accumulators.  Both operands are K-contiguous; a stage
+// holds 128 bytes (= 128 K) of every tile row, so each row's DMA is one whole 128-byte line and the
+// L2 serves one request per line (a 64-byte stage row costs the L2 a request slot for half a line:
+// the request rate, not the bytes, bounded the 64-byte form).  Operands move HBM -> LDS with
+// buffer_load_dwordx4 ... lds into a ring of NS stages (3 x 48 KB at BN = 128, 2 x 64 KB at
+// BN = 256).  Within a row the eight 16-byte chunks sit XOR-swizzled by (row >> 1) & 7, so the
+// 128-bit fragment reads (16 lanes a phase, 16 different rows) are bank-conflict free.  A stage is
+// two MFMA K substeps of 64: substep 0's MFMAs run with substep 1's fragment reads folded in; the
+// barrier that follows publishes the next stage and frees this one; substep 1's MFMAs then run with
+// the DMA that refills this stage's slot (NS stages ahead) and the reads of the next stage's
+// substep 0.  MFMAs take W as the first operand, so accumulators hold C^T blocks and each lane
+// stores 4 consecutive columns of a row of C at once.
 #include "ptb_common.h"
 
 using namespace ptb;
 
 namespace {
 
-constexpr int BM = 256, BK = 64;   // BK in bytes (= fp8 elements)
+constexpr int BM = 256, BK = 128;   // BK in bytes (= fp8 elements) per stage
 constexpr int kThreads = 256;
-constexpr int kStages = 4;
 constexpr int kGroupM = 8;
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 template <int BN>
 struct Cfg {
+  static constexpr int NS = BN == 256 ? 2 : 3;         // LDS ring depth
   static constexpr int WNT = BN / 64;                  // 32-wide column tiles per wave
-  static constexpr int kABytes = BM * BK;              // 16 KB
+  static constexpr int kABytes = BM * BK;              // 32 KB
   static constexpr int kWBytes = BN * BK;
   static constexpr int kStageBytes = kABytes + kWBytes;
-  static constexpr int kDmaA = BM / 16 / 4;            // per wave per stage
-  static constexpr int kDmaW = BN / 16 / 4;
+  static constexpr int kDmaA = BM / 8 / 4;             // DMA instructions per wave per stage (8 rows each)
+  static constexpr int kDmaW = BN / 8 / 4;
   static constexpr int kDma = kDmaA + kDmaW;
-  static constexpr int kPieces = 2 * (4 + WNT);        // 128-bit fragment reads per stage
-  static constexpr int kMfma = 4 * WNT;
+  static constexpr int kPieces = 2 * (4 + WNT);        // 128-bit fragment reads per wave per substep
+  static constexpr int kMfma = 4 * WNT;                // MFMAs per wave per substep
 };
 
 template <int BN>
@@ -48,12 +52,15 @@ struct Frags {
   u32x4 lo[4 + Cfg<BN>::WNT];
 };
 
+__device__ __forceinline__ int fp8_swz(int row) { return (row >> 1) & 7; }
+
 template <int BN>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_fp8_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ W,
     const float* __restrict__ SW, uint16_t* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
   using G = Cfg<BN>;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * G::kStageBytes];
+  constexpr int NS = G::NS;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * G::kStageBytes];
 
   const int ntiles = tiles_m * tiles_n;
   int pid = blockIdx.x;
@@ -69,21 +76,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // loaders: rows past M (A) or N (W) read as zero through num_records; stages past K read
-  // zeros too (the DMA stream runs ahead without a branch)
+  // loaders: rows past M (A) or N (W) read as zero through num_records; stages past K read other
+  // rows' bytes or zeros into slots nobody reads any more (the DMA stream runs ahead without a branch)
   const i32x4 rsrc_a = make_rsrc(A + int64_t(m0) * K, uint32_t(min(BM, M - m0)) * uint32_t(K));
   const i32x4 rsrc_w = make_rsrc(W + int64_t(n0) * K, uint32_t(min(BN, N - n0)) * uint32_t(K));
-  // DMA instruction d of this wave covers rows 16*(kDma_op*wave + d) .. +16; lane -> row lane/4,
-  // slot lane%4 holding chunk (lane%4) ^ ((row >> 2) & 3)
-  auto voff_of = [&](int row) { return uint32_t(row * K + (((lane & 3) ^ ((row >> 2) & 3)) << 4)); };
+  // DMA instruction d of this wave covers rows 8*(kDma_op*wave + d) .. +8; lane -> row lane/8,
+  // slot lane%8 holding chunk (lane%8) ^ swz(row)
+  auto voff_of = [&](int row) { return uint32_t(row * K + (((lane & 7) ^ fp8_swz(row)) << 4)); };
   uint32_t a_voff[G::kDmaA], w_voff[G::kDmaW];
 #pragma unroll
-  for (int t = 0; t < G::kDmaA; ++t) a_voff[t] = voff_of((wave * G::kDmaA + t) * 16 + (lane >> 2));
+  for (int t = 0; t < G::kDmaA; ++t) a_voff[t] = voff_of((wave * G::kDmaA + t) * 8 + (lane >> 3));
 #pragma unroll
-  for (int t = 0; t < G::kDmaW; ++t) w_voff[t] = voff_of((wave * G::kDmaW + t) * 16 + (lane >> 2));
+  for (int t = 0; t < G::kDmaW; ++t) w_voff[t] = voff_of((wave * G::kDmaW + t) * 8 + (lane >> 3));
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
-  auto dma_one = [&](int kt, int d) {
-    const uint32_t st = lds0 + uint32_t(kt % kStages) * G::kStageBytes;
+  auto dma_one = [&](int kt, int d) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + uint32_t(kt % NS) * G::kStageBytes;
     const uint32_t soff = uint32_t(kt * BK);
     if (d < G::kDmaA)
       dma16(rsrc_a, __builtin_amdgcn_readfirstlane(st + (wave * G::kDmaA + d) * 1024), a_voff[d], soff);
@@ -100,25 +107,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // lane -> row (or column) lane % 32, K half (32 bytes = chunks 2h, 2h+1) lane / 32
+  // lane -> row (or column) lane % 32, K half (32 bytes = chunks 4ks + 2h, 4ks + 2h + 1) lane / 32
   const int fr = lane & 31, h = lane >> 5;
   int row_off[4 + G::WNT], row_sw[4 + G::WNT];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = wm * 128 + i * 32 + fr;
     row_off[i] = m * BK;
-    row_sw[i] = (m >> 2) & 3;
+    row_sw[i] = fp8_swz(m);
   }
 #pragma unroll
   for (int j = 0; j < G::WNT; ++j) {
     const int n = wn * (BN / 2) + j * 32 + fr;
     row_off[4 + j] = G::kABytes + n * BK;
-    row_sw[4 + j] = (n >> 2) & 3;
+    row_sw[4 + j] = fp8_swz(n);
   }
-  // piece p: operand row t = p / 2, half c = p % 2 (chunk 2h + c)
-  auto read_piece = [&](const uint8_t* st, int p, Frags<BN>& f) {
+  // piece p of substep ks: operand row t = p / 2, half c = p % 2 (chunk 4ks + 2h + c)
+  auto read_piece = [&](const uint8_t* st, int ks, int p, Frags<BN>& f) __attribute__((always_inline)) {
     const int t = p >> 1, c = p & 1;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(st + row_off[t] + (((2 * h + c) ^ row_sw[t]) << 4));
+    const u32x4 v = *reinterpret_cast<const u32x4*>(st + row_off[t] + (((4 * ks + 2 * h + c) ^ row_sw[t]) << 4));
     if (c == 0) {
       f.lo[t] = v;
     } else {
@@ -128,68 +135,83 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       else f.w[t - 4] = x;
     }
   };
-  auto mfma_one = [&](const Frags<BN>& f, int u) {
+  auto mfma_one = [&](const Frags<BN>& f, int u) __attribute__((always_inline)) {
     const int i = u / G::WNT, j = u % G::WNT;
     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[j], f.a[i], acc[i][j], 0, 0, 0, 0, 0, 0);
   };
 
   const int nk = K / BK;
 #pragma unroll
-  for (int s = 0; s < kStages - 1; ++s)
+  for (int s = 0; s < NS; ++s)
 #pragma unroll
     for (int d = 0; d < G::kDma; ++d) dma_one(s, d);
-  wait_vmcnt<(kStages - 2) * G::kDma>();
-  __syncthreads();
-  Frags<BN> cur, nxt;
+  wait_vmcnt<(NS - 1) * G::kDma>();   // stage 0 landed (this wave's part)
+  __syncthreads();                    // ... and everyone's
+  Frags<BN> f0, f1;
 #pragma unroll
-  for (int p = 0; p < G::kPieces; ++p) read_piece(smem, p, cur);
+  for (int p = 0; p < G::kPieces; ++p) read_piece(smem, 0, p, f0);
 
-  constexpr int kHalf = G::kMfma / 2;
+  // Reads are issued in the order the MFMAs first use the operands (MFMA u multiplies A row block
+  // u / WNT by W column block u % WNT): A0, W0 .. W(WNT-1), A1, A2, A3, two 128-bit pieces each,
+  // two pieces per MFMA from the start of a substep, so the next substep's first MFMAs find their
+  // operands landed instead of waiting on the LDS.  The refill DMAs spread over the whole substep.
+  constexpr int U = G::kMfma, P = G::kPieces, D = G::kDma;
+  auto piece_of = [](int q) constexpr {
+    const int o = q >> 1;   // operand in first-use order
+    const int t = o == 0 ? 0 : (o <= G::WNT ? 4 + (o - 1) : o - G::WNT);
+    return 2 * t + (q & 1);
+  };
   for (int kt = 0; kt < nk; ++kt) {
+    const uint8_t* st = smem + (kt % NS) * G::kStageBytes;
+    // substep 0, with the reads of substep 1 of this stage
 #pragma unroll
-    for (int u = 0; u < kHalf; ++u) mfma_one(cur, u);
-    __builtin_amdgcn_sched_barrier(0);
-    // stage kt+1 landed; past this barrier stage kt-1's slot is free for stage kt+3
-    wait_vmcnt<(kStages - 3) * G::kDma>();
-    __syncthreads();
-    const uint8_t* nst = smem + ((kt + 1) % kStages) * G::kStageBytes;
-    // the second half of the MFMAs, with the DMA of stage kt+3 and the reads of stage kt+1 between
-    constexpr int kSlots = (G::kDma + G::kPieces + kHalf - 1) / kHalf;
+    for (int u = 0; u < U; ++u) {
+      mfma_one(f0, u);
 #pragma unroll
-    for (int u = 0; u < kHalf; ++u) {
-      mfma_one(cur, kHalf + u);
-#pragma unroll
-      for (int q = 0; q < kSlots; ++q) {
-        const int e = u * kSlots + q;
-        if (e < G::kDma) dma_one(kt + kStages - 1, e);
-        else if (e < G::kDma + G::kPieces) read_piece(nst, e - G::kDma, nxt);
-      }
+      for (int q = 2 * u; q < 2 * u + 2; ++q)
+        if (q < P) read_piece(st, 1, piece_of(q), f1);
       __builtin_amdgcn_sched_barrier(0);
     }
-    cur = nxt;
+    // stage kt+1 landed (stages up to kt+NS-1 may still be in flight); past the barrier every wave
+    // is done reading stage kt, whose slot takes stage kt+NS
+    wait_vmcnt<(NS - 2) * G::kDma>();
+    __syncthreads();
+    const uint8_t* nst = smem + ((kt + 1) % NS) * G::kStageBytes;
+    // substep 1, with the reads of the next stage's substep 0 and the refill DMA
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      mfma_one(f1, u);
+#pragma unroll
+      for (int q = 2 * u; q < 2 * u + 2; ++q)
+        if (q < P) read_piece(nst, 0, piece_of(q), f0);
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+        if (d * U / D == u) dma_one(kt + NS, d);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   wait_vmcnt<0>();
 
   // accumulator (i, j, r) of lane -> C row m0 + wm*128 + i*32 + lane%32, columns
-  // n0 + wn*BN/2 + j*32 + 8*(r/4) + 4*(lane/32) + r%4
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  // n0 + wn*BN/2 + j*32 + 8*(r/4) + 4*(lane/32) + r%4; the scaled epilogue of one 4-column group
+  auto store4 = [&](int i, int j, int g, const f32x4v& v) __attribute__((always_inline)) {
     const int row = m0 + wm * 128 + i * 32 + fr;
-    if (row >= M) continue;
+    const int col = n0 + wn * (BN / 2) + j * 32 + 8 * g + 4 * h;
+    if (row >= M || col >= N) return;   // N % 16 == 0: a 4-column group is all in or all out
     const float sa = SA[row];
+    const f32x4v sw = *reinterpret_cast<const f32x4v*>(SW + col);
+    const float v0 = (v.x * sa) * sw[0], v1 = (v.y * sa) * sw[1];
+    const float v2 = (v.z * sa) * sw[2], v3 = (v.w * sa) * sw[3];
+    *reinterpret_cast<u32x2*>(C + int64_t(row) * N + col) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+  };
+
 #pragma unroll
-    for (int j = 0; j < G::WNT; ++j) {
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int col = n0 + wn * (BN / 2) + j * 32 + 8 * g + 4 * h;
-        if (col >= N) continue;  // N % 16 == 0: a 4-column group is all in or all out
-        const f32x4v sw = *reinterpret_cast<const f32x4v*>(SW + col);
-        const float v0 = (acc[i][j][4 * g] * sa) * sw[0], v1 = (acc[i][j][4 * g + 1] * sa) * sw[1];
-        const float v2 = (acc[i][j][4 * g + 2] * sa) * sw[2], v3 = (acc[i][j][4 * g + 3] * sa) * sw[3];
-        *reinterpret_cast<u32x2*>(C + int64_t(row) * N + col) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
-      }
-    }
-  }
+    for (int j = 0; j < G::WNT; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        store4(i, j, g, f32x4v{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]});
 }
 
 // ---- per-row activation quantiser: one wave per row for rows up to 64*8*VPT elements
@@ -350,8 +372,16 @@ PTB_EXPORT int ptb_quant_weight_e4m3(const float* w, void* wq_t, float* scale, i
   return launch_status();
 }
 
-PTB_EXPORT int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* wq_t, const float* sw, void* c,
-                                   int64_t m, int64_t n, int64_t k, void* stream) {
+namespace {
+
+int device_cus() {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  return cus;
+}
+
+int fp8_check(const void* aq, const float* sa, const void* wq_t, const float* sw, void* c, int64_t m, int64_t n,
+              int64_t k) {
   if (m < 0 || n < 0 || k < 0) return PTB_ERR_SHAPE;
   if (m == 0 || n == 0) return PTB_OK;
   if (!aq || !sa || !wq_t || !sw || !c) return PTB_ERR_NULL;
@@ -361,21 +391,27 @@ PTB_EXPORT int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* 
   if (int64_t(BM) * k >= (int64_t(1) << 32)) return PTB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   if (!aligned16(aq) || !aligned16(wq_t) || !aligned16(sw) || (reinterpret_cast<uintptr_t>(c) & 7u))
     return PTB_ERR_ALIGN;
+  return 1;   // go on
+}
+
+}  // namespace
+
+PTB_EXPORT int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* wq_t, const float* sw, void* c,
+                                   int64_t m, int64_t n, int64_t k, void* stream) {
+  const int st = fp8_check(aq, sa, wq_t, sw, c, m, n, k);
+  if (st <= 0) return st;
   // 256x256 tiles unless that leaves CUs idle, then 256x128
   const int64_t tm = (m + BM - 1) / BM;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  const bool wide = tm * ((n + 255) / 256) >= cus;
+  const bool wide = tm * ((n + 255) / 256) >= device_cus();
   const int bn = wide ? 256 : 128;
   const int64_t tn = (n + bn - 1) / bn;
   if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
   const dim3 grid(unsigned(tm * tn)), block(kThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (wide)
-    gemm_fp8_kernel<256><<<grid, block, 0, s>>>(static_cast<const uint8_t*>(aq), sa, static_cast<const uint8_t*>(wq_t),
-                                                 sw, static_cast<uint16_t*>(c), int(m), int(n), int(k), int(tm), int(tn));
-  else
-    gemm_fp8_kernel<128><<<grid, block, 0, s>>>(static_cast<const uint8_t*>(aq), sa, static_cast<const uint8_t*>(wq_t),
-                                                 sw, static_cast<uint16_t*>(c), int(m), int(n), int(k), int(tm), int(tn));
+  const uint8_t* a8 = static_cast<const uint8_t*>(aq);
+  const uint8_t* w8 = static_cast<const uint8_t*>(wq_t);
+  uint16_t* c16 = static_cast<uint16_t*>(c);
+  if (wide) gemm_fp8_kernel<256><<<grid, block, 0, s>>>(a8, sa, w8, sw, c16, int(m), int(n), int(k), int(tm), int(tn));
+  else gemm_fp8_kernel<128><<<grid, block, 0, s>>>(a8, sa, w8, sw, c16, int(m), int(n), int(k), int(tm), int(tn));
   return launch_status();
 }

@@ -25,6 +25,10 @@ PTB_DTYPE_BF16 = 0
 PTB_DTYPE_F32 = 1
 PTB_DTYPE_I32 = 2
 PTB_DTYPE_I64 = 3
+PTB_DTYPE_E4M3 = 4
+PTB_ROLE_IN = 0
+PTB_ROLE_OUT = 1
+PTB_ROLE_INOUT = 2
 PTB_REDUCE_SUM = 0
 PTB_REDUCE_MAX = 1
 
@@ -71,6 +75,20 @@ _ERR_CLASS = {
 
 _c_int, _c_i64, _c_f32, _vp, _c_size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
 
+
+class PtbTensor(ctypes.Structure):
+    """ptb_tensor: the reference's memref descriptor (codegen/wrapper.py:140-146) plus dtype and role."""
+    _fields_ = [("allocated", ctypes.c_void_p), ("aligned", ctypes.c_void_p), ("offset", ctypes.c_int64),
+                ("size", ctypes.c_int64), ("stride", ctypes.c_int64), ("dtype", ctypes.c_int32),
+                ("role", ctypes.c_int32)]
+
+
+_ARGS_SIG = (ctypes.c_int, [ctypes.POINTER(PtbTensor), ctypes.c_int, ctypes.POINTER(ctypes.c_int64), ctypes.c_int,
+                            ctypes.POINTER(ctypes.c_double), ctypes.c_int, ctypes.POINTER(ctypes.c_int32),
+                            ctypes.c_void_p])
+ARGS_FAMILIES = ("rmsnorm", "softmax", "silu_mul", "gemm", "flash_attn", "attn_decode", "qk_norm_rope",
+                 "transpose_heads")
+
 # name -> (restype, argtypes), mirroring include/ptb_amd.h
 SIGNATURES = {
     "ptb_abi_version": (_c_int, []),
@@ -95,6 +113,11 @@ SIGNATURES = {
     "ptb_quant_rows_e4m3": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp]),
     "ptb_quant_weight_e4m3": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp]),
     "ptb_gemm_fp8_scaled": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
+    "ptb_rmsnorm_f32": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_f32, _vp]),
+    "ptb_col_rms_f32": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_f32, _vp]),
+    "ptb_softmax_rows_f32": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
+    "ptb_silu_mul_f32": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
+    "ptb_swiglu_f32": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "ptb_flash_attn_fwd_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32,
                                          _c_int, _vp]),
     "ptb_flash_attn_fwd_tokens_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32,
@@ -133,6 +156,7 @@ SIGNATURES = {
     "ptb_attn_decode_qnorm_rope_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_f32, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64,
                                                  _c_i64, _c_f32, _vp, _c_size, _vp]),
 }
+SIGNATURES.update({f"ptb_{fam}_args": _ARGS_SIG for fam in ARGS_FAMILIES})
 
 _lock = threading.Lock()
 _lib = None

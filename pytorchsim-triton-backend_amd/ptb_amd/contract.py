@@ -132,9 +132,11 @@ def spec_from_manifest(manifest: dict) -> KernelSpec:
     extra = dict(manifest.get("extra", {}))
     extra.update({"scalar_args": [(s["name"], s.get("ctype", "int32_t")) for s in scalars],
                   "scalar_values": {s["name"]: s.get("default") for s in scalars if s.get("default") is not None}})
+    gp = manifest.get("graph_prefetch")
     return KernelSpec(name=manifest["name"], signature=manifest.get("signature", {}),
                       constexprs=dict(manifest.get("constexprs", {})), args=args,
-                      grid=tuple(manifest.get("grid", (1,))), extra=extra)
+                      grid=tuple(manifest.get("grid", (1,))), extra=extra,
+                      graph_prefetch=None if gp is None else tuple(gp))
 
 
 def seeded_inputs(spec: KernelSpec, torch, seed: int = 0, recorded: dict | None = None) -> dict:
@@ -158,3 +160,69 @@ def seeded_inputs(spec: KernelSpec, torch, seed: int = 0, recorded: dict | None 
         dt = getattr(torch, a.dtype)
         out[a.name] = torch.randn(a.numel, generator=g).to(dt)
     return out
+
+
+class ObjectError(RuntimeError):
+    """A kernel object the launch cannot take (contract/kernel_object.py:75-76's ObjectError)."""
+
+
+PROGRAM_ID_LIMIT = 1 << 21
+"""Programs per grid axis a kernel object can name (contract/kernel_object.py:32, :125-128: program ids
+are packed 21 bits an axis)."""
+
+
+def grid3(grid) -> tuple:
+    """A grid padded to three axes (contract/kernel_object.py:84-87)."""
+    g = [int(v) for v in grid] + [1, 1, 1]
+    return g[0], g[1], g[2]
+
+
+def grid_bound(manifest_or_spec) -> tuple:
+    """The per-axis program bound a launch may not pass: kernel.json's ``grid_bound`` where the
+    manifest states one (None on an axis: unbounded there), else the spec's grid, which bounds the
+    compiled programs (driver/stage.py:95)."""
+    if isinstance(manifest_or_spec, KernelSpec):
+        return grid3(manifest_or_spec.grid)
+    bound = manifest_or_spec.get("grid_bound")
+    if bound is None:
+        return grid3(manifest_or_spec.get("grid", (1,)))
+    b = list(bound) + [1, 1, 1]
+    return tuple(None if v is None else int(v) for v in b[:3])
+
+
+def refuse_grid_past_bound(name: str, grid, bound) -> tuple:
+    """contract/kernel_object.py:93-107: refuse a launch grid with an axis past its bound, an axis below
+    one, or a program id past PROGRAM_ID_LIMIT; returns the grid padded to three axes."""
+    got = grid3(grid)
+    over = [f"{a}={g} (bound {b})" for a, g, b in zip("xyz", got, bound) if b is not None and g > b]
+    low = [f"{a}={g}" for a, g in zip("xyz", got) if g < 1]
+    if over or low or any(g > PROGRAM_ID_LIMIT for g in got):
+        raise ObjectError(f"{name}: launch grid {got} is refused; it was compiled for grids within {tuple(bound)}: "
+                          f"{', '.join(over + [x + ' is below 1' for x in low]) or 'a program id past the key'}")
+    return got
+
+
+def disagreements(manifest: dict, spec: KernelSpec) -> list:
+    """Every question a manifest and a spec both answer, asked of both (contract/kernel_object.py:264-278):
+    argument order, scalar names, grid, sizes, written arguments, graph prefetch."""
+    scalars = [s["name"] for s in manifest.get("scalars", [])]
+    spec_scalars = [n for n, _ in (spec.extra or {}).get("scalar_args", [])]
+    checks = (
+        ("argv_order", [a["name"] for a in manifest["args"]], [a.name for a in spec.args]),
+        ("scalars", scalars, spec_scalars),
+        ("grid3", list(grid3(manifest["grid"])), list(grid3(spec.grid))),
+        ("numel", [math.prod(a["shape"]) for a in manifest["args"]], [a.numel for a in spec.args]),
+        ("writable", [a["name"] for a in manifest["args"] if a["role"] in (OUT, INOUT)],
+         [a.name for a in spec.outputs()]),
+        ("graph_prefetch", [manifest.get("graph_prefetch")],
+         [None if spec.graph_prefetch is None else list(spec.graph_prefetch)]),
+    )
+    return [what for what, mine, theirs in checks if list(mine) != list(theirs)]
+
+
+def refuse_if_it_disagrees(manifest: dict, spec: KernelSpec) -> None:
+    """Refuse a manifest that answers differently from `spec` (contract/kernel_object.py:281-286)."""
+    bad = disagreements(manifest, spec)
+    if bad:
+        raise ObjectError(f"{spec.name}: the manifest and the spec disagree about {', '.join(bad)}; "
+                          "the manifest was written by a different compile")

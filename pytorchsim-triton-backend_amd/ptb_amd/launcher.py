@@ -1,29 +1,36 @@
 """The launch hooks the reference's callers use, served by the HIP kernels.
 
-* ``launch(spec_or_manifest, tensors, grid=None, source=None)`` -- run one kernel over device
-  tensors keyed by argument name (or given in argument order).
+* ``launch(spec_or_manifest, tensors, grid=None, source=None, scalars=None, manifest=None)`` -- run
+  one kernel over device tensors keyed by argument name (or given in argument order).
 * ``hip_launcher(binary, kernel_object, grid, args, artifacts=None)`` -- a callable with the
   signature PyTorchSim registers through ``pytorchsim_triton_backend.driver.set_launcher``
   (reference: pytorchsim_triton_compiler/triton_extension/python/pytorchsim_triton_backend/
   driver.py:86-100): ``binary`` (the compiled ELF) is not needed here; ``kernel_object`` is the
-  kernel.json text or dict; ``args`` are the call's arguments with constexprs dropped, tensors
-  first in argument order, then the runtime scalars.
+  kernel.json text or dict; ``args`` are the call's arguments with the constexprs dropped, in
+  signature order (driver.py:39-44): tensors and runtime scalars interleaved.
 * ``set_launcher`` / ``registered_launcher`` mirror the reference's registry (driver.py:86-100):
   with nothing registered, a launch raises ``RuntimeError`` as the reference's driver does.
 
-The whole grid is one HIP launch: the reference's per-program loop (codegen/wrapper.py:254-265)
-has no counterpart, so ``grid`` only has to name the grid the kernel was built for.
+Launch semantics follow the reference's kernel objects: a grid past the compiled bound (kernel.json's
+``grid_bound``, else the spec's grid) is refused (contract/kernel_object.py:93-107); a grid within it
+runs the programs it names -- the whole kernel at the spec's grid, a prefix of row blocks below it
+where the family's programs are row blocks -- through the family's spec-driven C entry
+(``ptb_<family>_args``); runtime scalars are taken by name (contract/kernel_object.py:122-127) and a
+manifest that disagrees with the spec it is launched beside is refused (:264-286).  The whole grid
+is one HIP launch: the reference's per-program loop (codegen/wrapper.py:254-265) has no
+counterpart.
 """
 from __future__ import annotations
 
 import json
 
-from . import kernels
-from .contract import KernelSpec, spec_from_manifest
+from . import capi, kernels
+from .contract import KernelSpec, ObjectError, grid3, grid_bound, refuse_grid_past_bound, refuse_if_it_disagrees
+from .contract import spec_from_manifest
 
 
-class GridMismatch(ValueError):
-    pass
+class GridMismatch(ObjectError, ValueError):
+    """A launch grid the compiled kernel does not take."""
 
 
 def _as_spec(obj) -> KernelSpec:
@@ -52,27 +59,81 @@ def _check_tensors(spec: KernelSpec, tensors: dict) -> None:
             raise ValueError(f"{spec.name}: argument {a.name} must be contiguous")
 
 
-def launch(spec_or_manifest, tensors, grid=None, source: str | None = None) -> kernels.Plan:
-    """Run one reference kernel on the GPU (asynchronously, on the current stream)."""
+def _with_scalars(spec: KernelSpec, scalars: dict | None) -> KernelSpec:
+    """The spec with a launch's runtime scalar values in place of its defaults, by name."""
+    if not scalars:
+        return spec
+    known = [n for n, _ in (spec.extra or {}).get("scalar_args", [])]
+    unknown = sorted(set(scalars) - set(known))
+    if unknown:
+        raise ObjectError(f"{spec.name}: no runtime scalar named {', '.join(unknown)} (it takes {known})")
+    extra = dict(spec.extra or {})
+    extra["scalar_values"] = {**spec.scalar_values, **{k: int(v) if isinstance(v, bool) or float(v).is_integer()
+                                                        else float(v) for k, v in scalars.items()}}
+    return KernelSpec(name=spec.name, signature=spec.signature, constexprs=spec.constexprs, args=spec.args,
+                      grid=spec.grid, extra=extra, graph_prefetch=spec.graph_prefetch)
+
+
+def launch(spec_or_manifest, tensors, grid=None, source: str | None = None, scalars: dict | None = None,
+           manifest: dict | None = None) -> kernels.Plan:
+    """Run one reference kernel on the GPU (asynchronously, on the current stream).
+
+    `grid` defaults to the spec's; one past the bound is refused with :class:`GridMismatch`.
+    `scalars` maps runtime scalar names to this launch's values.  `manifest`, when given beside a
+    spec, must agree with it."""
     spec = _as_spec(spec_or_manifest)
+    bound_of = manifest if manifest is not None else (
+        spec_or_manifest if isinstance(spec_or_manifest, dict) else spec)
+    if manifest is not None:
+        refuse_if_it_disagrees(manifest, spec)
     if not isinstance(tensors, dict):
         tensors = {a.name: t for a, t in zip(spec.args, tensors)}
-    if grid is not None:
-        g = tuple(int(x) for x in grid) + (1,) * (3 - len(tuple(grid)))
-        want = tuple(spec.grid) + (1,) * (3 - len(spec.grid))
-        if g != want:
-            raise GridMismatch(f"{spec.name}: launched with grid {g}, built for {want}")
+    bound = grid_bound(bound_of)
+    try:
+        g = refuse_grid_past_bound(spec.name, spec.grid if grid is None else grid, bound)
+    except ObjectError as e:
+        raise GridMismatch(str(e)) from None
     _check_tensors(spec, tensors)
-    return kernels.launch(spec, {a.name: tensors[a.name].view(-1) for a in spec.args}, source)
+    spec = _with_scalars(spec, scalars)
+    flat = {a.name: tensors[a.name].view(-1) for a in spec.args}
+    plan = kernels.resolve(spec, source)
+    entry = capi.plan_args(plan, bound[0] if bound[0] is not None else grid3(spec.grid)[0])
+    if entry is not None:
+        fam, names, ints, floats = entry
+        roles = {a.name: a.role for a in spec.args}
+        ts = [flat[n] for n in names]
+        rs = [roles[n] for n in names]
+        if plan.family == "attention_decode":
+            p = plan.params
+            ws = capi.decode_workspace(p["nkv"], p["group"], p["seq"], ts[0].device)
+            if ws is not None:
+                ts.append(ws)
+                rs.append("out")
+        capi.call_args(fam, ts, rs, ints, floats, g)
+        return plan
+    if g != grid3(spec.grid):
+        raise kernels.UnsupportedKernel(f"{spec.name}: family {plan.family} runs its whole grid "
+                                        f"{grid3(spec.grid)} only, not {g}")
+    kernels.run(plan, flat)
+    return plan
 
 
 def hip_launcher(binary, kernel_object, grid, args, artifacts=None):
-    """set_launcher-compatible entry: run the kernel object's kernel over `args` on the GPU."""
-    spec = _as_spec(kernel_object)
+    """set_launcher-compatible entry: run the kernel object's kernel over `args` on the GPU.  `args`
+    are in signature order with the constexprs dropped (driver.py:39-44): the tensors bind to the
+    kernel object's arguments in order, the other values to its runtime scalars in order."""
     ko = json.loads(kernel_object) if isinstance(kernel_object, (str, bytes)) else dict(kernel_object)
-    tensors = list(args)[: len(spec.args)]
-    source = ko.get("source")
-    return launch(spec, tensors, grid=grid, source=source)
+    spec = _as_spec(ko)
+    tensors, values = [], []
+    for a in args:
+        (tensors if hasattr(a, "data_ptr") else values).append(a)
+    if len(tensors) != len(spec.args):
+        raise ObjectError(f"{spec.name}: called with {len(tensors)} tensors, the kernel object has {len(spec.args)}")
+    names = [s["name"] for s in ko.get("scalars", [])]
+    if values and len(values) != len(names):
+        raise ObjectError(f"{spec.name}: called with {len(values)} scalars, the kernel object has {len(names)} "
+                          "(all or none)")
+    return launch(ko, tensors, grid=grid, source=ko.get("source"), scalars=dict(zip(names, values)) or None)
 
 
 _LAUNCHER = None

@@ -45,7 +45,17 @@ def _out(out, shape, dtype, like: torch.Tensor, name="out") -> torch.Tensor:
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6, out=None) -> torch.Tensor:
-    """y = bf16(x * rsqrt(mean(x^2) + eps) * w) over the last dim of a 2-D bf16 x."""
+    """y = bf16(x * rsqrt(mean(x^2) + eps) * w) over the last dim of a 2-D bf16 x; for an fp32 x (and
+    fp32 w) the same in fp32 throughout, y fp32."""
+    if isinstance(x, torch.Tensor) and x.dtype == F32:
+        _need(x, "x", F32, 2)
+        _need(w, "w", F32, 1)
+        rows, cols = x.shape
+        if w.numel() != cols:
+            raise ValueError(f"w has {w.numel()} elements, x rows have {cols}")
+        y = _out(out, (rows, cols), F32, x)
+        _lib.call("ptb_rmsnorm_f32", x.data_ptr(), w.data_ptr(), y.data_ptr(), rows, cols, float(eps), _stream(x))
+        return y
     _need(x, "x", BF16, 2)
     _need(w, "w", (BF16, F32), 1)
     rows, cols = x.shape
@@ -57,8 +67,24 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6, out=None) -> to
     return y
 
 
+def col_rms(x: torch.Tensor, eps: float = 1e-5, out=None) -> torch.Tensor:
+    """c[j] = rsqrt(mean_i x[i, j]^2 + eps) over the rows of a 2-D fp32 x (the column arm of the
+    reference's fp32 RMSNorm case)."""
+    _need(x, "x", F32, 2)
+    rows, cols = x.shape
+    c = _out(out, (cols,), F32, x)
+    _lib.call("ptb_col_rms_f32", x.data_ptr(), c.data_ptr(), rows, cols, float(eps), _stream(x))
+    return c
+
+
 def softmax_rows(x: torch.Tensor, out=None, out_dtype=BF16) -> torch.Tensor:
-    """Row softmax of bf16 rows; the result in bf16 (one rounding) or, with out_dtype fp32, unrounded."""
+    """Row softmax of bf16 rows; the result in bf16 (one rounding) or, with out_dtype fp32, unrounded.
+    fp32 rows give fp32 probabilities."""
+    if isinstance(x, torch.Tensor) and x.dtype == F32:
+        _need(x, "x", F32, 2)
+        y = _out(out, tuple(x.shape), F32, x)
+        _lib.call("ptb_softmax_rows_f32", x.data_ptr(), y.data_ptr(), x.shape[0], x.shape[1], _stream(x))
+        return y
     _need(x, "x", BF16, 2)
     if out_dtype not in (BF16, F32):
         raise TypeError(f"softmax_rows writes bf16 or fp32, not {out_dtype}")
@@ -69,14 +95,30 @@ def softmax_rows(x: torch.Tensor, out=None, out_dtype=BF16) -> torch.Tensor:
 
 
 def silu_mul(gate_up: torch.Tensor, out=None) -> torch.Tensor:
-    """[T, 2I] (gate | up) -> [T, I]: silu(gate) * up."""
-    _need(gate_up, "gate_up", BF16, 2)
+    """[T, 2I] (gate | up) -> [T, I]: silu(gate) * up, in bf16 (one rounding) or, for fp32 input, fp32."""
+    dt = F32 if isinstance(gate_up, torch.Tensor) and gate_up.dtype == F32 else BF16
+    _need(gate_up, "gate_up", dt, 2)
     rows, two_i = gate_up.shape
     if two_i % 2:
         raise ValueError("gate_up's last dim must be even (gate | up)")
-    y = _out(out, (rows, two_i // 2), BF16, gate_up)
-    _lib.call("ptb_silu_mul_bf16", gate_up.data_ptr(), y.data_ptr(), rows, two_i // 2, _stream(gate_up))
+    y = _out(out, (rows, two_i // 2), dt, gate_up)
+    fn = "ptb_silu_mul_f32" if dt == F32 else "ptb_silu_mul_bf16"
+    _lib.call(fn, gate_up.data_ptr(), y.data_ptr(), rows, two_i // 2, _stream(gate_up))
     return y
+
+
+def swiglu_f32(x: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, out=None) -> torch.Tensor:
+    """o = silu(x @ wg) * (x @ wu) for fp32 x [M, K], wg / wu [K, N], fp32 accumulation."""
+    _need(x, "x", F32, 2)
+    _need(wg, "wg", F32, 2)
+    _need(wu, "wu", F32, 2)
+    m, k = x.shape
+    if wg.shape[0] != k or tuple(wu.shape) != tuple(wg.shape):
+        raise ValueError("wg and wu must both be [K, N] for x [M, K]")
+    n = wg.shape[1]
+    o = _out(out, (m, n), F32, x)
+    _lib.call("ptb_swiglu_f32", x.data_ptr(), wg.data_ptr(), wu.data_ptr(), o.data_ptr(), m, n, k, _stream(x))
+    return o
 
 
 def _row_ld(x: torch.Tensor, name: str):

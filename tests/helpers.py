@@ -9,6 +9,12 @@ def randn(shape, seed, dtype=torch.bfloat16, std=1.0, mean=0.0):
     return (torch.randn(shape, generator=g) * std + mean).to(dtype)
 
 
+def rms(t) -> float:
+    """Root mean square of a tensor's values (fp64): the output scale absolute tolerances are
+    scaled by where outputs are not O(1)."""
+    return float(t.detach().double().cpu().pow(2).mean().sqrt())
+
+
 def assert_close(got, want, rtol, atol, what=""):
     """allclose(got, want, rtol, atol, equal_nan) with the reference verify's report
     (tests/runtime/verify.py:28-69) in the failure message."""
@@ -25,6 +31,32 @@ def assert_close(got, want, rtol, atol, what=""):
             f"{what}: max_abs_err={float(diff.max()):.6g} max_rel_err={float(rel.max()):.6g} "
             f"worst at {idx}: got={float(g.reshape(-1)[idx])!r} want={float(w.reshape(-1)[idx])!r}; "
             f"{bad}/{diff.numel()} outside (rtol={rtol}, atol={atol})")
+
+
+def rows_close(got, want, rtol, atol_frac):
+    """Per-row bound for outputs whose scale varies by row (late attention rows average more keys,
+    so their outputs shrink): |got - want| <= atol_frac * RMS(want row) + rtol * |want|, rows being
+    the last dimension.  Returns (ok, report)."""
+    g = got.detach().double().cpu()
+    w = want.detach().double().cpu()
+    d = w.shape[-1]
+    g2, w2 = g.reshape(-1, d), w.reshape(-1, d)
+    scale = w2.pow(2).mean(dim=1, keepdim=True).sqrt()
+    diff = (g2 - w2).abs().nan_to_num(float("inf"))
+    bound = atol_frac * scale + rtol * w2.abs()
+    bad = diff > bound
+    if not bool(bad.any()):
+        return True, ""
+    ratio = (diff / bound.clamp_min(1e-30)).reshape(-1)
+    idx = int(ratio.argmax())
+    return False, (f"{int(bad.sum())}/{bad.numel()} outside the per-row bound; worst at flat {idx}: "
+                   f"got={float(g2.reshape(-1)[idx])!r} want={float(w2.reshape(-1)[idx])!r} "
+                   f"(row {idx // d}, row RMS {float(scale[idx // d]):.3g})")
+
+
+def assert_close_rows(got, want, rtol, atol_frac, what=""):
+    ok, report = rows_close(got, want, rtol, atol_frac)
+    assert ok, f"{what}: {report}"
 
 
 def bits_equal(got, want):

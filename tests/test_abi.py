@@ -109,3 +109,58 @@ def test_error_mapping():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_lib.LibraryMissing):
         _lib.load(tmp_path / "nope.so")
+
+
+# ---- spec-driven entries (ptb_<family>_args): refusals happen before any HIP call
+def _desc(n, dtype=_lib.PTB_DTYPE_BF16, role=_lib.PTB_ROLE_IN, stride=1, ptr=None):
+    p = P16 if ptr is None else ptr
+    return _lib.PtbTensor(p, p, 0, n, stride, dtype, role)
+
+
+def _call(lib, fam, descs, ints, floats, grid):
+    arr = (_lib.PtbTensor * max(len(descs), 1))(*descs)
+    iv = (ctypes.c_int64 * max(len(ints), 1))(*ints)
+    fv = (ctypes.c_double * max(len(floats), 1))(*floats)
+    gv = (ctypes.c_int32 * 3)(*grid)
+    return getattr(lib, f"ptb_{fam}_args")(arr, len(descs), iv, len(ints), fv, len(floats), gv, None)
+
+
+def test_args_entries_refuse_bad_calls(lib):
+    rows, cols, programs = 16, 64, 4
+    x, w = _desc(rows * cols), _desc(cols)
+    y = _desc(rows * cols, role=_lib.PTB_ROLE_OUT)
+    ok_args = [x, w, y]
+    # wrong counts
+    assert _call(lib, "rmsnorm", ok_args[:2], [rows, cols, programs], [1e-6], (4, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "rmsnorm", ok_args, [rows, cols], [1e-6], (4, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "rmsnorm", ok_args, [rows, cols, programs], [], (4, 1, 1)) == _lib.PTB_ERR_SHAPE
+    # a size that disagrees with the parameters
+    bad = [x, _desc(cols + 1), y]
+    assert _call(lib, "rmsnorm", bad, [rows, cols, programs], [1e-6], (4, 1, 1)) == _lib.PTB_ERR_SHAPE
+    # the grid past the program bound, below 1, or off the x axis
+    assert _call(lib, "rmsnorm", ok_args, [rows, cols, programs], [1e-6], (5, 1, 1)) == _lib.PTB_ERR_GRID
+    assert _call(lib, "rmsnorm", ok_args, [rows, cols, programs], [1e-6], (0, 1, 1)) == _lib.PTB_ERR_GRID
+    assert _call(lib, "rmsnorm", ok_args, [rows, cols, programs], [1e-6], (4, 2, 1)) == _lib.PTB_ERR_GRID
+    # a written tensor declared read-only, an unknown dtype, a strided tensor
+    ro = [x, w, _desc(rows * cols)]
+    assert _call(lib, "rmsnorm", ro, [rows, cols, programs], [1e-6], (4, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "rmsnorm", [x, _desc(cols, dtype=9), y], [rows, cols, programs], [1e-6],
+                 (4, 1, 1)) == _lib.PTB_ERR_DTYPE
+    assert _call(lib, "rmsnorm", [x, w, _desc(rows * cols, role=1, stride=2)], [rows, cols, programs], [1e-6],
+                 (4, 1, 1)) == _lib.PTB_ERR_UNSUPPORTED
+    # GEMM: M*K, K*N, M*N must agree; only the whole grid runs
+    m, n, k = 64, 128, 64
+    a, b, c = _desc(m * k), _desc(k * n), _desc(m * n, role=_lib.PTB_ROLE_OUT)
+    assert _call(lib, "gemm", [a, b, _desc(m * n + 8, role=1)], [m, n, k, 2], [], (2, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "gemm", [a, b, c], [m, n, k, 2], [], (3, 1, 1)) == _lib.PTB_ERR_GRID
+    assert _call(lib, "gemm", [a, b, c], [m, n, k, 2], [], (1, 1, 1)) == _lib.PTB_ERR_UNSUPPORTED
+    # attention: one program per (batch, query head); a partial grid must cover whole batches
+    q, kk = _desc(4 * 128 * 128), _desc(2 * 128 * 128)
+    o = _desc(4 * 128 * 128, role=_lib.PTB_ROLE_INOUT)
+    ints = [1, 4, 2, 128, 128, 1]
+    assert _call(lib, "flash_attn", [q, kk, kk, o], ints, [0.088], (5, 1, 1)) == _lib.PTB_ERR_GRID
+    assert _call(lib, "flash_attn", [q, kk, kk, o], ints, [0.088], (3, 1, 1)) == _lib.PTB_ERR_UNSUPPORTED
+    assert _call(lib, "flash_attn", [q, kk, kk], ints, [0.088], (4, 1, 1)) == _lib.PTB_ERR_SHAPE
+    # silu_mul: a partial grid has to end on a whole row
+    gu, out = _desc(2 * 4 * 256), _desc(4 * 256, role=_lib.PTB_ROLE_OUT)
+    assert _call(lib, "silu_mul", [gu, out], [4, 256, 8], [], (3, 1, 1)) == _lib.PTB_ERR_UNSUPPORTED

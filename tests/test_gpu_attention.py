@@ -1,14 +1,18 @@
 """Parity of the flash-attention kernel with the oracle's restatement of the reference's
 _prefill_kernel (P rounded to bf16 before P.V).  The kernel blocks keys by 64 where the reference
-blocks by 1024, so the bf16 rounding points of P differ: bf16 tolerance rtol = atol = 2e-2 (O is
-O(1)), and the exact invariants (row 0 = V[0]) are checked bit-for-bit."""
+blocks by 1024, so the bf16 rounding points of P differ: bf16 tolerance rtol = 2e-2 with the
+absolute floor 2e-2 times each output row's RMS (a late row averages thousands of keys, so its
+outputs are far below 1 and a fixed absolute floor would hide a skipped key block;
+tests/test_tolerances.py shows this bound rejects one skipped 64-key block and an off-by-one causal
+mask), and the exact invariants (row 0 = V[0]) are checked bit-for-bit.  Outputs are NaN-filled
+before every launch (tests/conftest.py)."""
 import math
 
 import pytest
 import torch
 
 import oracle
-from helpers import assert_close, bits_equal, randn
+from helpers import assert_close_rows, bits_equal, randn
 from ptb_amd import _lib, ops
 
 pytestmark = pytest.mark.gpu
@@ -45,7 +49,7 @@ def test_flash_attention(batch, hq, hkv, s, causal):
     if s >= 2048:
         heads = torch.tensor([0, 5, 13, 31])
     want = oracle.flash_attention(q, k, v, hq, hkv, causal, 1.0 / math.sqrt(128))
-    assert_close(o[heads], want[heads], RTOL, ATOL, f"flash {batch}x{hq}x{hkv}x{s} causal={causal}")
+    assert_close_rows(o[heads], want[heads], RTOL, ATOL, f"flash {batch}x{hq}x{hkv}x{s} causal={causal}")
     if causal:
         # row 0 attends only to key 0: p = 1 exactly, so O[h, 0] = V[kv(h), 0] bit for bit
         g = hq // hkv

@@ -227,7 +227,8 @@ def test_hip_launcher_hook_takes_kernel_json():
     launcher.set_launcher(launcher.hip_launcher)
     try:
         fn = launcher.registered_launcher()
-        fn(b"", json.dumps(man), tuple(man["grid"]), args + [2048, 4096])
+        # signature order with constexprs dropped: the tensors, then xnumel and r0_numel by name
+        fn(b"", json.dumps(man), tuple(man["grid"]), args + [man["scalars"][0]["default"], man["scalars"][1]["default"]])
     finally:
         launcher.set_launcher(None)
     torch.cuda.synchronize()
@@ -238,8 +239,9 @@ def test_hip_launcher_hook_takes_kernel_json():
 
 def test_hip_device_over_raw_files(tmp_path):
     """HipDevice reads .raw inputs, poisons outputs, runs, writes .raw outputs; the result equals
-    the launcher's bit for bit and passes verify against the oracle."""
-    man = MANIFESTS["qwen3_8b_layer_prefill_512x512_bf16"]["kernels"][5]   # k/v projection GEMM
+    the launcher's bit for bit, matches the oracle on sampled rows, and passes verify.compare (the
+    reference verify's allclose and report) against the oracle's full output."""
+    man = MANIFESTS["qwen3_8b_layer_prefill_512x512_bf16"]["kernels"][3]   # k/v projection GEMM
     spec = contract.spec_from_manifest(man)
     host = contract.seeded_inputs(spec, torch, seed=0)
     paths = {a.name: str(tmp_path / f"{a.name}.raw") for a in spec.args}
@@ -255,6 +257,11 @@ def test_hip_device_over_raw_files(tmp_path):
     torch.cuda.synchronize()
     assert bits_equal(got, dev[out.name].cpu())
     check_against_oracle(plan, host, {out.name: got})
+    p = plan.params
+    want = oracle.gemm(host[p["a"]].view(p["m"], p["k"]), host[p["b"]].view(p["k"], p["n"])).reshape(-1)
+    ok, report = verify.compare(spec, {out.name: raw}, {out.name: want}, torch, rtol=2e-2,
+                                atol=2e-2 * float(want.float().abs().mean()))
+    assert ok, report
 
 
 def test_qwen3_layer_from_bundle_manifests_matches_composed_oracle():
@@ -349,3 +356,73 @@ def test_qwen3_decode_layer_from_bundle_manifests_matches_composed_oracle():
     want = oracle.qwen3_decode_layer(x, wts, kc, vc, cos, sin, hq, hkv, d, 1e-6)
     rms = float(want.float().pow(2).mean().sqrt())
     assert_close(y.cpu(), want, 2e-2, 2e-2 * max(1.0, rms), "qwen3 decode layer from manifests")
+
+
+# ---- the spec-driven C entries (ptb_<family>_args) on three bundle kernels ----------------------
+def _bundle(workload, index, seed=0):
+    man = MANIFESTS[workload]["kernels"][index]
+    spec = contract.spec_from_manifest(man)
+    host = contract.seeded_inputs(spec, torch, seed=seed)
+    dev = {a.name: (host[a.name].cuda() if a.name in host
+                    else torch.empty(a.numel, dtype=getattr(torch, a.dtype), device="cuda")) for a in spec.args}
+    return man, spec, host, dev
+
+
+def _roles(spec):
+    return [a.role for a in spec.args]
+
+
+def test_args_entry_rmsnorm_bundle_kernel():
+    """L2048/00 through ptb_rmsnorm_args with the spec's tensors in spec order, ints [xnumel,
+    r0_numel, programs] and the whole grid; then a grid of 3 of its 8 programs, which writes the
+    first 3 * 256 rows only (the rest keeps its NaN poison)."""
+    from ptb_amd import capi
+    man, spec, host, dev = _bundle("qwen3_8b_layer_prefill_2048x2048_bf16", 0)
+    rows, cols = 2048, 4096
+    tens = [dev[a.name] for a in spec.args]
+    capi.call_args("rmsnorm", tens, _roles(spec), [rows, cols, spec.grid[0]], [1e-6], spec.grid)
+    torch.cuda.synchronize()
+    want = oracle.rmsnorm(host["in_ptr0"].view(rows, cols), host["in_ptr1"], 1e-6)
+    assert_close(dev["out_ptr1"].cpu().view(rows, cols), want, 2e-2, 2e-2, "rmsnorm_args")
+    part = torch.full((rows * cols,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    capi.call_args("rmsnorm", tens[:2] + [part], _roles(spec), [rows, cols, spec.grid[0]], [1e-6], (3, 1, 1))
+    torch.cuda.synchronize()
+    got = part.cpu().view(rows, cols)
+    assert_close(got[: 3 * 256], want[: 3 * 256], 2e-2, 2e-2, "rmsnorm_args partial grid")
+    assert torch.isnan(got[3 * 256:].float()).all()
+
+
+def test_args_entry_gemm_residual_bundle_kernel():
+    """L2048/08 (o-projection + residual, args [in_ptr0 residual, arg_A, arg_B, out_ptr0]) through
+    ptb_gemm_args; sampled rows against the oracle with the absolute floor scaled to the output."""
+    from ptb_amd import capi
+    man, spec, host, dev = _bundle("qwen3_8b_layer_prefill_2048x2048_bf16", 8)
+    assert [a.name for a in spec.args] == ["in_ptr0", "arg_A", "arg_B", "out_ptr0"]
+    m, k, n = 2048, 4096, 4096
+    capi.call_args("gemm", [dev[a.name] for a in spec.args], _roles(spec), [m, n, k, spec.grid[0]], [], spec.grid)
+    torch.cuda.synchronize()
+    rows = sample(m, 16)
+    want = oracle.gemm(host["arg_A"].view(m, k)[rows], host["arg_B"].view(k, n),
+                       host["in_ptr0"].view(m, n)[rows])
+    got = dev["out_ptr0"].cpu().view(m, n)[rows]
+    assert_close(got, want, 2e-2, 2e-2 * float(want.float().abs().mean()), "gemm_args residual")
+
+
+def test_args_entry_attention_bundle_kernel():
+    """attention_prefill_32x8x4096_bf16's _prefill_kernel through ptb_flash_attn_args: ints [batch,
+    HQ, HQ / G, S, D, CAUSAL], floats [SCALE] from its constexprs, grid (32, 1, 1)."""
+    from ptb_amd import capi
+    man, spec, host, dev = _bundle("attention_prefill_32x8x4096_bf16", 0)
+    ce = man["constexprs"]
+    hq, g, s, d = ce["HQ"], ce["G"], ce["S"], ce["D"]
+    capi.call_args("flash_attn", [dev[a.name] for a in spec.args], _roles(spec),
+                   [1, hq, hq // g, s, d, int(ce["CAUSAL"])], [ce["SCALE"]], spec.grid)
+    torch.cuda.synchronize()
+    heads = torch.tensor([0, 17])
+    q = host["q_ptr"].view(hq, s, d)[heads]
+    k = host["k_ptr"].view(hq // g, s, d)[heads // g]
+    v = host["v_ptr"].view(hq // g, s, d)[heads // g]
+    want = oracle.flash_attention(q, k, v, 2, 2, True, ce["SCALE"])
+    got = dev["o_ptr"].cpu().view(hq, s, d)[heads]
+    from helpers import assert_close_rows
+    assert_close_rows(got, want, 2e-2, 2e-2, "flash_attn_args")

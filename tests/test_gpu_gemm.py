@@ -2,13 +2,17 @@
 
 Full-size shapes are checked on sampled rows (one random row from every 256-row tile plus the
 first and last rows): a row of C depends only on that row of A, so the oracle computes exactly
-those rows.  Tolerance: the BASELINE bf16/fp8 bound, rtol = atol = 2e-2 (outputs are O(1) by
-construction), and the quantisers are bit-exact."""
+those rows.  Tolerance: the BASELINE bf16/fp8 bound, rtol = 2e-2, with the absolute floor 2e-2
+times the RMS of the expected output wherever outputs are not O(1) (the BASELINE config-2 operands
+~N(0, 1/64^2) give outputs of RMS 1/64, so an absolute 2e-2 would exceed the outputs themselves;
+tests/test_tolerances.py shows the scaled bound rejects a product that drops one 32-deep K step).
+Every output buffer is NaN-filled before the launch (tests/conftest.py), so an unwritten tile
+fails.  The quantisers are bit-exact."""
 import pytest
 import torch
 
 import oracle
-from helpers import assert_close, bits_equal, randn
+from helpers import assert_close, bits_equal, randn, rms
 from ptb_amd import _lib, ops
 
 pytestmark = pytest.mark.gpu
@@ -46,7 +50,7 @@ def run_gemm(m, k, n, seed, std_a, std_b, resid=False):
 def test_gemm_layer_shapes(m, k, n, resid):
     std = 1.0 / 64.0
     got, want = run_gemm(m, k, n, 0, std, std, resid)
-    assert_close(got, want, RTOL, ATOL, f"gemm {m}x{k}x{n}")
+    assert_close(got, want, RTOL, ATOL * rms(want), f"gemm {m}x{k}x{n}")
 
 
 @pytest.mark.parametrize("m,k,n", [
@@ -187,4 +191,5 @@ def test_gemm_swiglu_refusals():
     b = torch.zeros((128, 2 * 192), dtype=torch.bfloat16, device=DEV)     # inter = 192: not a multiple of 128
     with pytest.raises(_lib.UnsupportedError):
         ops.gemm_swiglu(a, b)
+
 

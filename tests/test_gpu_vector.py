@@ -179,3 +179,80 @@ def test_error_paths_on_device():
     with pytest.raises(_lib.UnsupportedError):
         ops.qk_norm_rope(xh, torch.ones(64, dtype=torch.bfloat16, device=DEV),
                          torch.ones((4, 64), device=DEV), torch.zeros((4, 64), device=DEV))
+
+
+# ---- fp32 vector ops: the reference's own fp32 workload cases, at their tolerances -------------
+
+def _case_inputs(seed, *shapes_scales):
+    """make_inputs of tests/cases/workloads/{rmsnorm,softmax,swiglu}.py: one generator, fp32 randn per
+    argument in order (times the case's scale)."""
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(n, generator=g, dtype=torch.float32) * s for n, s in shapes_scales]
+
+
+def test_rmsnorm_f32_reference_case():
+    """tests/cases/workloads/rmsnorm.py: M=8, N=64, EPS=1e-5, fp32 x and w; outputs o (row arm) and
+    c (column arm) within the case's rtol = atol = 1e-4 and the north-star's 1e-5 relative bound."""
+    m, n, eps = 8, 64, 1e-5
+    x, w = _case_inputs(0, (m * n, 1.0), (n, 1.0))
+    x = x.reshape(m, n)
+    o = ops.rmsnorm(x.to(DEV), w.to(DEV), eps).cpu()
+    c = ops.col_rms(x.to(DEV), eps).cpu()
+    want_o, want_c = oracle.rmsnorm_f32(x, w, eps), oracle.col_rms_f32(x, eps)
+    assert_close(o, want_o, 1e-5, 1e-6, "rmsnorm.py o")
+    assert_close(c, want_c, 1e-5, 1e-6, "rmsnorm.py c")
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(2048, 4096, 1), (3, 20, 2), (5, 4100, 3), (2, 40000, 4)])
+def test_rmsnorm_f32_shapes(rows, cols, seed):
+    """Wave-per-row, block-per-row and the two-pass long-row forms, fp32 throughout."""
+    x = randn((rows, cols), seed, dtype=torch.float32)
+    w = randn((cols,), seed + 1, dtype=torch.float32, std=0.02, mean=1.0)
+    got = ops.rmsnorm(x.to(DEV), w.to(DEV), 1e-6).cpu()
+    assert_close(got, oracle.rmsnorm_f32(x, w, 1e-6), 1e-5, 1e-6, f"rmsnorm f32 {rows}x{cols}")
+    c = ops.col_rms(x.to(DEV), 1e-6).cpu()
+    assert_close(c, oracle.col_rms_f32(x, 1e-6), 1e-5, 1e-6, f"col rms {rows}x{cols}")
+
+
+def test_softmax_f32_reference_case():
+    """tests/cases/workloads/softmax.py: 256 rows of 64 fp32 values, rtol 1e-5, atol 1e-6 (:84)."""
+    (x,) = _case_inputs(0, (256 * 64, 1.0))
+    x = x.reshape(256, 64)
+    got = ops.softmax_rows(x.to(DEV)).cpu()
+    assert got.dtype == torch.float32
+    assert_close(got, oracle.softmax_rows(x, out_dtype=torch.float32), 1e-5, 1e-6, "softmax.py")
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(2048, 6144, 1), (7, 12, 2), (3, 9000, 3), (2, 40000, 4)])
+def test_softmax_f32_shapes(rows, cols, seed):
+    x = randn((rows, cols), seed, dtype=torch.float32, std=3.0)
+    if rows > 2:
+        x[1, 5] = float("nan")          # a NaN row stays NaN
+        x[2, :] = -5.0                  # constant row: uniform
+    got = ops.softmax_rows(x.to(DEV)).cpu()
+    assert_close(got, oracle.softmax_rows(x, out_dtype=torch.float32), 1e-5, 1e-6, f"softmax f32 {rows}x{cols}")
+    assert torch.isnan(got[1]).all() if rows > 2 else True
+
+
+def test_swiglu_f32_reference_case():
+    """tests/cases/workloads/swiglu.py: x [128, 256], wg / wu [256, 128], all randn * 0.1 in fp32,
+    o = silu(x @ wg) * (x @ wu) at rtol = atol = 1e-3 (:100); the elementwise half alone (silu_mul
+    over gate | up) at the fp32 vector bound 1e-5."""
+    m, n, k = 128, 128, 256
+    x, wg, wu = _case_inputs(0, (m * k, 0.1), (k * n, 0.1), (k * n, 0.1))
+    x, wg, wu = x.reshape(m, k), wg.reshape(k, n), wu.reshape(k, n)
+    o = ops.swiglu_f32(x.to(DEV), wg.to(DEV), wu.to(DEV)).cpu()
+    assert_close(o, oracle.swiglu_f32(x, wg, wu), 1e-3, 1e-3, "swiglu.py")
+    gu = torch.cat([x @ wg, x @ wu], dim=1).contiguous()
+    got = ops.silu_mul(gu.to(DEV)).cpu()
+    assert got.dtype == torch.float32
+    assert_close(got, oracle.silu_mul_f32(gu), 1e-5, 1e-6, "silu_mul f32")
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 200, 100), (64, 1000, 513)])
+def test_swiglu_f32_ragged(m, n, k):
+    x = randn((m, k), 7, dtype=torch.float32, std=0.1)
+    wg = randn((k, n), 8, dtype=torch.float32, std=0.1)
+    wu = randn((k, n), 9, dtype=torch.float32, std=0.1)
+    o = ops.swiglu_f32(x.to(DEV), wg.to(DEV), wu.to(DEV)).cpu()
+    assert_close(o, oracle.swiglu_f32(x, wg, wu), 1e-4, 1e-5, f"swiglu f32 {m}x{n}x{k}")

@@ -189,3 +189,55 @@ def test_device_registry_and_missing_inputs(tmp_path):
     req = device.Launch(str(tmp_path), man, raw_paths={})
     with pytest.raises(device.DeviceError):
         dev.launch(req)
+
+
+def test_grid_bound_and_refusal():
+    """contract/kernel_object.py:93-107: the bound is kernel.json's grid_bound where stated, else the
+    spec's grid; an axis past it, below 1, or past the 21-bit program id is refused."""
+    spec = spec_of("qwen3_8b_layer_prefill_2048x2048_bf16", 0)
+    assert contract.grid_bound(spec) == contract.grid3(spec.grid)
+    man = spec.manifest()
+    assert contract.grid_bound(dict(man, grid_bound=[16, None, 1])) == (16, None, 1)
+    assert contract.refuse_grid_past_bound("k", (8,), (8, 1, 1)) == (8, 1, 1)
+    assert contract.refuse_grid_past_bound("k", (3, 1, 1), (8, 1, 1)) == (3, 1, 1)
+    for g in [(9, 1, 1), (8, 2, 1), (0, 1, 1), (8, 1, 1 << 22)]:
+        with pytest.raises(contract.ObjectError):
+            contract.refuse_grid_past_bound("k", g, (8, 1, None))
+    with pytest.raises(launcher.GridMismatch):
+        launcher.launch(spec, {}, grid=(spec.grid[0] + 1, 1, 1))
+
+
+def test_manifest_spec_disagreements_refused():
+    """contract/kernel_object.py:264-286: a manifest from another compile is refused by name of what
+    differs, before any tensor is looked at."""
+    spec = spec_of("qwen3_8b_layer_prefill_2048x2048_bf16", 0)
+    man = spec.manifest()
+    assert contract.disagreements(man, spec) == []
+    other = json.loads(json.dumps(man))
+    other["grid"] = [spec.grid[0] * 2, 1, 1]
+    other["args"][0]["shape"] = [other["args"][0]["shape"][0] + 1]
+    assert contract.disagreements(other, spec) == ["grid3", "numel"]
+    with pytest.raises(contract.ObjectError):
+        launcher.launch(spec, {}, manifest=other)
+    swapped = json.loads(json.dumps(man))
+    swapped["args"][0], swapped["args"][1] = swapped["args"][1], swapped["args"][0]
+    assert "argv_order" in contract.disagreements(swapped, spec)
+
+
+def test_hip_launcher_maps_scalars_by_name():
+    """driver.py:39-44: the launcher gets the call's arguments in signature order with constexprs
+    dropped; the values that are not tensors bind to the kernel object's runtime scalars in order,
+    all or none, and an unknown scalar name is refused."""
+    spec = spec_of("qwen3_8b_layer_prefill_2048x2048_bf16", 0)   # rmsnorm: xnumel, r0_numel
+    man = spec.manifest()
+    names = [s["name"] for s in man["scalars"]]
+    assert names == ["xnumel", "r0_numel"]
+    with pytest.raises(contract.ObjectError):   # one scalar of two
+        launcher.hip_launcher(None, json.dumps(man), spec.grid, [torch.zeros(1), torch.zeros(1), torch.zeros(1), 5])
+    with pytest.raises(contract.ObjectError):   # a tensor missing
+        launcher.hip_launcher(None, man, spec.grid, [torch.zeros(1), torch.zeros(1), 2048, 4096])
+    with pytest.raises(contract.ObjectError):
+        launcher._with_scalars(spec, {"ynumel": 3})
+    s2 = launcher._with_scalars(spec, {"xnumel": 1024, "r0_numel": 4096})
+    assert s2.scalar_values == {"xnumel": 1024, "r0_numel": 4096}
+    assert spec.scalar_values["xnumel"] == 2048      # the spec itself is unchanged

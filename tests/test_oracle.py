@@ -446,3 +446,57 @@ def test_golden_vectors():
     # the independent fp64 references the fixtures were made from agree with the oracle too
     assert bits_frac(gv["rmsnorm.y"], gv["rmsnorm.y64"]) > 0.999
     assert torch.allclose(gv["attn.o"].float(), gv["attn.o64"].float(), rtol=2e-2, atol=2e-2)
+
+
+# ------------------------------------------------------------------ fp32 vector ops
+def test_rmsnorm_f32_matches_library_and_brute_force():
+    """The fp32 row arm against torch's rms_norm in fp64 (relative 1e-6: fp32 rounding only) and a
+    brute-force fsum loop; a normaliser off by one (dividing by N - 1) fails the fp64 pin."""
+    x = rnd((16, 64), 60, torch.float32)
+    w = rnd((64,), 61, torch.float32)
+    got = oracle.rmsnorm_f32(x, w, 1e-5)
+    assert got.dtype == torch.float32
+    want = torch.nn.functional.rms_norm(x.double(), (64,), w.double(), 1e-5)
+    assert torch.allclose(got.double(), want, rtol=1e-6, atol=1e-7)
+    for i in range(3):
+        r = 1 / math.sqrt(math.fsum(float(v) ** 2 for v in x[i]) / 64 + 1e-5)
+        for j in range(0, 64, 7):
+            assert abs(float(got[i, j]) - float(x[i, j]) * r * float(w[j])) <= 1e-6 * (abs(float(got[i, j])) + 1e-6)
+    off = (x.double() * torch.rsqrt((x.double() ** 2).sum(-1, keepdim=True) / 63 + 1e-5)) * w.double()
+    assert not torch.allclose(got.double(), off, rtol=1e-5, atol=1e-6)
+
+
+def test_col_rms_f32_closed_form():
+    """Column arm: a matrix whose column j is constant c_j gives 1/sqrt(c_j^2 + eps); random input
+    against the fp64 formula; a transposed reduction (over columns) fails it."""
+    c = torch.tensor([0.5, -2.0, 3.0, 1e-3])
+    x = c[None, :].repeat(8, 1)
+    got = oracle.col_rms_f32(x, 1e-5)
+    assert torch.allclose(got.double(), 1 / torch.sqrt(c.double() ** 2 + 1e-5), rtol=1e-6)
+    y = rnd((8, 64), 62, torch.float32)
+    want = torch.rsqrt((y.double() ** 2).mean(0) + 1e-5)
+    assert torch.allclose(oracle.col_rms_f32(y, 1e-5).double(), want, rtol=1e-6)
+    wrong = torch.rsqrt((y.double() ** 2).mean(1) + 1e-5)
+    assert wrong.shape != want.shape or not torch.allclose(wrong, want, rtol=1e-3)
+
+
+def test_softmax_f32_input_matches_library():
+    x = rnd((256, 64), 63, torch.float32)
+    got = oracle.softmax_rows(x, torch.float32)
+    assert torch.allclose(got.double(), torch.softmax(x.double(), -1), rtol=1e-6, atol=1e-9)
+
+
+def test_silu_mul_f32_and_swiglu_f32_match_library():
+    """silu(g) * u in fp32 against F.silu in fp64; the SwiGLU block against fp64 matmuls; swapping
+    the gate and up weights (a plausible slip) fails the pin."""
+    gu = rnd((9, 2 * 40), 64, torch.float32)
+    got = oracle.silu_mul_f32(gu)
+    g, u = gu[:, :40].double(), gu[:, 40:].double()
+    assert torch.allclose(got.double(), torch.nn.functional.silu(g) * u, rtol=1e-6, atol=1e-7)
+    x = rnd((32, 48), 65, torch.float32, 0.1)
+    wg, wu = rnd((48, 24), 66, torch.float32, 0.1), rnd((48, 24), 67, torch.float32, 0.1)
+    want = torch.nn.functional.silu(x.double() @ wg.double()) * (x.double() @ wu.double())
+    o = oracle.swiglu_f32(x, wg, wu)
+    assert torch.allclose(o.double(), want, rtol=1e-5, atol=1e-7)
+    swapped = torch.nn.functional.silu(x.double() @ wu.double()) * (x.double() @ wg.double())
+    assert not torch.allclose(o.double(), swapped, rtol=1e-3, atol=1e-3)

@@ -226,3 +226,23 @@ def test_grouped_mm_against_per_group_loops():
                 exact = math.fsum(float(a[i, q]) * float(b[g, q, j]) for q in range(k))
                 want[i, j] = torch.tensor(exact, dtype=torch.float64).to(F32).to(BF16)
     assert torch.equal(got, want.to(BF16))
+
+
+def test_fill_zero_cast_and_slice_add_closed_forms():
+    """The three small helpers, each against values written out by hand: fill_zero is n zeros of
+    the asked dtype; the int64 -> int32 cast keeps the low 32 bits as two's complement; slice_add
+    is float(x[first + j]) + s for j < count."""
+    z = oracle.fill_zero(5)
+    assert z.dtype == torch.int64 and z.tolist() == [0, 0, 0, 0, 0]
+    assert oracle.fill_zero(3, torch.int32).dtype == torch.int32
+    x = torch.tensor([0, 1, -1, 2 ** 31 - 1, 2 ** 31, 2 ** 32 + 5, -(2 ** 31) - 1, 2 ** 40 + 2 ** 31 + 7])
+    want = [0, 1, -1, 2147483647, -2147483648, 5, 2147483647, -2147483641]
+    got = oracle.cast_i64_i32(x)
+    assert got.dtype == torch.int32 and got.tolist() == want
+    v = torch.tensor([1.5, -2.0, 0.25, 3.0, 1e-8], dtype=torch.bfloat16)
+    s = oracle.slice_add(v, first=1, count=3, s=1.0)
+    assert s.dtype == torch.float32
+    assert s.tolist() == [-1.0, 1.25, 4.0]
+    assert oracle.slice_add(v).tolist() == [2.5]          # the bundle kernel: x[0] + 1
+    tiny = oracle.slice_add(v, first=4, count=1, s=1.0)
+    assert tiny.tolist() == [float(torch.tensor(1e-8, dtype=torch.bfloat16).float() + 1.0)]
