@@ -370,7 +370,10 @@ int ptb_rms_broadcast_bf16(const void* x, const void* a, const float* ss, const 
  * bf16( A[start[g] + i, :] . B_g ) for i < rows[g], B_g the row-major [k, n] bf16 matrix at
  * b + g * weight_stride (nweights of them); A is [a_rows, k], C [a_rows, n]; start/rows hold ntab
  * int32 entries.  Entries that do not describe rows inside A or a weight inside B count as empty.
- * k % 64 == 0, n % 8 == 0.
+ * A group listed by several programs is computed once (with ntab <= 1024).  The groups' row ranges
+ * must not overlap one another (the reference's tables, consecutive ranges of expert rows, never
+ * do; overlapping ranges written with different weights have no defined result there either): the
+ * launch sizes its grid for ceil(a_rows / 128) + nprog row tiles.  k % 64 == 0, n % 8 == 0.
  * Replaces: LOP_gmm_gate_up/05__grouped_mm_kernel/_grouped_mm_kernel_triton.py:4-46 (and gmm_down) */
 int ptb_grouped_gemm_bf16(const void* a, const void* b, const int32_t* group, const int32_t* start,
                           const int32_t* rows, void* c, int64_t nprog, int64_t ntab, int64_t a_rows,

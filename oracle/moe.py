@@ -108,22 +108,20 @@ def sort_rows(x: torch.Tensor, rows: int, descending: bool = False):
 
 def topk_rows(x: torch.Tensor, e: int, k: int, largest: bool = True):
     """LOP_router_post/01__topk_kernel/_topk_kernel_triton.py:4-30: k rounds of: the row's max
-    (min), the lowest column holding it, that column marked spent (-inf / +inf).  Returns
-    (values [rows*k] fp32, indices [rows*k] int64)."""
-    xr = x.reshape(-1, e).clone().float()
-    rows = xr.shape[0]
-    spent = float("-inf") if largest else float("inf")
-    vals = torch.zeros(rows, k, dtype=F32)
-    idxs = torch.zeros(rows, k, dtype=I64)
-    col = torch.arange(e)
-    for n in range(k):
-        best = xr.max(1).values if largest else xr.min(1).values
-        at = torch.where(xr == best[:, None], col[None, :], torch.full_like(col, e)[None, :]).min(1).values
-        vals[:, n] = best
-        idxs[:, n] = at
-        xr[torch.arange(rows), at.clamp(max=e - 1)] = torch.where(at < e, torch.full_like(best, spent),
-                                                                 xr[torch.arange(rows), at.clamp(max=e - 1)])
-    return vals.reshape(-1), idxs.reshape(-1)
+    (min), the lowest column holding it, that column marked spent (-inf / +inf) -- for rows of
+    numbers, the k largest (smallest) in order, equal values by lower column.  A NaN, which the
+    reference's comparisons leave to its backend, is ordered after every number and NaNs among
+    themselves by column (parity unpinned for NaN).  Restated as a stable two-key sort: by value,
+    then NaN-last.  Returns (values [rows*k] fp32, indices [rows*k] int64)."""
+    xr = x.reshape(-1, e).float()
+    v = xr.clone()
+    nan = torch.isnan(v)
+    v[nan] = 0.0
+    order = torch.sort(v, dim=1, descending=largest, stable=True).indices
+    order = torch.gather(order, 1, torch.sort(torch.gather(nan, 1, order).to(torch.int8), dim=1, stable=True).indices)
+    idxs = order[:, :k]
+    vals = torch.gather(xr, 1, idxs)
+    return vals.reshape(-1).contiguous(), idxs.to(I64).reshape(-1).contiguous()
 
 
 def gather_rows(slot: torch.Tensor, x: torch.Tensor, k: int, cols: int) -> torch.Tensor:

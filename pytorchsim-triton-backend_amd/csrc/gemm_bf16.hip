@@ -32,14 +32,10 @@ using namespace ptb;
 
 namespace {
 
-constexpr int BK = 32;
 constexpr int kThreads = 256;
-#ifndef PTB_GEMM_STAGES
-#define PTB_GEMM_STAGES 4
-#endif
-constexpr int kStages = PTB_GEMM_STAGES;  // LDS ring depth, 3..5 (up to 32 KB each of the 160 KB)
-static_assert(kStages >= 3 && kStages <= 5, "LDS ring of 3 to 5 stages");
 constexpr int kGroupM = 8;
+// K past the end the DMA stream may address (the deepest ring: 4 stages of 32 or 2 of 64)
+constexpr int kRunAhead = 128;
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -47,21 +43,39 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // Tile shape: the 4 waves sit 2x2, each owning WM x WN blocks of 32x32, so the workgroup tile is
-// BM = 64*WM rows by BN = 64*WN columns (256x256, 256x128 or 128x128).
-template <int WM, int WN>
+// BM = 64*WM rows by BN = 64*WN columns (256x256, 256x128 or 128x128).  A stage holds BK of K:
+// 32 (a 64-byte piece of every A row) in a ring of NS = 4 stages of up to 32 KB, or, for the
+// 256x256 tile, 64 (a whole 128-byte line of every A row: the L2 serves a request per line, and a
+// half-line request costs a whole one) in a ring of NS = 2 stages of 64 KB.  The DMA of stage kt + DIST
+// is issued after the barrier of step kt: DIST = NS - 1 reuses the slot freed one step earlier,
+// DIST = NS the slot freed by that barrier.
+template <int WM, int WN, int BKT>
 struct Shape {
+  static constexpr int BK = BKT;
+  static constexpr int NS = BK == 64 ? 2 : 4;
+  static constexpr int DIST = BK == 64 ? 2 : 3;
+  static constexpr int SPS = BK / 16;                    // 16-wide K slices per stage
   static constexpr int BM = 64 * WM, BN = 64 * WN;
-  static constexpr int kABytes = BM * BK * 2;            // BM rows x 64 B
-  static constexpr int kBBytes = BK * BN * 2;            // 32 rows x 2*BN B
+  static constexpr int kRowBytes = BK * 2;               // bytes of an A row in a stage
+  static constexpr int kChunks = BK / 8;                 // 16-byte chunks of an A row in a stage
+  static constexpr int kABytes = BM * BK * 2;
+  static constexpr int kBBytes = BK * BN * 2;
   static constexpr int kStageBytes = kABytes + kBBytes;
   static constexpr int kDmaA = kABytes / 4096;           // buffer_load ... lds per wave per stage
   static constexpr int kDmaB = kBBytes / 4096;
   static constexpr int kDma = kDmaA + kDmaB;
+  static constexpr int kARowsPerKB = 1024 / kRowBytes;   // A rows per DMA instruction
   static constexpr int kMfma = WM * WN;                  // MFMAs per wave per 16-wide K slice
   static constexpr int kPieces = WM + 2 * WN;            // LDS reads per wave per K slice
   static constexpr int kBRowsPerKB = 512 / BN;           // B rows per DMA instruction
   static constexpr int kBSlots = BN / 8;                 // 16-byte chunks per B row
+  static_assert(NS * kStageBytes <= 160 * 1024, "the ring fits the LDS");
+  static_assert(DIST <= NS && DIST >= 2, "the DMA refills a slot no wave reads any more");
 };
+// A row m keeps chunk c in slot c ^ swz: 4 chunks (BK 32) rotate by (m >> 2) & 3, 8 chunks (BK 64)
+// by (m >> 1) & 7; either way the 16 rows a 16-lane phase reads land in 16 distinct bank groups.
+template <int BKT>
+__device__ __forceinline__ int a_swz(int m) { return BKT == 64 ? (m >> 1) & 7 : (m >> 2) & 3; }
 
 // Grouped mode (the MoE grouped GEMM): program p of the launch multiplies group g = grp[p]'s
 // rows [gstart[g], gstart[g] + grows[g]) of A by weight g of B (row-major K x N at B + g*sbg) into
@@ -77,6 +91,7 @@ struct Groups {
   int64_t sbg;
 };
 constexpr int kMaxPrograms = 256;
+constexpr int kMaxDedupGroups = 1024;   // group tables up to this size have repeated programs skipped
 
 // Split-K mode: workgroup (tile, blockIdx.y = s) multiplies K columns [s*kchunk, s*kchunk + kchunk)
 // and stores its fp32 partial tile at part + s*M*N; splitk_finish sums the partials.
@@ -87,14 +102,15 @@ constexpr int kMaxPrograms = 256;
 // bf16(silu(bf16(gate)) * bf16(up)), as a separate silu_mul would compute it from the bf16 GEMM.
 enum { kPlain = 0, kGrouped = 1, kSplit = 2, kSwiGLU = 3 };
 
-template <int WM, int WN, bool RESID, int MODE>
+template <int WM, int WN, bool RESID, int MODE, int BKT = 32>
 __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A_in, const uint16_t* __restrict__ B_in, const uint16_t* __restrict__ R,
     uint16_t* __restrict__ C_in, int M_in, int N, int K, int tiles_m, int tiles_n, Groups gp,
     float* __restrict__ part, int kchunk) {
-  using Sh = Shape<WM, WN>;
+  using Sh = Shape<WM, WN, BKT>;
   constexpr int BM = Sh::BM, BN = Sh::BN, kABytes = Sh::kABytes, kStageBytes = Sh::kStageBytes;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStageBytes];
+  constexpr int BK = Sh::BK, NS = Sh::NS, DIST = Sh::DIST;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStageBytes];
 
   // ---- tile selection
   const uint16_t* A = A_in;
@@ -105,14 +121,22 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   if constexpr (MODE == kGrouped) {
     __shared__ int pref[kMaxPrograms + 1];
     __shared__ int wsum[kThreads / 64];
+    __shared__ int first_prog[kMaxDedupGroups];   // the first program listing each group
     const int t = threadIdx.x, l = t & 63, w = t >> 6;
+    const bool dedup = gp.ntab <= kMaxDedupGroups;
+    if (dedup)
+      for (int i = t; i < gp.ntab; i += kThreads) first_prog[i] = kMaxPrograms;
+    __syncthreads();
+    const int gt = t < gp.nprog ? gp.grp[t] : -1;
+    const bool in_table = gt >= 0 && gt < gp.ntab;
+    if (dedup && in_table) atomicMin(&first_prog[gt], t);
+    __syncthreads();
+    // a program repeating an earlier program's group writes the same rows with the same values:
+    // it takes no tiles, so repeats cannot push later programs' tiles past the grid
     int cnt = 0;
-    if (t < gp.nprog) {
-      const int g = gp.grp[t];
-      if (g >= 0 && g < gp.ntab) {
-        const int s0 = gp.gstart[g], nr = gp.grows[g];
-        if (nr > 0 && s0 >= 0 && int64_t(s0) + nr <= gp.a_rows && g < gp.nweights) cnt = (nr + BM - 1) / BM;
-      }
+    if (in_table && (!dedup || first_prog[gt] == t)) {
+      const int s0 = gp.gstart[gt], nr = gp.grows[gt];
+      if (nr > 0 && s0 >= 0 && int64_t(s0) + nr <= gp.a_rows && gt < gp.nweights) cnt = (nr + BM - 1) / BM;
     }
     int v = cnt;   // inclusive scan over the 256 programs: within waves, then across the 4 waves
 #pragma unroll
@@ -171,13 +195,14 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   const int koff = MODE == kSplit ? int(blockIdx.y) * kchunk : 0;   // this split's first K column
   const i32x4 rsrc_a = make_rsrc(A + int64_t(m0) * K, uint32_t(int64_t(min(BM, M - m0)) * K - koff) * 2u);
   const i32x4 rsrc_b = make_rsrc(B + n0, uint32_t((int64_t(K - koff) * N - n0) * 2));
-  // A: instruction t of this wave covers rows 16*(kDmaA*wave + t) .. +16; lane -> row l/4, slot l%4
+  // A: instruction t of this wave covers rows kARowsPerKB*(kDmaA*wave + t) + lane/kChunks; lane ->
+  //    slot lane%kChunks, holding chunk slot ^ a_swz(row)
   // B: instruction t covers rows kBRowsPerKB*(kDmaB*wave + t) + lane/kBSlots; lane -> slot lane%kBSlots
   uint32_t a_voff[Sh::kDmaA], b_voff[Sh::kDmaB];
 #pragma unroll
   for (int t = 0; t < Sh::kDmaA; ++t) {
-    const int row = (wave * Sh::kDmaA + t) * 16 + (lane >> 2);
-    const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+    const int row = (wave * Sh::kDmaA + t) * Sh::kARowsPerKB + lane / Sh::kChunks;
+    const int chunk = (lane % Sh::kChunks) ^ a_swz<BKT>(row);
     a_voff[t] = uint32_t(row * K + chunk * 8) * 2u;
   }
 #pragma unroll
@@ -194,7 +219,7 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
   // t-th of this wave's DMA instructions of stage kt (A first, then B)
   auto dma_one = [&](int kt, int t) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + uint32_t(kt % kStages) * kStageBytes;
+    const uint32_t st = lds0 + uint32_t(kt % NS) * kStageBytes;
     if (t < Sh::kDmaA)
       dma16(rsrc_a, __builtin_amdgcn_readfirstlane(st + (wave * Sh::kDmaA + t) * 1024), a_voff[t],
             uint32_t(kt * BK) * 2u);
@@ -213,13 +238,13 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
 
   // ---- fragment addressing
   const int fr = lane & 31, h = lane >> 5;
-  // A: row m (this lane's), chunk 2*ks + h, swizzled by (m >> 2) & 3
+  // A: row m (this lane's), chunk 2*ks + h, swizzled by a_swz(m)
   int a_row_off[WM], a_sw[WM];
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
     const int m = wm * (BM / 2) + i * 32 + fr;
-    a_row_off[i] = m * 64;
-    a_sw[i] = (m >> 2) & 3;
+    a_row_off[i] = m * Sh::kRowBytes;
+    a_sw[i] = a_swz<BKT>(m);
   }
   // B (transposing reads): group g = lane/16 -> k half g/2, column half 16*(g%2); in-group lane
   // 4*jj + q supplies row 8h + 4r + jj (+16 ks), columns +4q..+4q+3
@@ -258,51 +283,55 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
   };
 
-  // The DMA stream runs kStages-1 stages ahead of the MFMAs and does not stop at the last K step:
+  // The DMA stream runs DIST stages ahead of the MFMAs and does not stop at the last K step:
   // stages past the end read zeros (num_records) into slots nobody reads any more, which keeps the
   // loop free of branches; everything is drained before the epilogue.
-  constexpr int U = Sh::kMfma, P = Sh::kPieces, D = Sh::kDma;
+  constexpr int U = Sh::kMfma, P = Sh::kPieces, D = Sh::kDma, SPS = Sh::SPS;
   constexpr bool kOneReadPerMfma = P <= U;
   constexpr bool kStaggered = D <= U && P + 1 <= U;
   const int nk = Kl / BK;
-  for (int s = 0; s < kStages - 1; ++s)
+  for (int s = 0; s < DIST; ++s)
 #pragma unroll
     for (int t = 0; t < D; ++t) dma_one(s, t);
-  wait_vmcnt<(kStages - 2) * D>();  // stage 0 landed (this wave's part)
+  wait_vmcnt<(DIST - 1) * D>();     // stage 0 landed (this wave's part)
   __syncthreads();                  // ... and everyone's
-  Slice s0, s1;
+  Slice sl[2];
 #pragma unroll
-  for (int p = 0; p < P; ++p) read_piece(smem, 0, p, s0);
+  for (int p = 0; p < P; ++p) read_piece(smem, 0, p, sl[0]);
 
-  // Each K step: slice 0's MFMAs with slice 1's reads folded in; the barrier publishing stage kt+1;
-  // slice 1's MFMAs with the DMA of stage kt+3 and the reads of stage kt+1's slice 0 folded in.
-  // sched_barrier(0) pins that interleave, so the matrix core is fed between memory instructions.
+  // Each K step: slices 0 .. SPS-2, each with the next slice's reads folded in; the barrier that
+  // publishes stage kt+1 (and frees the slot DIST - NS steps back); the last slice with the DMA of
+  // stage kt+DIST and the reads of stage kt+1's slice 0 folded in.  sched_barrier(0) pins that
+  // interleave, so the matrix core is fed between memory instructions.
   for (int kt = 0; kt < nk; ++kt) {
-    const uint8_t* st = smem + (kt % kStages) * kStageBytes;
+    const uint8_t* st = smem + (kt % NS) * kStageBytes;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      mfma_one(s0, u);
+    for (int q = 0; q + 1 < SPS; ++q) {
 #pragma unroll
-      for (int p = 0; p < P; ++p)
-        if (kOneReadPerMfma ? p == u : (p >= u * P / U && p < (u + 1) * P / U)) read_piece(st, 1, p, s1);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int u = 0; u < U; ++u) {
+        mfma_one(sl[q & 1], u);
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          if (kOneReadPerMfma ? p == u : (p >= u * P / U && p < (u + 1) * P / U)) read_piece(st, q + 1, p, sl[(q + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    // stage kt+1 landed; past this barrier no wave reads stage kt-1's slot, which takes kt+3
-    wait_vmcnt<(kStages - 3) * D>();
+    // stage kt+1 landed; past this barrier no wave reads stage kt (nor, for DIST < NS, stage kt-1)
+    wait_vmcnt<(DIST - 2) * D>();
     __syncthreads();
-    const uint8_t* nst = smem + ((kt + 1) % kStages) * kStageBytes;
+    const uint8_t* nst = smem + ((kt + 1) % NS) * kStageBytes;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      mfma_one(s1, u);
+      mfma_one(sl[(SPS - 1) & 1], u);
       if constexpr (kStaggered) {   // DMA t after MFMA t, read p after MFMA p+1
-        if (u < D) dma_one(kt + kStages - 1, u);
-        if (u >= 1 && u <= P) read_piece(nst, 0, u - 1, s0);
+        if (u < D) dma_one(kt + DIST, u);
+        if (u >= 1 && u <= P) read_piece(nst, 0, u - 1, sl[0]);
       } else {                      // the DMAs and reads spread evenly over the MFMAs
 #pragma unroll
         for (int o = 0; o < D + P; ++o)
           if (o >= u * (D + P) / U && o < (u + 1) * (D + P) / U) {
-            if (o < D) dma_one(kt + kStages - 1, o);
-            else read_piece(nst, 0, o - D, s0);
+            if (o < D) dma_one(kt + DIST, o);
+            else read_piece(nst, 0, o - D, sl[0]);
           }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -368,20 +397,24 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   }
 }
 
+// 256x256 tiles take 64-deep stages (whole-line A requests), the smaller tiles 32-deep ones.
+template <int WM, int WN>
+constexpr int kBKOf = WM * WN == 16 ? 64 : 32;
+
 template <int WM, int WN>
 int launch_gemm(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n, int64_t k,
                 hipStream_t s) {
-  using Sh = Shape<WM, WN>;
+  using Sh = Shape<WM, WN, kBKOf<WM, WN>>;
   const int64_t tm = (m + Sh::BM - 1) / Sh::BM, tn = (n + Sh::BN - 1) / Sh::BN;
   if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
   const dim3 grid(unsigned(tm * tn)), block(kThreads);
   const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
   if (residual)
-    gemm_bf16_kernel<WM, WN, true, kPlain><<<grid, block, 0, s>>>(
+    gemm_bf16_kernel<WM, WN, true, kPlain, kBKOf<WM, WN>><<<grid, block, 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), static_cast<const uint16_t*>(residual),
         static_cast<uint16_t*>(c), int(m), int(n), int(k), int(tm), int(tn), none, nullptr, 0);
   else
-    gemm_bf16_kernel<WM, WN, false, kPlain><<<grid, block, 0, s>>>(
+    gemm_bf16_kernel<WM, WN, false, kPlain, kBKOf<WM, WN>><<<grid, block, 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, static_cast<uint16_t*>(c), int(m),
         int(n), int(k), int(tm), int(tn), none, nullptr, 0);
   return launch_status();
@@ -404,7 +437,7 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
   if (k % 64 || n % 8) return PTB_ERR_UNSUPPORTED;
   // buffer offsets are 32-bit: B and one 256-row panel of A must each stay under 4 GB
-  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || int64_t(256) * k * 2 >= (int64_t(1) << 32))
+  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(256) * k * 2 >= (int64_t(1) << 32))
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
@@ -513,7 +546,7 @@ PTB_EXPORT int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residu
   if (!a || !b || !c || !workspace) return PTB_ERR_NULL;
   if (workspace_bytes < ptb_gemm_bf16_workspace_bytes(m, n, k)) return PTB_ERR_WORKSPACE;
   const int64_t bt = wide ? 256 : 128;   // tile rows and columns
-  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || bt * k * 2 >= (int64_t(1) << 32))
+  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || bt * k * 2 >= (int64_t(1) << 32))
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || !aligned16(workspace) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
@@ -523,7 +556,7 @@ PTB_EXPORT int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residu
   float* part = static_cast<float*>(workspace);
   const dim3 grid(unsigned(tm * tn), unsigned(splits));
   if (wide)
-    gemm_bf16_kernel<4, 4, false, kSplit><<<grid, dim3(kThreads), 0, s>>>(
+    gemm_bf16_kernel<4, 4, false, kSplit, 64><<<grid, dim3(kThreads), 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, nullptr, int(m), int(n), int(k),
         int(tm), int(tn), none, part, kchunk);
   else
@@ -544,13 +577,14 @@ PTB_EXPORT int ptb_gemm_swiglu_bf16(const void* a, const void* b, void* c, int64
   if (k == 0 || k % 64 || inter % 128) return PTB_ERR_UNSUPPORTED;
   const int64_t n = 2 * inter;
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
-  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || int64_t(256) * k * 2 >= (int64_t(1) << 32))
+  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(256) * k * 2 >= (int64_t(1) << 32))
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c)) return PTB_ERR_ALIGN;
   const int64_t tm = (m + 255) / 256, tn = inter / 128;
   if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
   const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
-  gemm_bf16_kernel<4, 4, false, kSwiGLU><<<dim3(unsigned(tm * tn)), dim3(kThreads), 0, static_cast<hipStream_t>(stream)>>>(
+  gemm_bf16_kernel<4, 4, false, kSwiGLU, 64><<<dim3(unsigned(tm * tn)), dim3(kThreads), 0,
+                                              static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, static_cast<uint16_t*>(c), int(m),
       int(n), int(k), int(tm), int(tn), none, nullptr, 0);
   return launch_status();
@@ -564,7 +598,7 @@ PTB_EXPORT int ptb_grouped_gemm_bf16(const void* a, const void* b, const int32_t
   if (!a || !b || !group || !start || !rows || !c) return PTB_ERR_NULL;
   if (k == 0 || k % 64 || n % 8 || nprog > kMaxPrograms) return PTB_ERR_UNSUPPORTED;
   if (weight_stride < k * n || a_rows > 0x7fffffff || ntab > 0x7fffffff || nweights > 0x7fffffff) return PTB_ERR_SHAPE;
-  if ((k + kStages * BK) * n * 2 >= (int64_t(1) << 32) || int64_t(128) * k * 2 >= (int64_t(1) << 32))
+  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(128) * k * 2 >= (int64_t(1) << 32))
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (weight_stride % 8)) return PTB_ERR_ALIGN;
   // a bound on the row tiles of every program together: each program's rows lie inside A

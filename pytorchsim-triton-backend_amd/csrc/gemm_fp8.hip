@@ -214,7 +214,49 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         store4(i, j, g, f32x4v{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]});
 }
 
-// ---- per-row activation quantiser: one wave per row for rows up to 64*8*VPT elements
+// ---- per-row activation quantiser
+// Eight bf16 values of a row (one 128-bit chunk) to e4m3 with the row's scale s.  Exact form: the
+// IEEE quotient x / s, then the bit-arithmetic RNE cast.  Fast form (rows whose absmax lies in
+// [2^-100, FLT_MAX], so that s and r = 1 / s are normal fp32): the quotient as
+// q0 = x * r, q = q0 + (x - q0 * s) * r (two FMAs) with x's sign, then v_cvt_pk_fp8_f32 (gfx950: OCP
+// e4m3fn, round to nearest even).  On MI355X the fast form gives the exact form's byte for every bf16
+// x with |x| <= amax and every bf16 amax in that range (2^31 pairs checked on the device), and the
+// conversion instruction equals the bit-arithmetic cast for every fp32 input, NaN and infinity
+// included; the exact form stays for rows outside the range.
+__device__ __forceinline__ u32x2 quant8_exact(const u32x4& v, float s) {
+  uint32_t o[2] = {0u, 0u};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t b0 = f32_to_e4m3(bf16_lo(v[q]) / s), b1 = f32_to_e4m3(bf16_hi(v[q]) / s);
+    o[q >> 1] |= (b0 | (b1 << 8)) << (16 * (q & 1));
+  }
+  return u32x2{o[0], o[1]};
+}
+__device__ __forceinline__ float quot(float x, float s, float r) {
+  const float q0 = x * r;
+  return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, s, x), r, q0), x);
+}
+__device__ __forceinline__ u32x2 quant8_fast(const u32x4& v, float s, float r) {
+  uint32_t o[2];
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const uint32_t lo = v[2 * w], hi = v[2 * w + 1];
+    int p = __builtin_amdgcn_cvt_pk_fp8_f32(quot(bf16_lo(lo), s, r), quot(bf16_hi(lo), s, r), 0, false);
+    p = __builtin_amdgcn_cvt_pk_fp8_f32(quot(bf16_lo(hi), s, r), quot(bf16_hi(hi), s, r), p, true);
+    o[w] = uint32_t(p);
+  }
+  return u32x2{o[0], o[1]};
+}
+__device__ __forceinline__ bool quant_fast_row(float amax) { return amax >= 0x1p-100f && amax <= 3.402823466e38f; }
+// Non-zero when either bf16 of the word is a NaN (magnitude above 0x7f80 carries into its top bit).
+__device__ __forceinline__ uint32_t nan_pair(uint32_t w) { return ((w & 0x7fff7fffu) + 0x007f007fu) & 0x80008000u; }
+// The row's scale as torch computes it: absmax / 448, 1 for an all-zero row, and 1 for a row holding a
+// NaN (its absmax is NaN, and NaN > 0 is false).
+__device__ __forceinline__ float quant_scale(float amax, bool has_nan) {
+  return (!has_nan && amax > 0.f) ? amax / 448.0f : 1.0f;
+}
+
+// One wave per row for rows up to 64*8*VPT elements, the row held in registers.
 constexpr int kQBlock = 256;
 template <int VPT>
 __global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ xq,
@@ -226,28 +268,35 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const uint16_t* __r
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * int64_t(cols));
   u32x4 v[VPT];
   float amax = 0.f;
+  uint32_t nan = 0u;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = l + i * kWave;
     v[i] = c < chunks ? xr[c] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(v[i][q])), fabsf(bf16_hi(v[i][q]))));
+    for (int q = 0; q < 4; ++q) {
+      amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(v[i][q])), fabsf(bf16_hi(v[i][q]))));
+      nan |= nan_pair(v[i][q]);
+    }
   }
   amax = wave_absmax(amax);
-  const float s = amax > 0.f ? amax / 448.0f : 1.0f;
+  const bool has_nan = __ballot(nan != 0u) != 0ull;
+  const float s = quant_scale(amax, has_nan);
   if (l == 0) scale[row] = s;
-  uint2* qr = reinterpret_cast<uint2*>(xq + row * int64_t(cols));
+  u32x2* qr = reinterpret_cast<u32x2*>(xq + row * int64_t(cols));
+  if (!has_nan && quant_fast_row(amax)) {   // uniform over the wave
+    const float r = 1.0f / s;
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int c = l + i * kWave;
-    if (c >= chunks) continue;
-    uint32_t o[2] = {0u, 0u};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t b0 = f32_to_e4m3(bf16_lo(v[i][q]) / s), b1 = f32_to_e4m3(bf16_hi(v[i][q]) / s);
-      o[q >> 1] |= (b0 | (b1 << 8)) << (16 * (q & 1));
+    for (int i = 0; i < VPT; ++i) {
+      const int c = l + i * kWave;
+      if (c < chunks) qr[c] = quant8_fast(v[i], s, r);
     }
-    qr[c] = make_uint2(o[0], o[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int c = l + i * kWave;
+      if (c < chunks) qr[c] = quant8_exact(v[i], s);
+    }
   }
 }
 
@@ -256,36 +305,48 @@ template <int VPT>
 __global__ __launch_bounds__(kQBlock) void quant_rows_block(const uint16_t* __restrict__ x, uint8_t* __restrict__ xq,
                                                             float* __restrict__ scale, int cols) {
   __shared__ float red[kQBlock / kWave];
+  __shared__ int red_nan[kQBlock / kWave];
   const int64_t row = blockIdx.x;
   const int chunks = cols >> 3;
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * int64_t(cols));
   u32x4 v[VPT];
   float amax = 0.f;
+  uint32_t nan = 0u;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = threadIdx.x + i * kQBlock;
     v[i] = c < chunks ? xr[c] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(v[i][q])), fabsf(bf16_hi(v[i][q]))));
+    for (int q = 0; q < 4; ++q) {
+      amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(v[i][q])), fabsf(bf16_hi(v[i][q]))));
+      nan |= nan_pair(v[i][q]);
+    }
   }
   amax = wave_absmax(amax);
-  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = amax;
+  const bool wave_nan = __ballot(nan != 0u) != 0ull;
+  if (threadIdx.x % kWave == 0) {
+    red[threadIdx.x / kWave] = amax;
+    red_nan[threadIdx.x / kWave] = wave_nan;
+  }
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float s = amax > 0.f ? amax / 448.0f : 1.0f;
+  const bool has_nan = (red_nan[0] | red_nan[1] | red_nan[2] | red_nan[3]) != 0;
+  const float s = quant_scale(amax, has_nan);
   if (threadIdx.x == 0) scale[row] = s;
-  uint2* qr = reinterpret_cast<uint2*>(xq + row * int64_t(cols));
+  u32x2* qr = reinterpret_cast<u32x2*>(xq + row * int64_t(cols));
+  if (!has_nan && quant_fast_row(amax)) {   // uniform over the block
+    const float r = 1.0f / s;
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int c = threadIdx.x + i * kQBlock;
-    if (c >= chunks) continue;
-    uint32_t o[2] = {0u, 0u};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t b0 = f32_to_e4m3(bf16_lo(v[i][q]) / s), b1 = f32_to_e4m3(bf16_hi(v[i][q]) / s);
-      o[q >> 1] |= (b0 | (b1 << 8)) << (16 * (q & 1));
+    for (int i = 0; i < VPT; ++i) {
+      const int c = threadIdx.x + i * kQBlock;
+      if (c < chunks) qr[c] = quant8_fast(v[i], s, r);
     }
-    qr[c] = make_uint2(o[0], o[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int c = threadIdx.x + i * kQBlock;
+      if (c < chunks) qr[c] = quant8_exact(v[i], s);
+    }
   }
 }
 

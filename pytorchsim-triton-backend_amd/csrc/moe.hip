@@ -464,31 +464,47 @@ __global__ __launch_bounds__(kB) void sort_emit(const int64_t* __restrict__ sk, 
 }
 
 // ---------------------------------------------------------------- top-k
-// One wave per row, the row in LDS: element c's rank is the number of elements ordered before it
-// (larger -- smaller for largest = false -- or equal at a lower position); the elements of rank < k
-// are the k selected, in order.  This is the order the reference's k rounds of "take the best,
-// lowest position first, mark it spent" produce.
+// Order of the elements (both kernels): value, larger first (smaller first for largest = false),
+// equal values by lower position; a NaN ranks after every number (for either direction) and NaNs
+// among themselves by position.  This is the order the reference's k rounds of "take the best, lowest
+// position first, mark it spent" give rows without NaN; for NaN, which the reference's comparisons
+// leave to the backend, it fixes one deterministic order (the 32-bit key below).
+// order-preserving bits of a float: larger value, larger unsigned key
+__device__ __forceinline__ uint32_t order_bits(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+// The key of element v of a row searched for its largest (v already negated for smallest-k): a NaN
+// gets 1, below every number's key and above 0 (taken or absent elements); -0 and +0 share a key, as
+// they compare equal.
+__device__ __forceinline__ uint32_t topk_key(float v) {
+  return v != v ? 1u : (v == 0.f ? 0x80000000u : order_bits(v));
+}
+
+// One wave per row, the keys in LDS: element c's rank is the number of elements ordered before it
+// (a larger key, or an equal key at a lower position); the elements of rank < k are the k selected,
+// in order.
 constexpr int kTopkMax = 1024;   // row length
 constexpr int kTopkRows = kB / kWave;
 __global__ __launch_bounds__(kB) void topk_rows(const float* __restrict__ x, int64_t rows, int e, int k, bool largest,
                                                 float* __restrict__ vals, int64_t* __restrict__ idx) {
-  __shared__ __attribute__((aligned(16))) float sx[kTopkRows][kTopkMax];
+  __shared__ __attribute__((aligned(16))) uint32_t sk[kTopkRows][kTopkMax];
   const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int64_t row = int64_t(blockIdx.x) * kTopkRows + w;
   if (row >= rows) return;   // a whole wave; no block barrier below
-  float* r = sx[w];
+  uint32_t* r = sk[w];
   // smallest-k is largest-k of the negated values (negation reverses the order, keeps ties)
   const float sgn = largest ? 1.0f : -1.0f;
-  const int e4 = (e + 3) & ~3;   // padded with -inf, which never ranks before a real element
-  for (int c = lane; c < e4; c += kWave) r[c] = c < e ? sgn * x[row * e + c] : -INFINITY;
+  const int e4 = (e + 3) & ~3;   // padded with key 0, which never ranks before a real element
+  for (int c = lane; c < e4; c += kWave) r[c] = c < e ? topk_key(sgn * x[row * e + c]) : 0u;
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  const f32x4v* r4 = reinterpret_cast<const f32x4v*>(r);
+  const u32x4* r4 = reinterpret_cast<const u32x4*>(r);
   for (int c = lane; c < e; c += kWave) {
-    const float v = r[c];
+    const uint32_t v = r[c];
     int rank = 0;
 #pragma unroll 8
     for (int q = 0; q < e4 / 4; ++q) {
-      const f32x4v o = r4[q];
+      const u32x4 o = r4[q];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int j = 4 * q + t;
@@ -496,7 +512,7 @@ __global__ __launch_bounds__(kB) void topk_rows(const float* __restrict__ x, int
       }
     }
     if (rank < k) {
-      vals[row * k + rank] = sgn * v;
+      vals[row * k + rank] = x[row * e + c];
       idx[row * k + rank] = c;
     }
   }
@@ -504,17 +520,10 @@ __global__ __launch_bounds__(kB) void topk_rows(const float* __restrict__ x, int
 
 // Top-k with k <= 64 of rows of at most 64*R elements: one wave per row with the row in registers
 // (lane l holds elements l, l + 64, ...), every load in flight at once, then k rounds of a wave
-// argmax over the elements not yet taken.  The 64-bit key (order-preserving bits of the value,
-// then the inverted position) makes a round's winner the largest value and, among equal values,
-// the lowest position: the same selection and order as the rank kernel above.  Taken and absent
-// elements hold key 0, below every present one.
-__device__ __forceinline__ uint32_t order_bits(float v) {
-  const uint32_t u = __float_as_uint(v);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float from_order_bits(uint32_t o) {
-  return __uint_as_float((o & 0x80000000u) ? (o ^ 0x80000000u) : ~o);
-}
+// argmax over the elements not yet taken.  The 64-bit key (topk_key of the value, then the inverted
+// position) makes a round's winner the largest value and, among equal values, the lowest position:
+// the same selection and order as the rank kernel above.  Taken and absent elements hold key 0,
+// below every present one.
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xf, 0xf, false));
@@ -557,7 +566,7 @@ __global__ __launch_bounds__(kB) void topk_rows_wave(const float* __restrict__ x
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const bool in = lane + kWave * r < e;
-    kh[r] = in ? order_bits(sgn * raw[r]) : 0u;
+    kh[r] = in ? topk_key(sgn * raw[r]) : 0u;
     kl[r] = in ? ~uint32_t(lane + kWave * r) : 0u;
   }
   float outv = 0.f;
@@ -568,6 +577,10 @@ __global__ __launch_bounds__(kB) void topk_rows_wave(const float* __restrict__ x
     for (int r = 1; r < R; ++r) key_max(bh, bl, kh[r], kl[r]);
     wave_key_max(bh, bl);
     const int pos = int(~bl);
+    float mine = raw[0];   // the element at position pos, from the lane that holds it
+#pragma unroll
+    for (int r = 1; r < R; ++r) mine = pos / kWave == r ? raw[r] : mine;
+    const float won = __shfl(mine, pos % kWave, kWave);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const bool taken = lane + kWave * r == pos;
@@ -575,7 +588,7 @@ __global__ __launch_bounds__(kB) void topk_rows_wave(const float* __restrict__ x
       kl[r] = taken ? 0u : kl[r];
     }
     if (lane == n) {
-      outv = sgn * from_order_bits(bh);
+      outv = won;
       outi = pos;
     }
   }

@@ -193,3 +193,31 @@ def test_gemm_swiglu_refusals():
         ops.gemm_swiglu(a, b)
 
 
+
+
+def test_quant_rows_extreme_rows_exact():
+    """Rows across the scale range, bit-exact with the oracle's torch cast: a tiny row (absmax below
+    2^-100, the exact-division path), rows near that bound, a huge one, -0 and bf16 subnormals, a row
+    holding a NaN (torch's absmax is NaN, so the scale is 1), infinities, and ordinary rows; wave-per-row
+    (256 columns) and block-per-row (12288 columns) kernels."""
+    for cols in (256, 12288):
+        x = randn((12, cols), 70 + cols)
+        x[0] *= 1e-33                         # absmax ~ 4e-33: below 2^-100 (7.9e-31)
+        x[1] *= 2.0 ** -100                   # around the bound
+        x[2] *= 1e37                          # huge but finite
+        x[3, :] = -0.0
+        x[3, 1] = 1.0
+        x[4, ::2] = torch.tensor(1e-40, dtype=torch.bfloat16)   # subnormal bf16 beside normal values
+        x[5, 7] = float("nan")
+        x[6, 3] = float("inf")
+        x[7, 5] = float("-inf")
+        xq, sc = ops.quant_rows_e4m3(x.to(DEV))
+        wq, wsc = oracle.quant_rows_e4m3(x)
+        assert bits_equal(sc.cpu(), wsc), f"scales differ at {cols} columns"
+        got, want = xq.cpu().view(torch.uint8), wq.view(torch.uint8)
+        # inf / inf (the infinite rows) is a NaN whose sign is the platform's (x86 makes it negative,
+        # the GPU positive): NaN bytes compare as NaN, every other byte bit for bit
+        nan_w = (want & 0x7F) == 0x7F
+        assert torch.equal((got & 0x7F) == 0x7F, nan_w), f"NaN positions differ at {cols} columns"
+        assert torch.equal(got[~nan_w], want[~nan_w]), f"quantised bytes differ at {cols} columns"
+        assert torch.equal(got[:6], want[:6]), f"finite rows differ at {cols} columns"

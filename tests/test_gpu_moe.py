@@ -105,6 +105,33 @@ def test_topk_rows(rows, e, k, largest):
     assert torch.equal(v.cpu(), wv) and torch.equal(i.cpu(), wi)
 
 
+@pytest.mark.parametrize("e,k", [(64, 8), (100, 40), (300, 65), (1000, 100)])
+@pytest.mark.parametrize("largest", [True, False])
+def test_topk_rows_nan_and_signed_zero(e, k, largest):
+    """Rows holding NaNs (of either sign) and both zeros: both kernels (k <= 64 in registers, k > 64
+    through the LDS ranks) take the numbers first in value order, equal values (-0 == +0 included) by
+    lower position, then the NaNs by position -- the oracle's order -- and return the elements' own
+    values."""
+    rows = 6
+    x = torch.randn(rows * e, generator=gen(e + k)).view(rows, e)
+    x[0, 5] = float("nan")
+    x[0, 2] = -float("nan")
+    x[1, :] = float("nan")                       # all NaN: positions in order
+    x[2, 7], x[2, 3], x[2, 11] = 0.0, -0.0, 0.0
+    x[3, ::3] = float("nan")
+    x[4, :] = 0.0
+    x[4, 1::2] = -0.0
+    x = x.reshape(-1)
+    v, i = torch.empty(rows * k, device=DEV), torch.empty(rows * k, dtype=I64, device=DEV)
+    moe.topk_rows(x.to(DEV), v, i, e, k, largest)
+    wv, wi = oracle.topk_rows(x, e, k, largest)
+    assert torch.equal(i.cpu(), wi)
+    got, want = v.cpu(), wv
+    both_nan = torch.isnan(got) & torch.isnan(want)
+    assert torch.equal(torch.isnan(got), torch.isnan(want))
+    assert torch.equal(got[~both_nan].view(torch.int32), want[~both_nan].view(torch.int32))   # -0 stays -0
+
+
 @pytest.mark.parametrize("t,k,c", [(1024, 8, 2048), (1, 8, 2048), (37, 3, 64)])
 def test_gather_rows(t, k, c):
     r = t * k
@@ -310,3 +337,21 @@ def test_moe_layer_chain_matches_the_oracle():
     want = oracle.combine(ti_o, ends_o, counts_o, rank_o, y_o, tv_o, t, k, c, wsum=wsum_o, h=h,
                           io=torch.zeros(t * c, dtype=BF16))
     close_scaled(got, want, "moe layer chain")
+
+
+def test_grouped_gemm_repeated_groups_fill_the_grid():
+    """The MFMA form with large groups listed by several programs: repeats take no tiles, so the
+    later programs' rows are still computed (without that, 3 programs over 2 groups of 512 rows
+    need 12 row tiles where the grid has ceil(1024 / 128) + 3 = 11)."""
+    k_dim, n, a_rows = 256, 512, 1024
+    a = (torch.randn(a_rows * k_dim, generator=gen(30)) / 8).to(BF16)
+    b = (torch.randn(2 * k_dim * n, generator=gen(31)) / 16).to(BF16)
+    group = torch.tensor([0, 0, 1, 0], dtype=I32)
+    starts = torch.tensor([0, 512], dtype=I32)
+    rows = torch.tensor([512, 512], dtype=I32)
+    c0 = torch.randn(a_rows * n, generator=gen(32)).to(BF16)
+    c = c0.to(DEV)
+    moe.grouped_gemm(a.to(DEV), b.to(DEV), group.to(DEV), starts.to(DEV), rows.to(DEV), c, k_dim, n, k_dim * n,
+                     gemv=False)
+    want = oracle.grouped_mm(a, b, group, starts, rows, k_dim, n, k_dim * n, c=c0)
+    close_scaled(c.cpu(), want, "grouped gemm, repeated groups")
