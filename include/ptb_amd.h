@@ -9,7 +9,9 @@
  * grid: every entry point below takes caller-owned device pointers (bf16 carried as uint16 bits,
  * fp8 e4m3fn as uint8 bits, as contract/kernel_object.py:43-56 carries them), sizes, and a
  * hipStream_t passed as void* (NULL = the null stream).  Launches are asynchronous on that stream,
- * nothing is allocated, and there is no global mutable state, so entry points are thread-safe.
+ * nothing is allocated, and there is no global mutable state, so entry points are thread-safe --
+ * except ptb_attn_decode_bf16_noalloc, whose static per-device scratch is shared by every call on
+ * a GPU (see there).
  *
  * An entry point whose output is empty returns 0 without looking at its pointers.
  * Return value: 0 on success; a negative PTB_ERR_* for an argument the library refuses before
@@ -252,6 +254,17 @@ size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, int64_t seq);
 int ptb_attn_decode_bf16(const void* q, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
                          int64_t seq, int64_t head_dim, float scale, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* Allocation-free decode attention: ptb_attn_decode_bf16 with its partial records in a static device
+ * scratch of ptb_attn_decode_noalloc_max_bytes() bytes (16 MiB) instead of a caller workspace; no
+ * allocation of any kind.  No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, serving loops that forbid hipMalloc).  A shape whose workspace
+ * (ptb_attn_decode_workspace_bytes) exceeds the scratch is refused with PTB_ERR_WORKSPACE.  Each GPU
+ * holds its own scratch until the process ends, its address looked up on the first call on that
+ * device; calls that overlap on one GPU share it and race. */
+size_t ptb_attn_decode_noalloc_max_bytes(void);
+int ptb_attn_decode_bf16_noalloc(const void* q, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
+                                 int64_t seq, int64_t head_dim, float scale, void* stream);
 
 /* Decode attention with the query's per-head RMSNorm and rotate-half RoPE done in its prologue:
  * q is the q projection's raw output [nkv, group, 128]; each workgroup normalizes (qnorm_w [128]

@@ -20,6 +20,8 @@
 //   pass 2: workgroup (row group, query row): o = sum acc_r 2^(m_r-M) / sum l_r 2^(m_r-M), M = max m_r.
 #include <cmath>
 
+#include <mutex>
+
 #include "ptb_common.h"
 
 using namespace ptb;
@@ -857,6 +859,54 @@ PTB_EXPORT int ptb_attn_decode_qnorm_rope_bf16(const void* q, const void* qnorm_
   return attn_decode_entry(q, k, v, o, nkv, group, seq, head_dim, scale,
                            QNorm{static_cast<const uint16_t*>(qnorm_w), cos_t, sin_t, eps}, workspace,
                            workspace_bytes, stream);
+}
+
+// ---- allocation-free decode attention
+// For callers that cannot allocate (code under HIP graph capture, serving loops that forbid
+// hipMalloc): the partial records live in a file-scope device array instead of a caller workspace.
+// Each GPU the library runs on holds its own copy of the array until the process ends; its address is
+// looked up once per device (hipGetSymbolAddress, with that device current) and kept.  Every call on a
+// GPU shares that GPU's array, so calls that overlap on one GPU race; nothing in it has to start at
+// zero (each record is written before the merge pass reads it).
+constexpr size_t kScratchBytes = size_t(16) << 20;   // 16 MiB: 8 kv heads x group 8 to 131072 keys
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int device_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return int(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return PTB_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return int(e);
+    if (!p) return PTB_ERR_NULL;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PTB_OK;
+}
+}  // namespace
+
+PTB_EXPORT size_t ptb_attn_decode_noalloc_max_bytes(void) { return kScratchBytes; }
+
+PTB_EXPORT int ptb_attn_decode_bf16_noalloc(const void* q, const void* k, const void* v, void* o, int64_t nkv,
+                                            int64_t group, int64_t seq, int64_t head_dim, float scale, void* stream) {
+  const size_t need = ptb_attn_decode_workspace_bytes(nkv, group, seq);
+  if (need > kScratchBytes) return PTB_ERR_WORKSPACE;   // past the static scratch's size
+  void* ws = nullptr;
+  if (need) {
+    const int st = device_scratch(&ws);
+    if (st != PTB_OK) return st;
+  }
+  return attn_decode_entry(q, k, v, o, nkv, group, seq, head_dim, scale, QNorm{nullptr, nullptr, nullptr, 0.f}, ws,
+                           need ? kScratchBytes : 0, stream);
 }
 
 PTB_EXPORT size_t ptb_grouped_gemm_workspace_bytes(int64_t nprog, int64_t a_rows, int64_t k, int64_t n) {

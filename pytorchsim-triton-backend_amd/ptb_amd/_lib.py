@@ -153,6 +153,8 @@ SIGNATURES = {
     "ptb_attn_decode_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "ptb_attn_decode_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _vp, _c_size,
                                       _vp]),
+    "ptb_attn_decode_noalloc_max_bytes": (_c_size, []),
+    "ptb_attn_decode_bf16_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _vp]),
     "ptb_attn_decode_qnorm_rope_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_f32, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64,
                                                  _c_i64, _c_f32, _vp, _c_size, _vp]),
 }
