@@ -8,8 +8,9 @@ launches over inputs resident in HBM, bracketed by torch.cuda.synchronize().  ``
 measured the same way (RMSNorm GB/s, fp8 GEMM TFLOP/s, flash-attention TFLOP/s, Qwen3-8B layer
 latency) and the single-token decode path (the decode layer's largest GEMV and the decode attention
 in GB/s, the 8-launch decode layer's latency), each with its roofline fraction, and
-``cpu_baseline`` times the CPU golden (torch-CPU, the oracle's arithmetic) on a bounded sample of
-the headline workload.
+``cpu_baseline`` times the CPU golden (the oracle, torch-CPU) on this host's cores: the headline's
+figure at top level and, under ``configs``, one entry per BASELINE config (a bounded sample of each
+workload, on all host threads and on one thread).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm_bf16,...]
 """
@@ -81,7 +82,7 @@ def bench_gemm_bf16(steps, warmup):
         "us": ms * 1e3, "wall_us": wall * 1e3, "tflops": tf,
         "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": tf / PEAK_BF16_TFLOPS},
-        "flops": flops, "_a": a, "_b": b,
+        "flops": flops,
     }
 
 
@@ -264,29 +265,103 @@ def bench_decode_layer(steps, warmup):
             "launches": 8}
 
 
-def cpu_baseline_gemm(a, b, sample_rows=256):
-    """The CPU golden for the headline workload: torch-CPU fp32 matmul of the oracle's arithmetic
-    (bf16 operands upcast, fp32 accumulation, one bf16 rounding), on `sample_rows` rows of A against
-    all of B, scaled to TFLOP/s."""
-    import torch
-
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
-    a_s = a[:sample_rows].float().cpu()
-    b_f = b.float().cpu()
-    (a_s[:8] @ b_f).to(torch.bfloat16)   # warm
+def _trial_seconds(fn, min_s: float) -> float:
+    """Seconds per call of fn over one trial: at least one call, repeated until min_s has passed."""
     t0 = time.perf_counter()
     reps = 0
     while True:
-        (a_s @ b_f).to(torch.bfloat16)
+        fn()
         reps += 1
-        if time.perf_counter() - t0 > 10.0:   # a bounded sample: about 10 s of CPU work
-            break
-    sec = (time.perf_counter() - t0) / reps
-    flops = 2.0 * sample_rows * b.shape[0] * b.shape[1]
-    return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{sample_rows} of 4096 rows of A @ full B[4096x12288], torch-CPU fp32, "
-                      f"{reps} reps, {sec * 1e3:.1f} ms each"}
+        if time.perf_counter() - t0 >= min_s:
+            return (time.perf_counter() - t0) / reps
+
+
+def _median_seconds(fn, trials: int, min_s: float) -> float:
+    ts = sorted(_trial_seconds(fn, min_s) for _ in range(trials))
+    return ts[len(ts) // 2]
+
+
+def cpu_baselines() -> list:
+    """The reference's CPU golden for each BASELINE config, timed on this host: the oracle's
+    functions (torch-CPU; GEMM and fp8 dots summed in fp64 and rounded once, as the golden
+    defines them) on a bounded sample of each workload, on all host threads (median of 3 trials, 1
+    for the layer) and on one thread (median of 3, 1 for the layer).  Throughput is the sample's
+    algorithmic work over its time, in the GPU line's unit; the layer also gives its latency."""
+    import torch
+    import oracle
+    from ptb_amd import qwen3
+
+    bf = torch.bfloat16
+    threads = len(os.sched_getaffinity(0))
+    g = torch.Generator().manual_seed(0)
+    out = []
+
+    def leg(name, unit, work, sample_all, sample_one, fn_all, fn_one, trials=3, min_s=1.0):
+        """work(sample) -> algorithmic units of one call (GB or GFLOP); fn_*() runs the sample."""
+        rec = {"config": name, "unit": unit, "cores": threads, "kind": "port"}
+        for key, n, fn, samp in (("all", threads, fn_all, sample_all), ("one", 1, fn_one, sample_one)):
+            torch.set_num_threads(n)
+            if trials > 1:
+                fn()   # warm (allocations)
+            sec = _median_seconds(fn, trials, min_s if key == "all" else 0.0)
+            rate = work(samp) / sec / (1e3 if unit == "TFLOP/s" else 1.0)
+            rec["value" if key == "all" else "value_1_thread"] = rate
+            rec["sample" if key == "all" else "sample_1_thread"] = f"{samp['what']}: {sec * 1e3:.1f} ms per call"
+        rec["trials"] = trials
+        torch.set_num_threads(threads)
+        log(f"[bench] cpu {name}: {rec['value']:.4g} {unit} on {threads} threads, "
+            f"{rec['value_1_thread']:.4g} on 1")
+        return rec
+
+    # config 1: RMSNorm, the whole workload
+    x = torch.randn(2048, 4096, generator=g).to(bf)
+    w = torch.randn(4096, generator=g) * 0.02 + 1.0
+    s1 = {"what": "the whole 2048x4096 RMSNorm", "bytes": 2 * 2048 * 4096 * 2 + 4096 * 4}
+    out.append(leg("1 rmsnorm", "GB/s", lambda s: s["bytes"] / 1e9, s1, s1,
+                   lambda: oracle.rmsnorm(x, w, 1e-6), lambda: oracle.rmsnorm(x, w, 1e-6)))
+    # config 2: bf16 GEMM, rows of A against all of B
+    a = (torch.randn(4096, 4096, generator=g) / 64).to(bf)
+    b = (torch.randn(4096, 12288, generator=g) / 64).to(bf)
+    s2a = {"what": "256 of 4096 rows of A @ B[4096x12288]", "rows": 256}
+    s2o = {"what": "32 of 4096 rows of A @ B[4096x12288]", "rows": 32}
+    out.append(leg("2 gemm_bf16", "TFLOP/s", lambda s: 2.0 * s["rows"] * 4096 * 12288 / 1e9, s2a, s2o,
+                   lambda: oracle.gemm(a[:256], b), lambda: oracle.gemm(a[:32], b)))
+    del a, b
+    # config 3: causal GQA attention, one kv head with its 4 query heads (1/8 of the heads), full S
+    q = torch.randn(4, 4096, 128, generator=g).to(bf)
+    k = torch.randn(1, 4096, 128, generator=g).to(bf)
+    v = torch.randn(1, 4096, 128, generator=g).to(bf)
+    s3 = {"what": "4 of 32 query heads (one kv head), S 4096, causal", "heads": 4}
+    att = lambda: oracle.flash_attention(q, k, v, 4, 1, True)  # noqa: E731
+    out.append(leg("3 flash_attention", "TFLOP/s", lambda s: 4.0 * s["heads"] * 128 * 4096 * 4097 / 2 / 1e9,
+                   s3, s3, att, att))
+    # config 4: per-token quantise + fp8 GEMM, rows of x against the whole packed weight
+    xs = torch.randn(64, 12288, generator=g).to(bf)
+    wq, sw = oracle.quant_weight_e4m3(torch.randn(12288, 4096, generator=g) * 0.02)
+    s4a = {"what": "quantise + e4m3 GEMM of 64 of 2048 rows against W[12288x4096]", "rows": 64}
+    s4o = {"what": "quantise + e4m3 GEMM of 16 of 2048 rows against W[12288x4096]", "rows": 16}
+
+    def fp8(rows):
+        aq, sa = oracle.quant_rows_e4m3(xs[:rows])
+        oracle.gemm_fp8(aq, sa, wq, sw)
+
+    out.append(leg("4 gemm_fp8", "TFLOP/s", lambda s: 2.0 * s["rows"] * 12288 * 4096 / 1e9, s4a, s4o,
+                   lambda: fp8(64), lambda: fp8(16)))
+    del wq, sw
+    # config 5: the layer; all threads run T = 2048, one thread the first 256 tokens (a causal
+    # layer's first rows are exactly a shorter sequence)
+    wts = qwen3.random_weights()
+    xt = torch.randn(2048, 4096, generator=torch.Generator().manual_seed(1)).to(bf)
+    cos, sin = oracle.rope_tables(2048, 128, 1.0e6)
+    lay = lambda t: oracle.qwen3_layer(xt[:t], wts, cos[:t], sin[:t], bq=min(t, 1024))  # noqa: E731
+    flops = lambda s: sum(f for _, f, _ in qwen3.layer_work(s["t"])) / 1e9  # noqa: E731
+    s5a = {"what": "the whole layer, T = S = 2048", "t": 2048}
+    s5o = {"what": "the layer over the first 256 tokens", "t": 256}
+    rec = leg("5 qwen3_8b_layer", "TFLOP/s", flops, s5a, s5o, lambda: lay(2048), lambda: lay(256),
+              trials=1, min_s=0.0)
+    rec["layer_us"] = flops(s5a) / rec["value"] * 1e3   # GFLOP / (TFLOP/s) = ms
+    out.append(rec)
+    return out
 
 
 def pmc_driver(which: str) -> None:
@@ -409,10 +484,13 @@ def main(argv=None):
 
     head = results.get("gemm_bf16") or next(iter(results.values()))
     cpu = None
-    if not args.no_cpu and "gemm_bf16" in results:
-        log("[bench] cpu baseline ...")
-        cpu = cpu_baseline_gemm(head["_a"], head["_b"])
-        log(f"[bench] cpu baseline: {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads")
+    if not args.no_cpu:
+        log("[bench] cpu baselines (the oracle on this host's cores) ...")
+        per_config = cpu_baselines()
+        c2 = next(r for r in per_config if r["config"].startswith("2 "))
+        cpu = {"value": c2["value"], "unit": c2["unit"], "cores": c2["cores"], "kind": "port",
+               "sample": c2["sample"], "value_1_thread": c2["value_1_thread"],
+               "sample_1_thread": c2["sample_1_thread"], "configs": per_config}
     kernels = []
     for r in results.values():
         kernels.append({k: v for k, v in r.items() if not k.startswith("_")})
