@@ -89,6 +89,20 @@ def test_shape_and_alignment_refused(lib):
     assert lib.ptb_reduce_bf16(P16, P16, 64, 0, P16, 4, None) == _lib.PTB_ERR_WORKSPACE
 
 
+def test_32bit_buffer_offset_limits_refused(lib):
+    """The kernels address each operand through a buffer resource with 32-bit byte offsets; shapes
+    past that range are refused before any launch (PTB_ERR_UNSUPPORTED / PTB_ERR_GRID)."""
+    # B (plus the DMA run-ahead) at or past 4 GiB: (65536 + 128) * 32768 * 2 bytes
+    assert lib.ptb_gemm_bf16(P16, P16, None, P16, 256, 32768, 65536, None) == _lib.PTB_ERR_UNSUPPORTED
+    assert lib.ptb_gemm_swiglu_bf16(P16, P16, P16, 256, 16384, 65536, None) == _lib.PTB_ERR_UNSUPPORTED
+    # one 256-row panel of A at 4 GiB: 256 * 8388608 * 2 bytes
+    assert lib.ptb_gemm_bf16(P16, P16, None, P16, 256, 8, 8388608, None) == _lib.PTB_ERR_UNSUPPORTED
+    # fp8: a 256-row panel of e4m3 A at 4 GiB
+    assert lib.ptb_gemm_fp8_scaled(P16, P16, P16, P16, P16, 256, 16, 1 << 24, None) == _lib.PTB_ERR_UNSUPPORTED
+    # attention: one kv head's K at 4 GiB (2^24 keys x 256 bytes)
+    assert lib.ptb_flash_attn_fwd_bf16(P16, P16, P16, P16, 1, 1, 1, 1 << 24, 128, 0.1, 1, None) == _lib.PTB_ERR_GRID
+
+
 def test_empty_work_is_a_no_op(lib):
     # zero rows / zero-size outputs return OK without launching
     assert lib.ptb_rmsnorm_bf16(P16, P16, 0, P16, 0, 64, 1e-6, None) == _lib.PTB_OK

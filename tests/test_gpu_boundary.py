@@ -203,19 +203,44 @@ def check_moe_against_oracle(plan, host, got):
         assert_close(got[p["c"]], want, 2e-2, 2e-2 * scale, "grouped_mm")
 
 
+def _device_args(spec, host, fill=None):
+    """The launch's device tensors: inputs (and in/out arguments) from host; pure outputs freshly
+    allocated (NaN-poisoned by the conftest allocator) or, with fill, every byte set to fill."""
+    dev = {}
+    for a in spec.args:
+        if a.name in host:
+            dev[a.name] = host[a.name].cuda()
+        else:
+            dev[a.name] = torch.empty(a.numel, dtype=getattr(torch, a.dtype), device="cuda")
+            if fill is not None:
+                dev[a.name].view(torch.uint8).fill_(fill)
+    return dev
+
+
 @pytest.mark.parametrize("workload,index", CASES)
 def test_bundle_kernel_through_launcher(workload, index):
+    """Each distinct bundle kernel against the oracle, then once more over outputs poisoned with a
+    different byte pattern: the two runs must agree byte for byte, so every output byte is written by
+    the kernel (a missed write would keep each run's own poison) and the result does not depend on
+    the order the programs ran in -- the missing / conflicting-write checks of the reference's
+    functional runtime (runtime/spike.py:310-334)."""
     man = MANIFESTS[workload]["kernels"][index]
     spec = contract.spec_from_manifest(man)
     rec = bundle.read_recorded(RECORDED, workload, man["dir"]) if man["extra"].get("recorded") else None
     host = contract.seeded_inputs(spec, torch, seed=0, recorded=rec)
     print(f"[case] {workload}/{man['dir']} {plan_family(spec)}", flush=True)
-    dev = {a.name: (host[a.name].cuda() if a.name in host
-                    else torch.empty(a.numel, dtype=getattr(torch, a.dtype), device="cuda")) for a in spec.args}
+    dev = _device_args(spec, host)
     plan = launcher.launch(spec, dev, grid=tuple(man["grid"]))
     torch.cuda.synchronize()
     got = {a.name: dev[a.name].cpu() for a in spec.outputs()}
     check_against_oracle(plan, host, got)
+    again = _device_args(spec, host, fill=0x5A)
+    launcher.launch(spec, again, grid=tuple(man["grid"]))
+    torch.cuda.synchronize()
+    for a in spec.outputs():
+        first = got[a.name].contiguous().view(torch.uint8)
+        second = again[a.name].cpu().contiguous().view(torch.uint8)
+        assert torch.equal(first, second), f"{a.name}: the two runs differ (unwritten or order-dependent bytes)"
 
 
 def test_hip_launcher_hook_takes_kernel_json():
