@@ -213,6 +213,20 @@ int ptb_flash_attn_fwd_tokens_bf16(const void* q, const void* k, const void* v, 
                                    int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale, int causal,
                                    void* stream);
 
+/* The prefill layer's attention reading the fused projection in place: qkv is [batch*seq, ld] bf16
+ * (ld >= (hq + 2*hkv)*128, ld % 8 == 0) holding each token's q (columns [0, hq*128)), k and v
+ * (columns [(hq+hkv)*128, (hq+2*hkv)*128)); k is the k-norm + RoPE output [batch*hkv, seq, 128].
+ * Each query row gets its per-head RMSNorm (qnorm_w [128] bf16, eps) and rotate-half RoPE (cos_t /
+ * sin_t [seq, 128] fp32) in the kernel's prologue, v is read with row stride ld, and o is written
+ * token-major [batch, seq, hq, 128]: bit-identical to ptb_qk_norm_rope_ld_bf16 (q) +
+ * ptb_transpose_heads_ld_bf16 (v) + ptb_flash_attn_fwd_tokens_bf16, in one launch.
+ * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/02_..._mmis7ufj_triton.py:17-98 (q-norm + RoPE),
+ *           05_..._ff5nvvqz_triton.py:17-27 (v transpose), 06__prefill_kernel and
+ *           07_..._fused_clone_select_transpose_ei42assc (O -> [T, 32, 128]). */
+int ptb_flash_attn_fwd_qkv_bf16(const void* qkv, int64_t ld, const void* k, const void* qnorm_w, const float* cos_t,
+                                const float* sin_t, float eps, void* o, int64_t batch, int64_t hq, int64_t hkv,
+                                int64_t seq, int64_t head_dim, float scale, int causal, void* stream);
+
 /* ---- single-token (decode) path: qwen3_8b_layer_decode_1x<S>_bf16 and attention_decode_* ---- */
 
 /* out[0] = sum_i (float(x[i]) + float(y[i]))^2 in fp32; y may be NULL (then sum x^2).  One workgroup.

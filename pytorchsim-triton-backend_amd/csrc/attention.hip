@@ -157,13 +157,95 @@ __device__ __forceinline__ void pv_step(WaveState& w, const bf16x8 (&pf)[2][2], 
       }
 }
 
+// The fused form's inputs (QKV = true): q and v are read in place from the [B*S, ld] output of a
+// fused q|k|v projection (query head hd of token t at row b*S + t, columns hd*128 ..; kv head j's v
+// at columns vcol + j*128 ..), and each q row gets its per-head RMSNorm (weight w, eps) and
+// rotate-half RoPE (cos/sin [S, 128] fp32) in the prologue, with the fp32 operations of
+// qk_norm_rope in the same order (the sum of squares chunk by chunk, then the same pairwise tree),
+// so the result is bit-identical to the qk_norm_rope + transpose + attention launches.
+struct QkvIn {
+  const uint16_t* w;
+  const float* cos;
+  const float* sin;
+  float eps;
+  int ld;
+  int vcol;
+};
+
+// 8 bf16 of a 16-byte word as fp32 (exact)
+__device__ __forceinline__ void unpack8(const u32x4& v, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(v[i] << 16);
+    f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+
+// One query row's 128 values as this lane holds them (chunks c = 2*kk + h, d = 8c .. 8c+7; the other
+// half of the row is in lane ^ 32), normalised and rotated, as the MFMA B fragments.
+__device__ __forceinline__ void qnorm_rope_row(const uint16_t* __restrict__ src, const QkvIn& in, int pos, int h,
+                                               uint32_t flip, bf16x8 (&qf)[8]) {
+  u32x4 raw[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) raw[kk] = *reinterpret_cast<const u32x4*>(src + kk * 16);
+  float s[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    float f[8];
+    unpack8(raw[kk], f);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+    s[kk] = ss;
+  }
+  // qk_norm_rope's 16-lane tree over chunks 0..15: (c, c^1), then (c, c^2), then the halves of 8,
+  // then of 16; chunk c^1 is the partner lane's, c^2 and up this lane's kk^1, kk^2, kk^4
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(s[kk]), __float_as_uint(s[kk]), false, false);
+    s[kk] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  const float ss = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+  const float r = 1.0f / sqrtf(ss / 128.f + in.eps);
+  const float* cs = in.cos + int64_t(pos) * 128;
+  const float* sn = in.sin + int64_t(pos) * 128;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    const int c = 2 * kk + h, pc = c ^ 8;
+    float f[8], pf[8], wf[8], pw[8];
+    unpack8(raw[kk], f);
+    unpack8(raw[kk ^ 4], pf);
+    unpack8(reinterpret_cast<const u32x4*>(in.w)[c], wf);
+    unpack8(reinterpret_cast<const u32x4*>(in.w)[pc], pw);
+    const f32x4v c0 = reinterpret_cast<const f32x4v*>(cs + 8 * c)[0], c1 = reinterpret_cast<const f32x4v*>(cs + 8 * c)[1];
+    const f32x4v s0 = reinterpret_cast<const f32x4v*>(sn + 8 * c)[0], s1 = reinterpret_cast<const f32x4v*>(sn + 8 * c)[1];
+    const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float y[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const float a = (f[e + u] * r) * wf[e + u];
+        const float p = (pf[e + u] * r) * pw[e + u];
+        const float rot = kk < 4 ? -p : p;
+        y[u] = fmaf(a, cv[e + u], rot * sv[e + u]);
+      }
+      o[e / 2] = pack_bf16x2(y[0], y[1]);
+    }
+    o ^= flip;
+    qf[kk] = __builtin_bit_cast(bf16x8, o);
+  }
+}
+
 // WAVES = 8: 256 query rows per workgroup, one workgroup per CU; WAVES = 4: 128 rows, two per CU
 // (more, smaller workgroups balance the causal triangle when there are few 256-row tiles).
-template <int WAVES>
+template <int WAVES, bool QKV = false>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int S, int hq, int hkv, int nkv, int nt, float c, int negate, int causal,
-    int o_tokens) {
+    int o_tokens, QkvIn qin) {
   constexpr int BQ = 32 * WAVES;               // query rows per workgroup
   constexpr int kDmaT = 16 / WAVES;            // DMA instructions per wave per 16 KB tile
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
@@ -187,7 +269,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   const int64_t bh = int64_t(b) * hq + kvh * G + g;
   const uint16_t* qp = Q + bh * S * D;
   const uint16_t* kp = K + int64_t(kvi) * S * D;
-  const uint16_t* vp = V + int64_t(kvi) * S * D;
+  // V rows: D apart in [B*HKV, S, D], or ld apart in the fused projection output
+  const int64_t vrow = QKV ? qin.ld : D;
+  const uint16_t* vp = QKV ? V + int64_t(b) * S * qin.ld + qin.vcol + kvh * D : V + int64_t(kvi) * S * D;
   uint16_t* op = O + bh * S * D;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -201,25 +285,27 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   //      lane L writes row L/16, slot L%16, so it fetches the chunk that belongs in that slot
   const uint32_t kv_bytes = uint32_t(S) * D * 2u;
   const i32x4 rsrc_k = make_rsrc(kp, kv_bytes);
-  const i32x4 rsrc_v = make_rsrc(vp, kv_bytes);
+  const i32x4 rsrc_v = make_rsrc(vp, uint32_t((int64_t(S) - 1) * vrow * 2 + D * 2));
   uint32_t k_voff[kDmaT], v_voff[kDmaT];
 #pragma unroll
   for (int t = 0; t < kDmaT; ++t) {
     const int key = 4 * (kDmaT * wave + t) + (lane >> 4);
     const int slot = lane & 15;
     k_voff[t] = uint32_t(key * D + ((slot ^ (key & 15)) * 8)) * 2u;
-    v_voff[t] = uint32_t(key * D + ((slot ^ (4 * (key & 3))) * 8)) * 2u;
+    v_voff[t] = uint32_t(int64_t(key) * vrow + ((slot ^ (4 * (key & 3))) * 8)) * 2u;
   }
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
   auto issue_block = [&](int kb) __attribute__((always_inline)) {
     const uint32_t st = lds0 + uint32_t(kb & 1) * kStageBytes;
     const uint32_t soff = uint32_t(kb) * uint32_t(kTileBytes);
+    const uint32_t soff_v = uint32_t(int64_t(kb) * BKV * vrow * 2);
 #pragma unroll
     for (int t = 0; t < kDmaT; ++t)
       dma16(rsrc_k, __builtin_amdgcn_readfirstlane(st + (wave * kDmaT + t) * 1024), k_voff[t], soff);
 #pragma unroll
     for (int t = 0; t < kDmaT; ++t)
-      dma16(rsrc_v, __builtin_amdgcn_readfirstlane(st + kTileBytes + (wave * kDmaT + t) * 1024), v_voff[t], soff);
+      dma16(rsrc_v, __builtin_amdgcn_readfirstlane(st + kTileBytes + (wave * kDmaT + t) * 1024), v_voff[t],
+            soff_v);
   };
 
   // ---- fragment addressing
@@ -246,13 +332,17 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   //      carried by Q's sign (exact in bf16) so that c > 0 and the max commutes with the scaling
   bf16x8 qf[8];
   if (active) {
-    const uint16_t* src = qp + int64_t(qi) * D + h * 8;
     const uint32_t flip = negate ? 0x80008000u : 0u;
+    if constexpr (QKV) {
+      qnorm_rope_row(Q + (int64_t(b) * S + qi) * qin.ld + (kvh * G + g) * D + h * 8, qin, qi, h, flip, qf);
+    } else {
+      const uint16_t* src = qp + int64_t(qi) * D + h * 8;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      u32x4 v = *reinterpret_cast<const u32x4*>(src + kk * 16);
-      v ^= flip;
-      qf[kk] = __builtin_bit_cast(bf16x8, v);
+      for (int kk = 0; kk < 8; ++kk) {
+        u32x4 v = *reinterpret_cast<const u32x4*>(src + kk * 16);
+        v ^= flip;
+        qf[kk] = __builtin_bit_cast(bf16x8, v);
+      }
     }
   }
 
@@ -304,8 +394,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
 }  // namespace
 
+// qin.w non-null: the fused form (q and v read from the projection output, q normalised in place)
 static int flash_launch(const void* q, const void* k, const void* v, void* o, int64_t batch, int64_t hq, int64_t hkv,
-                        int64_t seq, int64_t head_dim, float scale, int causal, int o_tokens, void* stream) {
+                        int64_t seq, int64_t head_dim, float scale, int causal, int o_tokens, const QkvIn& qin,
+                        void* stream) {
   if (batch < 0 || hq <= 0 || hkv <= 0 || seq < 0 || head_dim <= 0) return PTB_ERR_SHAPE;
   if (hq % hkv) return PTB_ERR_SHAPE;
   if (head_dim != D) return PTB_ERR_UNSUPPORTED;
@@ -314,6 +406,7 @@ static int flash_launch(const void* q, const void* k, const void* v, void* o, in
   if (!q || !k || !v || !o) return PTB_ERR_NULL;
   if (seq % 128) return PTB_ERR_UNSUPPORTED;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return PTB_ERR_ALIGN;
+  const bool fused = qin.w != nullptr;
   const int64_t nkv = batch * hkv;
   // 256-row workgroups when there are at least two per CU, else 128-row ones (two per CU)
   int dev = 0, cus = 256;
@@ -322,32 +415,52 @@ static int flash_launch(const void* q, const void* k, const void* v, void* o, in
   const int64_t bq = wide ? 256 : 128;
   const int64_t nt = (seq + bq - 1) / bq;
   const int64_t total = nt * nkv * (hq / hkv);
-  // K/V of one kv head are addressed through a 32-bit buffer range
-  if (total > 0x7fffffff || seq * D * 2 >= (int64_t(1) << 32) || batch * hq * seq > (int64_t(1) << 40))
+  // K/V of one kv head are addressed through a 32-bit buffer range (v with its row stride)
+  const int64_t vrow = fused ? qin.ld : D;
+  if (total > 0x7fffffff || seq * vrow * 2 >= (int64_t(1) << 32) || batch * hq * seq > (int64_t(1) << 40))
     return PTB_ERR_GRID;
   const float c = std::fabs(scale) * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto qp = static_cast<const uint16_t*>(q), kp = static_cast<const uint16_t*>(k), vp = static_cast<const uint16_t*>(v);
   auto op = static_cast<uint16_t*>(o);
-  if (wide)
-    flash_fwd_kernel<8><<<dim3(unsigned(total)), dim3(512), 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv),
-                                                                   int(nkv), int(nt), c, scale < 0.f ? 1 : 0,
-                                                                   causal ? 1 : 0, o_tokens);
+  const int neg = scale < 0.f ? 1 : 0, cz = causal ? 1 : 0;
+  const unsigned grid = unsigned(total);
+  if (wide && fused)
+    flash_fwd_kernel<8, true><<<grid, 512, 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv), int(nkv), int(nt), c,
+                                                   neg, cz, o_tokens, qin);
+  else if (wide)
+    flash_fwd_kernel<8><<<grid, 512, 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv), int(nkv), int(nt), c, neg,
+                                             cz, o_tokens, qin);
+  else if (fused)
+    flash_fwd_kernel<4, true><<<grid, 256, 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv), int(nkv), int(nt), c,
+                                                   neg, cz, o_tokens, qin);
   else
-    flash_fwd_kernel<4><<<dim3(unsigned(total)), dim3(256), 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv),
-                                                                   int(nkv), int(nt), c, scale < 0.f ? 1 : 0,
-                                                                   causal ? 1 : 0, o_tokens);
+    flash_fwd_kernel<4><<<grid, 256, 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv), int(nkv), int(nt), c, neg,
+                                             cz, o_tokens, qin);
   return launch_status();
 }
 
 PTB_EXPORT int ptb_flash_attn_fwd_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
                                        int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale,
                                        int causal, void* stream) {
-  return flash_launch(q, k, v, o, batch, hq, hkv, seq, head_dim, scale, causal, 0, stream);
+  return flash_launch(q, k, v, o, batch, hq, hkv, seq, head_dim, scale, causal, 0, QkvIn{}, stream);
 }
 
 PTB_EXPORT int ptb_flash_attn_fwd_tokens_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
                                               int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim, float scale,
                                               int causal, void* stream) {
-  return flash_launch(q, k, v, o, batch, hq, hkv, seq, head_dim, scale, causal, 1, stream);
+  return flash_launch(q, k, v, o, batch, hq, hkv, seq, head_dim, scale, causal, 1, QkvIn{}, stream);
+}
+
+PTB_EXPORT int ptb_flash_attn_fwd_qkv_bf16(const void* qkv, int64_t ld, const void* k, const void* qnorm_w,
+                                           const float* cos_t, const float* sin_t, float eps, void* o,
+                                           int64_t batch, int64_t hq, int64_t hkv, int64_t seq, int64_t head_dim,
+                                           float scale, int causal, void* stream) {
+  if (hq <= 0 || hkv <= 0 || ld < (hq + 2 * hkv) * D || ld > 0x7fffffff) return PTB_ERR_SHAPE;
+  if (batch > 0 && seq > 0 && head_dim == D) {
+    if (!qnorm_w || !cos_t || !sin_t) return PTB_ERR_NULL;
+    if (ld % 8 || !aligned16(qnorm_w) || !aligned16(cos_t) || !aligned16(sin_t)) return PTB_ERR_ALIGN;
+  }
+  const QkvIn qin{static_cast<const uint16_t*>(qnorm_w), cos_t, sin_t, eps, int(ld), int((hq + hkv) * D)};
+  return flash_launch(qkv, k, qkv, o, batch, hq, hkv, seq, head_dim, scale, causal, 1, qin, stream);
 }

@@ -122,6 +122,8 @@ SIGNATURES = {
                                          _c_int, _vp]),
     "ptb_flash_attn_fwd_tokens_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32,
                                          _c_int, _vp]),
+    "ptb_flash_attn_fwd_qkv_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _vp, _c_f32, _vp, _c_i64, _c_i64, _c_i64,
+                                             _c_i64, _c_i64, _c_f32, _c_int, _vp]),
     "ptb_sumsq_bf16": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
     "ptb_gemv_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
     "ptb_gemv_bf16": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),

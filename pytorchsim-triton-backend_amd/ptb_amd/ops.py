@@ -307,6 +307,36 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, hq: int, 
     return o
 
 
+def flash_attention_qkv(qkv: torch.Tensor, k: torch.Tensor, qnorm_w: torch.Tensor, cos: torch.Tensor,
+                        sin: torch.Tensor, hq: int, hkv: int, eps: float, causal: bool = True,
+                        scale: float | None = None, out=None) -> torch.Tensor:
+    """Attention over a fused projection output: qkv [B*S, ld] bf16 holds q | k | v per token
+    (row stride ld >= (hq + 2*hkv)*128), k the normalised, rotated keys [B*hkv, S, 128]; the queries
+    are normalised (qnorm_w, eps) and rotated (cos/sin [S, 128] fp32) in the kernel and v read in
+    place.  Returns o [B, S, hq, 128] token-major, bit for bit qk_norm_rope(q) + transpose_heads(v) +
+    flash_attention(tokens_out=True)."""
+    _need(k, "k", BF16, 3)
+    _need(qnorm_w, "qnorm_w", BF16, 1)
+    _need(cos, "cos", F32, 2)
+    _need(sin, "sin", F32, 2)
+    if qkv.dtype != BF16 or qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be a row-major [B*S, ld] bf16 matrix (rows may be a strided view)")
+    bhkv, s, d = k.shape
+    if hq <= 0 or hkv <= 0 or hq % hkv or bhkv % hkv:
+        raise ValueError(f"bad head counts hq={hq}, hkv={hkv} for k of shape {tuple(k.shape)}")
+    batch = bhkv // hkv
+    ld = qkv.stride(0)
+    if qkv.shape[0] != batch * s or qkv.shape[1] < (hq + 2 * hkv) * d:
+        raise ValueError(f"qkv must be [B*S, >= (hq + 2*hkv)*{d}], got {tuple(qkv.shape)}")
+    if tuple(cos.shape) != (s, d) or tuple(sin.shape) != (s, d) or qnorm_w.numel() != d:
+        raise ValueError("cos/sin must be [S, head_dim] and qnorm_w [head_dim]")
+    o = _out(out, (batch, s, hq, d), BF16, qkv)
+    sc = default_scale(d) if scale is None else float(scale)
+    _lib.call("ptb_flash_attn_fwd_qkv_bf16", qkv.data_ptr(), ld, k.data_ptr(), qnorm_w.data_ptr(), cos.data_ptr(),
+              sin.data_ptr(), float(eps), o.data_ptr(), batch, hq, hkv, s, d, sc, 1 if causal else 0, _stream(qkv))
+    return o
+
+
 # ---- single-token (decode) path -------------------------------------------------------------------
 
 def sumsq(x: torch.Tensor, y: torch.Tensor | None = None, out=None) -> torch.Tensor:

@@ -113,8 +113,7 @@ class Qwen3Layer:
 
             self._bufs[key] = {
                 "xn": e(tokens, c.hidden), "qkv": e(tokens, qd + 2 * kd),
-                "qh": e(c.heads, tokens, c.head_dim), "kh": e(c.kv_heads, tokens, c.head_dim),
-                "vh": e(c.kv_heads, tokens, c.head_dim),
+                "kh": e(c.kv_heads, tokens, c.head_dim),
                 "o": e(tokens, c.heads, c.head_dim), "h": e(tokens, c.hidden), "hn": e(tokens, c.hidden),
                 "a": e(tokens, c.intermediate), "y": e(tokens, c.hidden),
             }
@@ -130,15 +129,13 @@ class Qwen3Layer:
         qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
         qkv = b["qkv"]
         ops.gemm(b["xn"], self.wqkv, out=qkv)                                              # K01 + K03
-        # the norms and the v transpose read their column slices of [T, q|k|v] in place
-        ops.qk_norm_rope(qkv[:, :qd].view(t, c.heads, c.head_dim), w["w_qn"], cos, sin, c.eps,
-                         out=b["qh"])                                                        # K02
+        # the k-norm reads its column slice of [T, q|k|v] in place; attention reads q (normalising and
+        # rotating it in its prologue) and v there too, and writes O token-major
         ops.qk_norm_rope(qkv[:, qd:qd + kd].view(t, c.kv_heads, c.head_dim), w["w_kn"], cos, sin, c.eps,
                          out=b["kh"])                                                        # K04
-        ops.transpose_heads(qkv[:, qd + kd:].view(t, c.kv_heads, c.head_dim), out=b["vh"])   # K05
-        ops.flash_attention(b["qh"], b["kh"], b["vh"], c.heads, c.kv_heads, True,
-                            1.0 / math.sqrt(c.head_dim), out=b["o"].view(1, t, c.heads, c.head_dim),
-                            tokens_out=True)                                                # K06 + K07
+        ops.flash_attention_qkv(qkv, b["kh"], w["w_qn"], cos, sin, c.heads, c.kv_heads, c.eps, True,
+                                1.0 / math.sqrt(c.head_dim),
+                                out=b["o"].view(1, t, c.heads, c.head_dim))                  # K02 K05 K06 K07
         ops.gemm(b["o"].view(t, c.heads * c.head_dim), w["wo"], residual=x, out=b["h"])     # K08
         ops.rmsnorm(b["h"], w["w_post"], c.eps, out=b["hn"])                                # K00
         ops.gemm_swiglu(b["hn"], w["wgu"], out=b["a"])                                      # K09 + K10

@@ -103,6 +103,16 @@ def test_32bit_buffer_offset_limits_refused(lib):
     assert lib.ptb_flash_attn_fwd_bf16(P16, P16, P16, P16, 1, 1, 1, 1 << 24, 128, 0.1, 1, None) == _lib.PTB_ERR_GRID
 
 
+def test_fused_attention_refusals(lib):
+    # ld narrower than q|k|v; a missing q-norm weight; a row stride that breaks 16-byte rows
+    assert lib.ptb_flash_attn_fwd_qkv_bf16(P16, 1000, P16, P16, P16, P16, 1e-6, P16, 1, 4, 2, 128, 128, 0.1, 1,
+                                           None) == _lib.PTB_ERR_SHAPE
+    assert lib.ptb_flash_attn_fwd_qkv_bf16(P16, 1024, P16, None, P16, P16, 1e-6, P16, 1, 4, 2, 128, 128, 0.1, 1,
+                                           None) == _lib.PTB_ERR_NULL
+    assert lib.ptb_flash_attn_fwd_qkv_bf16(P16, 1028, P16, P16, P16, P16, 1e-6, P16, 1, 4, 2, 128, 128, 0.1, 1,
+                                           None) == _lib.PTB_ERR_ALIGN
+
+
 def test_empty_work_is_a_no_op(lib):
     # zero rows / zero-size outputs return OK without launching
     assert lib.ptb_rmsnorm_bf16(P16, P16, 0, P16, 0, 64, 1e-6, None) == _lib.PTB_OK

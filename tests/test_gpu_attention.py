@@ -79,6 +79,35 @@ def test_flash_tokens_out_is_the_transposed_output(batch, hq, hkv, s):
     assert bits_equal(tokens, heads.view(batch, hq, s, 128).transpose(1, 2).contiguous())
 
 
+@pytest.mark.parametrize("batch,hq,hkv,s,causal,scale", [
+    (1, 32, 8, 2048, True, None),      # the prefill layer's shape (128-row workgroups)
+    (1, 32, 8, 4096, True, None),      # 256-row workgroups
+    (2, 8, 2, 256, False, -0.05),      # batches, no mask, a negative scale
+])
+def test_flash_qkv_is_the_launch_chain(batch, hq, hkv, s, causal, scale):
+    """The fused form (q normalised and rotated in the prologue, q and v read in place from the
+    [B*S, ld] projection output, ld wider than q|k|v) equals qk_norm_rope(q) + transpose_heads(v) +
+    flash_attention(tokens_out) bit for bit, batch by batch."""
+    from ptb_amd import qwen3
+
+    d, eps = 128, 1e-6
+    ld = (hq + 2 * hkv) * d + 64
+    qkv = randn((batch * s, ld), 40).to(DEV)
+    w_qn = (randn((d,), 41).float() * 0.1 + 1).to(torch.bfloat16).to(DEV)
+    w_kn = (randn((d,), 42).float() * 0.1 + 1).to(torch.bfloat16).to(DEV)
+    cos, sin = qwen3.rope_tables(s, d, 1.0e6, DEV)
+    kcol, vcol = hq * d, (hq + hkv) * d
+    kh = torch.cat([ops.qk_norm_rope(qkv[i * s:(i + 1) * s, kcol:vcol].view(s, hkv, d), w_kn, cos, sin, eps)
+                    for i in range(batch)])
+    got = ops.flash_attention_qkv(qkv, kh, w_qn, cos, sin, hq, hkv, eps, causal, scale)
+    for i in range(batch):
+        rows = qkv[i * s:(i + 1) * s]
+        qh = ops.qk_norm_rope(rows[:, :kcol].view(s, hq, d), w_qn, cos, sin, eps)
+        vh = ops.transpose_heads(rows[:, vcol:vcol + hkv * d].view(s, hkv, d))
+        want = ops.flash_attention(qh, kh[i * hkv:(i + 1) * hkv], vh, hq, hkv, causal, scale, tokens_out=True)
+        assert bits_equal(got[i], want[0]), f"batch {i}"
+
+
 def test_flash_refuses_bad_shapes():
     q = torch.zeros((4, 100, 128), dtype=torch.bfloat16, device=DEV)
     with pytest.raises(_lib.UnsupportedError):
