@@ -106,10 +106,19 @@ def bench_rmsnorm(steps, warmup):
     ms, wall = timed(step, steps * 4, warmup)
     nbytes = 2 * rows * cols * 2 + cols * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
+
+    # the practical ceiling: a device copy (hipMemcpyAsync) of the same bytes, x -> y, same cycling
+    def copy_step():
+        i = it[0] % copies
+        it[0] += 1
+        ys[i].copy_(xs[i])
+
+    copy_ms, _ = timed(copy_step, steps * 4, warmup)
     return {"name": "rmsnorm", "config": "BASELINE config 1: x bf16 [2048x4096], w fp32",
             "us": ms * 1e3, "wall_us": wall * 1e3, "gbs": gbs,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": gbs / PEAK_HBM_GBS}}
+                         "frac": gbs / PEAK_HBM_GBS},
+            "device_copy_us": copy_ms * 1e3, "vs_device_copy": copy_ms / ms}
 
 
 def bench_gemm_fp8(steps, warmup):
@@ -394,6 +403,9 @@ def pmc_driver(which: str) -> None:
         w = (torch.randn(4096, generator=g) * 0.02 + 1).cuda()
         y = torch.empty_like(x)
         run = lambda: ops.rmsnorm(x, w, 1e-6, out=y)  # noqa: E731
+    elif which == "quant_rows":
+        x = torch.randn(2048, 12288, generator=g).to(torch.bfloat16).cuda()
+        run = lambda: ops.quant_rows_e4m3(x)  # noqa: E731
     elif which == "gemv_decode":
         from ptb_amd import _lib
         wg = (torch.randn(4096, 24576, generator=g) * 0.02).to(torch.bfloat16).cuda()

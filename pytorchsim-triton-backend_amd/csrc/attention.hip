@@ -330,6 +330,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
   // ---- Q fragments (B operand of S^T = K Q^T): 8 K-steps of 16 over d; a negative scale is
   //      carried by Q's sign (exact in bf16) so that c > 0 and the max commutes with the scaling
+  // the first K/V block's DMA goes out before the query loads: its latency overlaps theirs
+  issue_block(0);
+
   bf16x8 qf[8];
   if (active) {
     const uint32_t flip = negate ? 0x80008000u : 0u;
@@ -360,7 +363,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   // diagonal (blocks past it are fully masked); inactive waves compute nothing
   const int nb = causal ? min(q0 + BQ, S) / BKV : S / BKV;
   const int last = !active ? -1 : causal ? (qw0 + 31) / BKV : nb - 1;
-  issue_block(0);
   for (int kb = 0; kb < nb; ++kb) {
     wait_vmcnt<0>();
     __syncthreads();  // block kb landed (all waves); every wave is done with block kb-1's stage
