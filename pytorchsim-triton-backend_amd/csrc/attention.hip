@@ -33,6 +33,7 @@
 // When S is not a multiple of the tile height, the last tile's waves past S only keep the loads and
 // barriers going (keys past S read as zero through the buffer range).
 #include <cmath>
+#include <type_traits>
 
 #include "ptb_common.h"
 
@@ -295,8 +296,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     v_voff[t] = uint32_t(int64_t(key) * vrow + ((slot ^ (4 * (key & 3))) * 8)) * 2u;
   }
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
-  auto issue_block = [&](int kb) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + uint32_t(kb & 1) * kStageBytes;
+  // par = kb & 1, a compile-time constant at every call, so stage addresses fold into the LDS
+  // instructions' offset fields
+  auto issue_block = [&](int kb, auto par) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + uint32_t(decltype(par)::value) * kStageBytes;
     const uint32_t soff = uint32_t(kb) * uint32_t(kTileBytes);
     const uint32_t soff_v = uint32_t(int64_t(kb) * BKV * vrow * 2);
 #pragma unroll
@@ -331,7 +334,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   // ---- Q fragments (B operand of S^T = K Q^T): 8 K-steps of 16 over d; a negative scale is
   //      carried by Q's sign (exact in bf16) so that c > 0 and the max commutes with the scaling
   // the first K/V block's DMA goes out before the query loads: its latency overlaps theirs
-  issue_block(0);
+  issue_block(0, std::integral_constant<int, 0>{});
 
   bf16x8 qf[8];
   if (active) {
@@ -363,12 +366,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   // diagonal (blocks past it are fully masked); inactive waves compute nothing
   const int nb = causal ? min(q0 + BQ, S) / BKV : S / BKV;
   const int last = !active ? -1 : causal ? (qw0 + 31) / BKV : nb - 1;
-  for (int kb = 0; kb < nb; ++kb) {
+  auto block = [&](int kb, auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
     wait_vmcnt<0>();
     __syncthreads();  // block kb landed (all waves); every wave is done with block kb-1's stage
-    if (kb + 1 < nb) issue_block(kb + 1);
+    if (kb + 1 < nb) issue_block(kb + 1, std::integral_constant<int, 1 - P>{});
     if (kb <= last) {
-      const uint32_t st = lds0 + uint32_t(kb & 1) * kStageBytes;
+      const uint32_t st = lds0 + uint32_t(P) * kStageBytes;
       qk_step(sacc, qf, st, koff);
       if (causal && kb == last)
         softmax_step<true>(w, sacc, pf, c, qi - kb * BKV - 4 * h);
@@ -376,7 +380,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         softmax_step<false>(w, sacc, pf, c, 0);
       pv_step(w, pf, st + kTileBytes, voff);
     }
+  };
+  int kb = 0;
+  for (; kb + 1 < nb; kb += 2) {   // two blocks a trip: the stage of each is a constant
+    block(kb, std::integral_constant<int, 0>{});
+    block(kb + 1, std::integral_constant<int, 1>{});
   }
+  if (kb < nb) block(kb, std::integral_constant<int, 0>{});
   if (!active) return;
 
   const float l = pair32_sum(w.l);
