@@ -19,6 +19,8 @@
 // the DMA that refills this stage's slot (NS stages ahead) and the reads of the next stage's
 // substep 0.  MFMAs take W as the first operand, so accumulators hold C^T blocks and each lane
 // stores 4 consecutive columns of a row of C at once.
+#include <type_traits>
+
 #include "ptb_common.h"
 
 using namespace ptb;
@@ -88,15 +90,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   for (int t = 0; t < G::kDmaA; ++t) a_voff[t] = voff_of((wave * G::kDmaA + t) * 8 + (lane >> 3));
 #pragma unroll
   for (int t = 0; t < G::kDmaW; ++t) w_voff[t] = voff_of((wave * G::kDmaW + t) * 8 + (lane >> 3));
+  // stg = kt % NS is a compile-time constant at every call (the main loop runs NS steps a trip), so
+  // stage addresses are constants: scalar adds for the DMA bases, immediate offsets for the reads
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
-  auto dma_one = [&](int kt, int d) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + uint32_t(kt % NS) * G::kStageBytes;
+  const uint32_t wave_a = __builtin_amdgcn_readfirstlane(uint32_t(wave * G::kDmaA * 1024));
+  const uint32_t wave_w = __builtin_amdgcn_readfirstlane(uint32_t(wave * G::kDmaW * 1024));
+  auto dma_one = [&](int kt, int d, auto stg) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + uint32_t(decltype(stg)::value) * G::kStageBytes;
     const uint32_t soff = uint32_t(kt * BK);
     if (d < G::kDmaA)
-      dma16(rsrc_a, __builtin_amdgcn_readfirstlane(st + (wave * G::kDmaA + d) * 1024), a_voff[d], soff);
+      dma16(rsrc_a, st + wave_a + d * 1024, a_voff[d], soff);
     else
-      dma16(rsrc_w, __builtin_amdgcn_readfirstlane(st + G::kABytes + (wave * G::kDmaW + d - G::kDmaA) * 1024),
-            w_voff[d - G::kDmaA], soff);
+      dma16(rsrc_w, st + G::kABytes + wave_w + (d - G::kDmaA) * 1024, w_voff[d - G::kDmaA], soff);
   };
 
   f32x16 acc[4][G::WNT];
@@ -141,10 +146,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   };
 
   const int nk = K / BK;
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2 % NS>;
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
+  for (int d = 0; d < G::kDma; ++d) dma_one(0, d, S0{});
 #pragma unroll
-    for (int d = 0; d < G::kDma; ++d) dma_one(s, d);
+  for (int d = 0; d < G::kDma; ++d) dma_one(1, d, S1{});
+  if constexpr (NS > 2) {
+#pragma unroll
+    for (int d = 0; d < G::kDma; ++d) dma_one(2, d, S2{});
+  }
   wait_vmcnt<(NS - 1) * G::kDma>();   // stage 0 landed (this wave's part)
   __syncthreads();                    // ... and everyone's
   Frags<BN> f0, f1;
@@ -161,8 +173,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int t = o == 0 ? 0 : (o <= G::WNT ? 4 + (o - 1) : o - G::WNT);
     return 2 * t + (q & 1);
   };
-  for (int kt = 0; kt < nk; ++kt) {
-    const uint8_t* st = smem + (kt % NS) * G::kStageBytes;
+  auto step = [&](int kt, auto stg) __attribute__((always_inline)) {
+    constexpr int SI = decltype(stg)::value;   // kt % NS
+    const uint8_t* st = smem + SI * G::kStageBytes;
     // substep 0, with the reads of substep 1 of this stage
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -176,7 +189,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     // is done reading stage kt, whose slot takes stage kt+NS
     wait_vmcnt<(NS - 2) * G::kDma>();
     __syncthreads();
-    const uint8_t* nst = smem + ((kt + 1) % NS) * G::kStageBytes;
+    const uint8_t* nst = smem + ((SI + 1) % NS) * G::kStageBytes;
     // substep 1, with the reads of the next stage's substep 0 and the refill DMA
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -186,9 +199,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         if (q < P) read_piece(nst, 0, piece_of(q), f0);
 #pragma unroll
       for (int d = 0; d < D; ++d)
-        if (d * U / D == u) dma_one(kt + NS, d);
+        if (d * U / D == u) dma_one(kt + NS, d, stg);
       __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  int kt = 0;
+  for (; kt + NS <= nk; kt += NS) {
+    step(kt, S0{});
+    step(kt + 1, S1{});
+    if constexpr (NS > 2) step(kt + 2, S2{});
+  }
+  if (kt < nk) step(kt, S0{});
+  if constexpr (NS > 2) {
+    if (kt + 1 < nk) step(kt + 1, S1{});
   }
   wait_vmcnt<0>();
 
