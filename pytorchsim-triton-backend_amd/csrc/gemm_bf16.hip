@@ -24,6 +24,8 @@
 //
 // Tile order is XCD-aware: hardware hands workgroup i to XCD i % 8, so ids are remapped to give
 // each XCD a contiguous range of tiles, walked in groups of 8 tile-rows for L2 reuse.
+#include <type_traits>
+
 #include "ptb_common.h"
 
 using namespace ptb;
@@ -217,16 +219,23 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     b_voff[t] = uint32_t(k * N + bcol) * 2u;
   }
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
-  // t-th of this wave's DMA instructions of stage kt (A first, then B)
-  auto dma_one = [&](int kt, int t) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + uint32_t(kt % NS) * kStageBytes;
+  const uint32_t wave_a = __builtin_amdgcn_readfirstlane(uint32_t(wave * Sh::kDmaA * 1024));
+  const uint32_t wave_b = __builtin_amdgcn_readfirstlane(uint32_t(wave * Sh::kDmaB * 1024));
+  // t-th of this wave's DMA instructions of stage kt (A first, then B); stg = kt % NS is a
+  // compile-time constant at every call (the main loop runs NS steps a trip), so the LDS addresses
+  // are constants plus scalar offsets and the fragment reads take them as immediate offsets
+  auto dma_one = [&](int kt, int t, auto stg) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + uint32_t(decltype(stg)::value) * kStageBytes;
     if (t < Sh::kDmaA)
-      dma16(rsrc_a, __builtin_amdgcn_readfirstlane(st + (wave * Sh::kDmaA + t) * 1024), a_voff[t],
-            uint32_t(kt * BK) * 2u);
+      dma16(rsrc_a, st + wave_a + t * 1024, a_voff[t], uint32_t(kt * BK) * 2u);
     else
-      dma16(rsrc_b, __builtin_amdgcn_readfirstlane(st + kABytes + (wave * Sh::kDmaB + t - Sh::kDmaA) * 1024),
-            b_voff[t - Sh::kDmaA], uint32_t(kt * BK) * uint32_t(N) * 2u);
+      dma16(rsrc_b, st + kABytes + wave_b + (t - Sh::kDmaA) * 1024, b_voff[t - Sh::kDmaA],
+            uint32_t(kt * BK) * uint32_t(N) * 2u);
   };
+  using Stg0 = std::integral_constant<int, 0>;
+  using Stg1 = std::integral_constant<int, 1 % NS>;
+  using Stg2 = std::integral_constant<int, 2 % NS>;
+  using Stg3 = std::integral_constant<int, 3 % NS>;
 
   f32x16 acc[WM][WN];
 #pragma unroll
@@ -290,9 +299,14 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   constexpr bool kOneReadPerMfma = P <= U;
   constexpr bool kStaggered = D <= U && P + 1 <= U;
   const int nk = Kl / BK;
-  for (int s = 0; s < DIST; ++s)
 #pragma unroll
-    for (int t = 0; t < D; ++t) dma_one(s, t);
+  for (int t = 0; t < D; ++t) dma_one(0, t, Stg0{});
+#pragma unroll
+  for (int t = 0; t < D; ++t) dma_one(1, t, Stg1{});
+  if constexpr (DIST > 2) {
+#pragma unroll
+    for (int t = 0; t < D; ++t) dma_one(2, t, Stg2{});
+  }
   wait_vmcnt<(DIST - 1) * D>();     // stage 0 landed (this wave's part)
   __syncthreads();                  // ... and everyone's
   Slice sl[2];
@@ -303,8 +317,10 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   // publishes stage kt+1 (and frees the slot DIST - NS steps back); the last slice with the DMA of
   // stage kt+DIST and the reads of stage kt+1's slice 0 folded in.  sched_barrier(0) pins that
   // interleave, so the matrix core is fed between memory instructions.
-  for (int kt = 0; kt < nk; ++kt) {
-    const uint8_t* st = smem + (kt % NS) * kStageBytes;
+  auto step = [&](int kt, auto stg) __attribute__((always_inline)) {
+    constexpr int SI = decltype(stg)::value;   // kt % NS
+    using Far = std::integral_constant<int, (SI + DIST) % NS>;
+    const uint8_t* st = smem + SI * kStageBytes;
 #pragma unroll
     for (int q = 0; q + 1 < SPS; ++q) {
 #pragma unroll
@@ -319,23 +335,37 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     // stage kt+1 landed; past this barrier no wave reads stage kt (nor, for DIST < NS, stage kt-1)
     wait_vmcnt<(DIST - 2) * D>();
     __syncthreads();
-    const uint8_t* nst = smem + ((kt + 1) % NS) * kStageBytes;
+    const uint8_t* nst = smem + ((SI + 1) % NS) * kStageBytes;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       mfma_one(sl[(SPS - 1) & 1], u);
       if constexpr (kStaggered) {   // DMA t after MFMA t, read p after MFMA p+1
-        if (u < D) dma_one(kt + DIST, u);
+        if (u < D) dma_one(kt + DIST, u, Far{});
         if (u >= 1 && u <= P) read_piece(nst, 0, u - 1, sl[0]);
       } else {                      // the DMAs and reads spread evenly over the MFMAs
 #pragma unroll
         for (int o = 0; o < D + P; ++o)
           if (o >= u * (D + P) / U && o < (u + 1) * (D + P) / U) {
-            if (o < D) dma_one(kt + DIST, o);
+            if (o < D) dma_one(kt + DIST, o, Far{});
             else read_piece(nst, 0, o - D, sl[0]);
           }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  int kt = 0;
+  for (; kt + NS <= nk; kt += NS) {
+    step(kt, Stg0{});
+    step(kt + 1, Stg1{});
+    if constexpr (NS > 2) {
+      step(kt + 2, Stg2{});
+      step(kt + 3, Stg3{});
+    }
+  }
+  if (kt < nk) step(kt, Stg0{});
+  if constexpr (NS > 2) {
+    if (kt + 1 < nk) step(kt + 1, Stg1{});
+    if (kt + 2 < nk) step(kt + 2, Stg2{});
   }
   wait_vmcnt<0>();
 
