@@ -101,7 +101,9 @@ def test_quant_weight_exact(k, n, seed):
     assert bits_equal(wq, owq)
 
 
-@pytest.mark.parametrize("m,k,n", [(2048, 12288, 4096), (1, 128, 16), (300, 256, 272), (257, 1024, 512)])
+@pytest.mark.parametrize("m,k,n", [(2048, 12288, 4096), (1, 128, 16), (300, 256, 272), (257, 1024, 512),
+                                   (4096, 1152, 4096),   # 256x256 tiles, two-stage ring, an odd step count
+                                   (2048, 896, 4096)])   # 256x128 tiles, 7 steps: a one-step remainder
 def test_gemm_fp8(m, k, n):
     """activations bf16 ~N(0,1) quantised per token, weights from N(0,0.02)
     quantised per output channel; the GPU GEMM and the oracle see the same quantised operands."""
@@ -184,6 +186,27 @@ def test_gemm_swiglu_fused(m, k, inter):
     if m * k * inter <= 300 * 512 * 256:
         want = oracle.silu_mul(oracle.gemm(a, b))
         assert_close(fused, want, RTOL, 2e-2 * float(want.float().abs().mean()), f"swiglu {m}x{k}x{inter}")
+
+
+@pytest.mark.parametrize("m,k,n,resid", [
+    (4096, 1088, 4096, False),   # 256x256 tiles, 17 steps of 64: the unrolled loop's one-step remainder
+    (2048, 4160, 4096, True),    # 256x128 tiles, 65 steps, with the residual epilogue
+])
+def test_gemm_odd_step_count(m, k, n, resid):
+    """The two-stage (64-deep) pipeline runs two K steps a loop trip; an odd step count ends on a
+    single step on stage 0, which must still read the right stage and drain the DMA stream."""
+    std = 1.0 / 64.0
+    got, want = run_gemm(m, k, n, 1, std, std, resid)
+    assert_close(got, want, RTOL, ATOL * rms(want), f"gemm {m}x{k}x{n}")
+
+
+def test_gemm_swiglu_odd_step_count():
+    """The SwiGLU-fused GEMM with K = 64 * 17 (an odd step count) equals the GEMM + silu_mul pair."""
+    a = randn((2048, 1088), 43, std=1 / 16).to(DEV)
+    b = randn((1088, 2 * 6144), 44, std=1 / 4).to(DEV)
+    fused = ops.gemm_swiglu(a, b).cpu()
+    pair = ops.silu_mul(ops.gemm(a, b, split_k=False)).cpu()
+    assert bits_equal(fused, pair)
 
 
 def test_gemm_swiglu_refusals():
