@@ -46,16 +46,16 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // Tile shape: the 4 waves sit 2x2, each owning WM x WN blocks of 32x32, so the workgroup tile is
 // BM = 64*WM rows by BN = 64*WN columns (256x256, 256x128 or 128x128).  A stage holds BK of K:
-// 32 (a 64-byte piece of every A row) in a ring of NS = 4 stages of up to 32 KB, or, for the
-// 256x256 and 256x128 tiles, 64 (a whole 128-byte line of every A row: the L2 serves a request per
-// line, and a half-line request costs a whole one) in a ring of NS = 2 stages of 64 or 48 KB.  The DMA of stage kt + DIST
-// is issued after the barrier of step kt: DIST = NS - 1 reuses the slot freed one step earlier,
-// DIST = NS the slot freed by that barrier.
+// 32 (a 64-byte piece of every A row) in a ring of NS = 4 stages of up to 32 KB, or 64 (a whole
+// 128-byte line of every A row: the L2 serves a request per line, and a half-line request costs a
+// whole one) in a ring of NS = 3 stages of 48 KB (256x128 tiles).  Stage kt + DIST, DIST = NS - 1,
+// refills the slot of stage kt-1, which the barrier of step kt-1 freed, so the stage's DMAs spread
+// over all of step kt's MFMAs.
 template <int WM, int WN, int BKT>
 struct Shape {
   static constexpr int BK = BKT;
-  static constexpr int NS = BK == 64 ? 2 : 4;
-  static constexpr int DIST = BK == 64 ? 2 : 3;
+  static constexpr int NS = BK == 64 ? 3 : 4;
+  static constexpr int DIST = NS - 1;
   static constexpr int SPS = BK / 16;                    // 16-wide K slices per stage
   static constexpr int BM = 64 * WM, BN = 64 * WN;
   static constexpr int kRowBytes = BK * 2;               // bytes of an A row in a stage
@@ -72,7 +72,7 @@ struct Shape {
   static constexpr int kBRowsPerKB = 512 / BN;           // B rows per DMA instruction
   static constexpr int kBSlots = BN / 8;                 // 16-byte chunks per B row
   static_assert(NS * kStageBytes <= 160 * 1024, "the ring fits the LDS");
-  static_assert(DIST <= NS && DIST >= 2, "the DMA refills a slot no wave reads any more");
+  static_assert(DIST == NS - 1 && DIST >= 2, "the DMA refills the slot freed a step earlier");
 };
 // A row m keeps chunk c in slot c ^ swz: 4 chunks (BK 32) rotate by (m >> 2) & 3, 8 chunks (BK 64)
 // by (m >> 1) & 7; either way the 16 rows a 16-lane phase reads land in 16 distinct bank groups.
@@ -297,7 +297,15 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   // loop free of branches; everything is drained before the epilogue.
   constexpr int U = Sh::kMfma, P = Sh::kPieces, D = Sh::kDma, SPS = Sh::SPS;
   constexpr bool kOneReadPerMfma = P <= U;
-  constexpr bool kStaggered = D <= U && P + 1 <= U;
+  // stage kt+DIST's DMAs go out one every SLOTS/D MFMAs of step kt (bunched after the barrier they
+  // would queue behind each other in the address unit and stall the MFMAs)
+  constexpr int SLOTS = SPS * U;
+  constexpr int NPRE = [] {   // DMAs of stage kt+DIST issued before step kt's barrier
+    int n = 0;
+    for (int o = 0; o < D; ++o)
+      if (o * SLOTS / D < (SPS - 1) * U) ++n;
+    return n;
+  }();
   const int nk = Kl / BK;
 #pragma unroll
   for (int t = 0; t < D; ++t) dma_one(0, t, Stg0{});
@@ -313,10 +321,11 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
 #pragma unroll
   for (int p = 0; p < P; ++p) read_piece(smem, 0, p, sl[0]);
 
-  // Each K step: slices 0 .. SPS-2, each with the next slice's reads folded in; the barrier that
-  // publishes stage kt+1 (and frees the slot DIST - NS steps back); the last slice with the DMA of
-  // stage kt+DIST and the reads of stage kt+1's slice 0 folded in.  sched_barrier(0) pins that
-  // interleave, so the matrix core is fed between memory instructions.
+  // Each K step: slices 0 .. SPS-2, each with the next slice's reads and a share of stage
+  // kt+DIST's DMAs folded in; the barrier that publishes stage kt+1 (and frees stage kt's slot for
+  // the next step's DMAs); the last slice with the rest of the DMAs and the reads of stage kt+1's
+  // slice 0 folded in.  sched_barrier(0) pins that interleave, so the matrix core is fed between
+  // memory instructions.
   auto step = [&](int kt, auto stg) __attribute__((always_inline)) {
     constexpr int SI = decltype(stg)::value;   // kt % NS
     using Far = std::integral_constant<int, (SI + DIST) % NS>;
@@ -329,27 +338,27 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
 #pragma unroll
         for (int p = 0; p < P; ++p)
           if (kOneReadPerMfma ? p == u : (p >= u * P / U && p < (u + 1) * P / U)) read_piece(st, q + 1, p, sl[(q + 1) & 1]);
+#pragma unroll
+        for (int o = 0; o < D; ++o)
+          if (o * SLOTS / D == q * U + u) dma_one(kt + DIST, o, Far{});
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // stage kt+1 landed; past this barrier no wave reads stage kt (nor, for DIST < NS, stage kt-1)
-    wait_vmcnt<(DIST - 2) * D>();
+    // stage kt+1 landed (later stages' DMAs may still be in flight); past this barrier no wave
+    // reads stage kt
+    wait_vmcnt<(DIST - 2) * D + NPRE>();
     __syncthreads();
     const uint8_t* nst = smem + ((SI + 1) % NS) * kStageBytes;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       mfma_one(sl[(SPS - 1) & 1], u);
-      if constexpr (kStaggered) {   // DMA t after MFMA t, read p after MFMA p+1
-        if (u < D) dma_one(kt + DIST, u, Far{});
-        if (u >= 1 && u <= P) read_piece(nst, 0, u - 1, sl[0]);
-      } else {                      // the DMAs and reads spread evenly over the MFMAs
+      // the stage's remaining DMAs, and the next stage's first reads spread evenly
 #pragma unroll
-        for (int o = 0; o < D + P; ++o)
-          if (o >= u * (D + P) / U && o < (u + 1) * (D + P) / U) {
-            if (o < D) dma_one(kt + DIST, o, Far{});
-            else read_piece(nst, 0, o - D, sl[0]);
-          }
-      }
+      for (int o = 0; o < D; ++o)
+        if (o * SLOTS / D == (SPS - 1) * U + u) dma_one(kt + DIST, o, Far{});
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        if (p >= u * P / U && p < (u + 1) * P / U) read_piece(nst, 0, p, sl[0]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -357,14 +366,14 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   for (; kt + NS <= nk; kt += NS) {
     step(kt, Stg0{});
     step(kt + 1, Stg1{});
-    if constexpr (NS > 2) {
-      step(kt + 2, Stg2{});
-      step(kt + 3, Stg3{});
-    }
+    if constexpr (NS > 2) step(kt + 2, Stg2{});
+    if constexpr (NS > 3) step(kt + 3, Stg3{});
   }
   if (kt < nk) step(kt, Stg0{});
   if constexpr (NS > 2) {
     if (kt + 1 < nk) step(kt + 1, Stg1{});
+  }
+  if constexpr (NS > 3) {
     if (kt + 2 < nk) step(kt + 2, Stg2{});
   }
   wait_vmcnt<0>();
@@ -427,10 +436,12 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   }
 }
 
-// 256x256 and 256x128 tiles take 64-deep stages (whole-line A requests; 2048x4096x4096 + residual at
-// 256x128: 75 -> 71 us), the smaller tiles 32-deep ones.
+// 256x128 tiles take 64-deep stages (whole-line A requests, three of 48 KB with the DMAs spread over
+// each step), the others 32-deep ones: two 64-deep stages of a 256x256 tile leave no free slot, and
+// bunching each stage's 16 DMAs a wave into one slice costs more than half-line A requests do
+// (4096x4096x12288 323 -> 318 us, SwiGLU 2048x4096x24576 318 -> 307 us, 2048x4096x6144 92 -> 88 us).
 template <int WM, int WN>
-constexpr int kBKOf = WM * WN >= 8 ? 64 : 32;
+constexpr int kBKOf = WM * WN == 8 ? 64 : 32;
 
 template <int WM, int WN>
 int launch_gemm(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n, int64_t k,
@@ -519,31 +530,12 @@ __global__ __launch_bounds__(256) void splitk_finish(const float* __restrict__ P
 }
 
 // Split-K plan for a GEMM whose 128x128 tiles would fill at most a quarter of the CUs: S slices of kchunk
-// (a multiple of 64, at least 256) columns so that tiles * S roughly covers the chip once.
-// Wide form (*wide = true, 256x256 tiles): where 256x256 tiles fill at most half the CUs and one
-// round of smaller tiles would be chosen instead, S = CUs / tiles slices of at least kWideMinChunk
-// columns give every CU a 256x256 workgroup (~1.4x the flops per CU of a 256x128 one), at the cost
-// of the fp32 partials and the finish pass.  Measured: 2048x12288x4096 (+ residual) 205 -> 198 us in
-// two 6144-deep slices, but 2048x4096x4096 79 -> 95 us in two of 2048, hence the depth floor.
-constexpr int64_t kWideMinChunk = 6144;
-
-bool split_plan(int64_t m, int64_t n, int64_t k, int* splits, int* kchunk, bool* wide) {
+// (a multiple of 64, at least 256) columns so that tiles * S roughly covers the chip once.  (Where
+// 256x128 tiles fill the CUs once, one pass over K beats splitting 256x256 tiles: 2048x12288x4096 +
+// residual 180 us as two 6144-deep slices + the finish, 162 us in one pass.)
+bool split_plan(int64_t m, int64_t n, int64_t k, int* splits, int* kchunk) {
   const int64_t cus = cu_count();
   const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-  *wide = false;
-  const int64_t t44 = ((m + 255) / 256) * ((n + 255) / 256), t42 = ((m + 255) / 256) * ((n + 127) / 128);
-  if (tiles * 4 > cus && t44 * 2 <= cus && t42 <= cus) {
-    int64_t s = cus / t44;
-    if (s > k / kWideMinChunk) s = k / kWideMinChunk;
-    if (s < 2 || t44 * s * 4 < cus * 3) return false;   // the slices must still fill 3/4 of the CUs
-    const int64_t kc = ((k + s - 1) / s + 63) / 64 * 64;
-    s = (k + kc - 1) / kc;
-    if (s < 2) return false;
-    *splits = int(s);
-    *kchunk = int(kc);
-    *wide = true;
-    return true;
-  }
   // measured over the bundle's GEMM shapes: below K = 1024 one pass over K (about 7 us) beats
   // partials plus the finish launch; slices under 256 deep cost more in pipeline fill than they save
   if (k < 1024 || tiles * 4 > cus) return false;   // a quarter of the CUs or more: 64x128 tiles instead
@@ -562,21 +554,19 @@ bool split_plan(int64_t m, int64_t n, int64_t k, int* splits, int* kchunk, bool*
 
 PTB_EXPORT size_t ptb_gemm_bf16_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   int s, kc;
-  bool wide;
-  if (m <= 0 || n <= 0 || k <= 0 || !split_plan(m, n, k, &s, &kc, &wide)) return 0;
+  if (m <= 0 || n <= 0 || k <= 0 || !split_plan(m, n, k, &s, &kc)) return 0;
   return size_t(s) * size_t(m) * size_t(n) * sizeof(float);
 }
 
 PTB_EXPORT int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n,
                                 int64_t k, void* workspace, size_t workspace_bytes, void* stream) {
   int splits, kchunk;
-  bool wide;
-  if (m <= 0 || n <= 0 || k <= 0 || k % 64 || n % 8 || !split_plan(m, n, k, &splits, &kchunk, &wide))
+  if (m <= 0 || n <= 0 || k <= 0 || k % 64 || n % 8 || !split_plan(m, n, k, &splits, &kchunk))
     return ptb_gemm_bf16(a, b, residual, c, m, n, k, stream);   // no split for this shape (or it is refused there)
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
   if (!a || !b || !c || !workspace) return PTB_ERR_NULL;
   if (workspace_bytes < ptb_gemm_bf16_workspace_bytes(m, n, k)) return PTB_ERR_WORKSPACE;
-  const int64_t bt = wide ? 256 : 128;   // tile rows and columns
+  const int64_t bt = 128;   // tile rows and columns
   if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || bt * k * 2 >= (int64_t(1) << 32))
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || !aligned16(workspace) || (residual && !aligned16(residual)))
@@ -586,12 +576,7 @@ PTB_EXPORT int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residu
   const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
   float* part = static_cast<float*>(workspace);
   const dim3 grid(unsigned(tm * tn), unsigned(splits));
-  if (wide)
-    gemm_bf16_kernel<4, 4, false, kSplit, 64><<<grid, dim3(kThreads), 0, s>>>(
-        static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, nullptr, int(m), int(n), int(k),
-        int(tm), int(tn), none, part, kchunk);
-  else
-    gemm_bf16_kernel<2, 2, false, kSplit><<<grid, dim3(kThreads), 0, s>>>(
+  gemm_bf16_kernel<2, 2, false, kSplit><<<grid, dim3(kThreads), 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, nullptr, int(m), int(n), int(k),
         int(tm), int(tn), none, part, kchunk);
   const int64_t mn = m * n;
@@ -614,8 +599,8 @@ PTB_EXPORT int ptb_gemm_swiglu_bf16(const void* a, const void* b, void* c, int64
   const int64_t tm = (m + 255) / 256, tn = inter / 128;
   if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
   const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
-  gemm_bf16_kernel<4, 4, false, kSwiGLU, 64><<<dim3(unsigned(tm * tn)), dim3(kThreads), 0,
-                                              static_cast<hipStream_t>(stream)>>>(
+  gemm_bf16_kernel<4, 4, false, kSwiGLU, kBKOf<4, 4>><<<dim3(unsigned(tm * tn)), dim3(kThreads), 0,
+                                                        static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, static_cast<uint16_t*>(c), int(m),
       int(n), int(k), int(tm), int(tn), none, nullptr, 0);
   return launch_status();

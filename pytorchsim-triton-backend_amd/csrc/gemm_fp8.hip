@@ -62,6 +62,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const float* __restrict__ SW, uint16_t* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
   using G = Cfg<BN>;
   constexpr int NS = G::NS;
+  // stage kt+DIST refills the slot of stage kt+DIST-NS: with a three-stage ring that is stage kt-1,
+  // freed by step kt-1's barrier, so the stage's DMAs spread over both substeps of step kt; with
+  // two stages, stage kt's own slot, freed only by step kt's barrier (the DMAs go in substep 1)
+  constexpr int DIST = NS > 2 ? NS - 1 : NS;
+  constexpr bool kSpread = DIST < NS;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * G::kStageBytes];
 
   const int ntiles = tiles_m * tiles_n;
@@ -153,11 +158,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   for (int d = 0; d < G::kDma; ++d) dma_one(0, d, S0{});
 #pragma unroll
   for (int d = 0; d < G::kDma; ++d) dma_one(1, d, S1{});
-  if constexpr (NS > 2) {
+  if constexpr (DIST > 2) {
 #pragma unroll
     for (int d = 0; d < G::kDma; ++d) dma_one(2, d, S2{});
   }
-  wait_vmcnt<(NS - 1) * G::kDma>();   // stage 0 landed (this wave's part)
+  wait_vmcnt<(DIST - 1) * G::kDma>();   // stage 0 landed (this wave's part)
   __syncthreads();                    // ... and everyone's
   Frags<BN> f0, f1;
 #pragma unroll
@@ -168,6 +173,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // two pieces per MFMA from the start of a substep, so the next substep's first MFMAs find their
   // operands landed instead of waiting on the LDS.  The refill DMAs spread over the whole substep.
   constexpr int U = G::kMfma, P = G::kPieces, D = G::kDma;
+  constexpr int NPRE = [] {   // DMAs of stage kt+DIST issued before step kt's barrier
+    int n = 0;
+    for (int o = 0; o < D; ++o)
+      if (kSpread && o * 2 * U / D < U) ++n;
+    return n;
+  }();
   auto piece_of = [](int q) constexpr {
     const int o = q >> 1;   // operand in first-use order
     const int t = o == 0 ? 0 : (o <= G::WNT ? 4 + (o - 1) : o - G::WNT);
@@ -175,19 +186,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   };
   auto step = [&](int kt, auto stg) __attribute__((always_inline)) {
     constexpr int SI = decltype(stg)::value;   // kt % NS
+    using Far = std::integral_constant<int, (SI + DIST) % NS>;
     const uint8_t* st = smem + SI * G::kStageBytes;
-    // substep 0, with the reads of substep 1 of this stage
+    // substep 0, with the reads of substep 1 of this stage (and, spread, the first of stage
+    // kt+DIST's DMAs)
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       mfma_one(f0, u);
 #pragma unroll
       for (int q = 2 * u; q < 2 * u + 2; ++q)
         if (q < P) read_piece(st, 1, piece_of(q), f1);
+      if constexpr (kSpread) {
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+          if (d * 2 * U / D == u) dma_one(kt + DIST, d, Far{});
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    // stage kt+1 landed (stages up to kt+NS-1 may still be in flight); past the barrier every wave
-    // is done reading stage kt, whose slot takes stage kt+NS
-    wait_vmcnt<(NS - 2) * G::kDma>();
+    // stage kt+1 landed (later stages' DMAs may still be in flight); past the barrier every wave
+    // is done reading stage kt
+    wait_vmcnt<(DIST - 2) * G::kDma + NPRE>();
     __syncthreads();
     const uint8_t* nst = smem + ((SI + 1) % NS) * G::kStageBytes;
     // substep 1, with the reads of the next stage's substep 0 and the refill DMA
@@ -199,7 +217,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         if (q < P) read_piece(nst, 0, piece_of(q), f0);
 #pragma unroll
       for (int d = 0; d < D; ++d)
-        if (d * U / D == u) dma_one(kt + NS, d, stg);
+        if (kSpread ? d * 2 * U / D == U + u : d * U / D == u) dma_one(kt + DIST, d, Far{});
       __builtin_amdgcn_sched_barrier(0);
     }
   };

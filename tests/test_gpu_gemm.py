@@ -122,8 +122,6 @@ def test_gemm_fp8(m, k, n):
 @pytest.mark.parametrize("m,k,n,resid", [
     (128, 2048, 128, False), (8, 2048, 768, False), (512, 2048, 128, True), (32, 3072, 768, False),
     (1000, 4096, 264, True), (64, 1024, 2048, False), (256, 12288, 512, True),
-    # wide form (256x256 tiles, slices 6144+ deep): the down projection; ragged M and N in 4 slices
-    (2048, 12288, 4096, True), (1800, 24576, 2000, True),
 ])
 def test_split_k_gemm(m, k, n, resid):
     """Shapes with few output tiles run split-K (fp32 partials, one finish pass): the same result as
@@ -141,11 +139,12 @@ def test_split_k_gemm(m, k, n, resid):
     assert_close(split, single, RTOL, 2e-2 * scale, f"split-K vs single pass {m}x{k}x{n}")
 
 
-@pytest.mark.parametrize("m,k,n", [(64, 768, 2048), (256, 960, 768), (2048, 4096, 4096)])
+@pytest.mark.parametrize("m,k,n", [(64, 768, 2048), (256, 960, 768), (2048, 4096, 4096), (2048, 12288, 4096),
+                                   (1800, 24576, 2000)])
 def test_no_split_below_1024(m, k, n):
     """Below K = 1024 a single pass over K is faster than partials plus a finish, and so is a GEMM
-    whose 256x256 slices would be under 6144 deep (2048x4096x4096): no workspace is asked for, and
-    the result matches the oracle."""
+    whose 128x128 tiles fill a quarter of the CUs or more (the o- and down projections, and a ragged
+    24576-deep one): no workspace is asked for, and the result matches the oracle."""
     assert _lib.load().ptb_gemm_bf16_workspace_bytes(m, n, k) == 0
     a, b = randn((m, k), 35, std=1 / 32), randn((k, n), 36)
     got = ops.gemm(a.to(DEV), b.to(DEV)).cpu()
