@@ -16,8 +16,10 @@
 // 128-bit fragment reads (16 lanes a phase, 16 different rows) are bank-conflict free.  A stage is
 // two MFMA K substeps of 64: substep 0's MFMAs run with substep 1's fragment reads folded in; the
 // barrier that follows publishes the next stage and frees this one; substep 1's MFMAs then run with
-// the DMA that refills this stage's slot (NS stages ahead) and the reads of the next stage's
-// substep 0.  MFMAs take W as the first operand, so accumulators hold C^T blocks and each lane
+// the reads of the next stage's substep 0.  The refill DMAs of a three-stage ring go into the slot
+// the previous step freed and spread over both substeps (bunched into one substep they queue in the
+// address unit and stall the MFMAs: config 4 85 -> 82 us); a two-stage ring refills the slot its
+// own barrier frees, during substep 1.  MFMAs take W as the first operand, so accumulators hold C^T blocks and each lane
 // stores 4 consecutive columns of a row of C at once.
 #include <type_traits>
 
