@@ -115,6 +115,15 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __r
   const int split = blockIdx.y;
   const int k0 = split * kb;
   const int rows = min(K - k0, kb);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = n0 + 8 * lane;
+  const uint16_t* wp = W + int64_t(k0) * N + col;
+  // the first eight rows' weights go out before the prologue, whose loads and reduction they overlap
+  u32x4 v[8];
+  if (col < N && wave + 28 < rows) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const u32x4*>(wp + int64_t(wave + 4 * u) * N);
+  }
   float r = 0.f;
   if constexpr (MODE == kRms) {
     float sv;
@@ -144,18 +153,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __r
   for (int i = threadIdx.x; i < rows; i += kGemvThreads) xs[i] = prologue<MODE>(x, add, g, r, k0 + i, K);
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int col = n0 + 8 * lane;
   float acc[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) acc[c] = 0.f;
   if (col < N) {
-    const uint16_t* wp = W + int64_t(k0) * N + col;
     int i = wave;
     for (; i + 28 < rows; i += 32) {
-      u32x4 v[8];
+      if (i != wave) {   // the first eight rows are already loaded
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const u32x4*>(wp + int64_t(i + 4 * u) * N);
+        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const u32x4*>(wp + int64_t(i + 4 * u) * N);
+      }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const float xv = xs[i + 4 * u];
