@@ -46,23 +46,30 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // Tile shape: the 4 waves sit 2x2, each owning WM x WN blocks of 32x32, so the workgroup tile is
 // BM = 64*WM rows by BN = 64*WN columns (256x256, 256x128 or 128x128).  A stage holds BK of K:
-// 32 (a 64-byte piece of every A row) in a ring of NS = 4 stages of up to 32 KB, or 64 (a whole
-// 128-byte line of every A row: the L2 serves a request per line, and a half-line request costs a
-// whole one) in a ring of NS = 3 stages of 48 KB (256x128 tiles).  Stage kt + DIST, DIST = NS - 1,
-// refills the slot of stage kt-1, which the barrier of step kt-1 freed, so the stage's DMAs spread
-// over all of step kt's MFMAs.
+// 32 (a 64-byte piece of every A row; 128x128 tiles) in rings of 4 slots, or 64 (a whole 128-byte
+// line of every A row: the L2 serves a request per line, and a half-line request costs a whole
+// one) in rings of 3 slots (256x128 tiles) or of 3 A slots and 2 B slots (256x256 tiles).  Stage
+// kt + DIST, DIST = NSA - 1 = 2 or 3, refills the slots of stage kt-1, which the barrier of step
+// kt-1 freed, so the stage's DMAs spread over all of step kt's MFMAs; with two B slots, its B part
+// waits for the barrier of step kt and spreads over the slice after it.
 template <int WM, int WN, int BKT>
 struct Shape {
   static constexpr int BK = BKT;
-  static constexpr int NS = BK == 64 ? 3 : 4;
-  static constexpr int DIST = NS - 1;
+  // A and B live in rings of their own: NSA and NSB slots.  256x256 tiles with 64-deep stages have
+  // room for three A slots and two B slots only (160 KB), so their B ring refills a slot only after
+  // the barrier that frees it (the "hybrid" schedule below); every other ring is one slot deeper
+  // than its DMA distance.
+  static constexpr bool kHybrid = BK == 64 && WM * WN == 16;
+  static constexpr int NSA = BK == 64 ? 3 : 4;
+  static constexpr int NSB = kHybrid ? 2 : NSA;
+  static constexpr int NS = NSA;
+  static constexpr int DIST = NSA - 1;
   static constexpr int SPS = BK / 16;                    // 16-wide K slices per stage
   static constexpr int BM = 64 * WM, BN = 64 * WN;
   static constexpr int kRowBytes = BK * 2;               // bytes of an A row in a stage
   static constexpr int kChunks = BK / 8;                 // 16-byte chunks of an A row in a stage
   static constexpr int kABytes = BM * BK * 2;
   static constexpr int kBBytes = BK * BN * 2;
-  static constexpr int kStageBytes = kABytes + kBBytes;
   static constexpr int kDmaA = kABytes / 4096;           // buffer_load ... lds per wave per stage
   static constexpr int kDmaB = kBBytes / 4096;
   static constexpr int kDma = kDmaA + kDmaB;
@@ -71,7 +78,8 @@ struct Shape {
   static constexpr int kPieces = WM + 2 * WN;            // LDS reads per wave per K slice
   static constexpr int kBRowsPerKB = 512 / BN;           // B rows per DMA instruction
   static constexpr int kBSlots = BN / 8;                 // 16-byte chunks per B row
-  static_assert(NS * kStageBytes <= 160 * 1024, "the ring fits the LDS");
+  static constexpr int kSmemBytes = NSA * kABytes + NSB * kBBytes;
+  static_assert(kSmemBytes <= 160 * 1024, "the rings fit the LDS");
   static_assert(DIST == NS - 1 && DIST >= 2, "the DMA refills the slot freed a step earlier");
 };
 // A row m keeps chunk c in slot c ^ swz: 4 chunks (BK 32) rotate by (m >> 2) & 3, 8 chunks (BK 64)
@@ -110,9 +118,10 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     uint16_t* __restrict__ C_in, int M_in, int N, int K, int tiles_m, int tiles_n, Groups gp,
     float* __restrict__ part, int kchunk) {
   using Sh = Shape<WM, WN, BKT>;
-  constexpr int BM = Sh::BM, BN = Sh::BN, kABytes = Sh::kABytes, kStageBytes = Sh::kStageBytes;
-  constexpr int BK = Sh::BK, NS = Sh::NS, DIST = Sh::DIST;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStageBytes];
+  constexpr int BM = Sh::BM, BN = Sh::BN, kABytes = Sh::kABytes;
+  constexpr int BK = Sh::BK, NS = Sh::NS, DIST = Sh::DIST, NSA = Sh::NSA, NSB = Sh::NSB;
+  constexpr bool kHybrid = Sh::kHybrid;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Sh::kSmemBytes];
 
   // ---- tile selection
   const uint16_t* A = A_in;
@@ -221,21 +230,30 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
   const uint32_t wave_a = __builtin_amdgcn_readfirstlane(uint32_t(wave * Sh::kDmaA * 1024));
   const uint32_t wave_b = __builtin_amdgcn_readfirstlane(uint32_t(wave * Sh::kDmaB * 1024));
-  // t-th of this wave's DMA instructions of stage kt (A first, then B); stg = kt % NS is a
-  // compile-time constant at every call (the main loop runs NS steps a trip), so the LDS addresses
-  // are constants plus scalar offsets and the fragment reads take them as immediate offsets
-  auto dma_one = [&](int kt, int t, auto stg) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + uint32_t(decltype(stg)::value) * kStageBytes;
-    if (t < Sh::kDmaA)
-      dma16(rsrc_a, st + wave_a + t * 1024, a_voff[t], uint32_t(kt * BK) * 2u);
-    else
-      dma16(rsrc_b, st + kABytes + wave_b + (t - Sh::kDmaA) * 1024, b_voff[t - Sh::kDmaA],
-            uint32_t(kt * BK) * uint32_t(N) * 2u);
+  // t-th of this wave's A (or B) DMA instructions of stage kt into A slot sa (B slot sb); the slots
+  // are compile-time constants at every call (the main loop runs a whole number of ring turns a
+  // trip), so the LDS addresses are constants plus scalar offsets and the fragment reads take them
+  // as immediate offsets
+  const uint32_t lds_b0 = lds0 + uint32_t(NSA * kABytes);
+  auto dma_a = [&](int kt, int t, auto sa) __attribute__((always_inline)) {
+    dma16(rsrc_a, lds0 + uint32_t(decltype(sa)::value) * kABytes + wave_a + t * 1024, a_voff[t],
+          uint32_t(kt * BK) * 2u);
   };
-  using Stg0 = std::integral_constant<int, 0>;
-  using Stg1 = std::integral_constant<int, 1 % NS>;
-  using Stg2 = std::integral_constant<int, 2 % NS>;
-  using Stg3 = std::integral_constant<int, 3 % NS>;
+  auto dma_b = [&](int kt, int t, auto sb) __attribute__((always_inline)) {
+    dma16(rsrc_b, lds_b0 + uint32_t(decltype(sb)::value) * Sh::kBBytes + wave_b + t * 1024, b_voff[t],
+          uint32_t(kt * BK) * uint32_t(N) * 2u);
+  };
+  // the t-th DMA of a stage, A first, then B
+  auto dma_one = [&](int kt, int t, auto sa, auto sb) __attribute__((always_inline)) {
+    if (t < Sh::kDmaA) dma_a(kt, t, sa);
+    else dma_b(kt, t - Sh::kDmaA, sb);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using I4 = std::integral_constant<int, 4>;
+  using I5 = std::integral_constant<int, 5>;
 
   f32x16 acc[WM][WN];
 #pragma unroll
@@ -266,7 +284,7 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int k = 8 * h + 4 * r + jj;  // + 16*ks, which keeps k & 3
-      b_off[j][r] = kABytes + k * (2 * BN) + ((chunk ^ (4 * (k & 3))) << 4) + (q & 1) * 8;
+      b_off[j][r] = k * (2 * BN) + ((chunk ^ (4 * (k & 3))) << 4) + (q & 1) * 8;
     }
   }
 
@@ -277,12 +295,12 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     bf16x8 b[WN];
     i16x4 blo[WN];
   };
-  auto read_piece = [&](const uint8_t* st, int ks, int p, Slice& f) __attribute__((always_inline)) {
+  auto read_piece = [&](const uint8_t* sta, const uint8_t* stb, int ks, int p, Slice& f) __attribute__((always_inline)) {
     if (p < WM) {
-      f.a[p] = *reinterpret_cast<const bf16x8*>(st + a_row_off[p] + (((2 * ks + h) ^ a_sw[p]) << 4));
+      f.a[p] = *reinterpret_cast<const bf16x8*>(sta + a_row_off[p] + (((2 * ks + h) ^ a_sw[p]) << 4));
     } else {
       const int j = (p - WM) >> 1, r = (p - WM) & 1;
-      const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(st + b_off[j][r] + ks * 16 * 2 * BN));
+      const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(stb + b_off[j][r] + ks * 16 * 2 * BN));
       if (r == 0) f.blo[j] = v;
       else f.b[j] = __builtin_bit_cast(bf16x8, i16x8{f.blo[j][0], f.blo[j][1], f.blo[j][2], f.blo[j][3], v[0], v[1], v[2], v[3]});
     }
@@ -300,36 +318,43 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   // stage kt+DIST's DMAs go out one every SLOTS/D MFMAs of step kt (bunched after the barrier they
   // would queue behind each other in the address unit and stall the MFMAs)
   constexpr int SLOTS = SPS * U;
+  // Hybrid schedule (two B slots): stage kt+2's A DMAs spread over step kt before its barrier, into
+  // the A slot step kt-1 freed; its B DMAs go into the B slot step kt's barrier frees, spread over
+  // step kt's last slice (one per two MFMAs, against the A DMAs' one per six).  Splitting the B
+  // DMAs between that slice and the next step's first MFMAs measured no faster.
   constexpr int NPRE = [] {   // DMAs of stage kt+DIST issued before step kt's barrier
     int n = 0;
+    if (kHybrid) return Sh::kDmaA;
     for (int o = 0; o < D; ++o)
       if (o * SLOTS / D < (SPS - 1) * U) ++n;
     return n;
   }();
   const int nk = Kl / BK;
+  const uint8_t* const smem_b = smem + NSA * kABytes;
 #pragma unroll
-  for (int t = 0; t < D; ++t) dma_one(0, t, Stg0{});
+  for (int t = 0; t < D; ++t) dma_one(0, t, I0{}, I0{});
 #pragma unroll
-  for (int t = 0; t < D; ++t) dma_one(1, t, Stg1{});
+  for (int t = 0; t < D; ++t) dma_one(1, t, I1{}, std::integral_constant<int, 1 % NSB>{});
   if constexpr (DIST > 2) {
 #pragma unroll
-    for (int t = 0; t < D; ++t) dma_one(2, t, Stg2{});
+    for (int t = 0; t < D; ++t) dma_one(2, t, I2{}, std::integral_constant<int, 2 % NSB>{});
   }
   wait_vmcnt<(DIST - 1) * D>();     // stage 0 landed (this wave's part)
   __syncthreads();                  // ... and everyone's
   Slice sl[2];
 #pragma unroll
-  for (int p = 0; p < P; ++p) read_piece(smem, 0, p, sl[0]);
+  for (int p = 0; p < P; ++p) read_piece(smem, smem_b, 0, p, sl[0]);
 
-  // Each K step: slices 0 .. SPS-2, each with the next slice's reads and a share of stage
-  // kt+DIST's DMAs folded in; the barrier that publishes stage kt+1 (and frees stage kt's slot for
-  // the next step's DMAs); the last slice with the rest of the DMAs and the reads of stage kt+1's
-  // slice 0 folded in.  sched_barrier(0) pins that interleave, so the matrix core is fed between
-  // memory instructions.
-  auto step = [&](int kt, auto stg) __attribute__((always_inline)) {
-    constexpr int SI = decltype(stg)::value;   // kt % NS
-    using Far = std::integral_constant<int, (SI + DIST) % NS>;
-    const uint8_t* st = smem + SI * kStageBytes;
+  // Each K step: slices 0 .. SPS-2, each with the next slice's reads and a share of the DMAs folded
+  // in; the barrier that publishes stage kt+1 (and frees stage kt's slots); the last slice with the
+  // rest of the DMAs and the reads of stage kt+1's slice 0 folded in.  sched_barrier(0) pins that
+  // interleave, so the matrix core is fed between memory instructions.
+  auto step = [&](int kt, auto sa, auto sb) __attribute__((always_inline)) {
+    constexpr int SA = decltype(sa)::value, SB = decltype(sb)::value;   // kt % NSA, kt % NSB
+    using FarA = std::integral_constant<int, (SA + DIST) % NSA>;
+    using FarB = std::integral_constant<int, (SB + DIST) % NSB>;
+    const uint8_t* sta = smem + SA * kABytes;
+    const uint8_t* stb = smem_b + SB * Sh::kBBytes;
 #pragma unroll
     for (int q = 0; q + 1 < SPS; ++q) {
 #pragma unroll
@@ -337,10 +362,16 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
         mfma_one(sl[q & 1], u);
 #pragma unroll
         for (int p = 0; p < P; ++p)
-          if (kOneReadPerMfma ? p == u : (p >= u * P / U && p < (u + 1) * P / U)) read_piece(st, q + 1, p, sl[(q + 1) & 1]);
+          if (kOneReadPerMfma ? p == u : (p >= u * P / U && p < (u + 1) * P / U)) read_piece(sta, stb, q + 1, p, sl[(q + 1) & 1]);
+        if constexpr (kHybrid) {
 #pragma unroll
-        for (int o = 0; o < D; ++o)
-          if (o * SLOTS / D == q * U + u) dma_one(kt + DIST, o, Far{});
+          for (int o = 0; o < Sh::kDmaA; ++o)
+            if (o * (SPS - 1) * U / Sh::kDmaA == q * U + u) dma_a(kt + DIST, o, FarA{});
+        } else {
+#pragma unroll
+          for (int o = 0; o < D; ++o)
+            if (o * SLOTS / D == q * U + u) dma_one(kt + DIST, o, FarA{}, FarB{});
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -348,33 +379,52 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     // reads stage kt
     wait_vmcnt<(DIST - 2) * D + NPRE>();
     __syncthreads();
-    const uint8_t* nst = smem + ((SI + 1) % NS) * kStageBytes;
+    const uint8_t* nsta = smem + ((SA + 1) % NSA) * kABytes;
+    const uint8_t* nstb = smem_b + ((SB + 1) % NSB) * Sh::kBBytes;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       mfma_one(sl[(SPS - 1) & 1], u);
       // the stage's remaining DMAs, and the next stage's first reads spread evenly
+      if constexpr (kHybrid) {
 #pragma unroll
-      for (int o = 0; o < D; ++o)
-        if (o * SLOTS / D == (SPS - 1) * U + u) dma_one(kt + DIST, o, Far{});
+        for (int o = 0; o < Sh::kDmaB; ++o)
+          if (o * U / Sh::kDmaB == u) dma_b(kt + DIST, o, FarB{});   // into the B slot this barrier freed
+      } else {
+#pragma unroll
+        for (int o = 0; o < D; ++o)
+          if (o * SLOTS / D == (SPS - 1) * U + u) dma_one(kt + DIST, o, FarA{}, FarB{});
+      }
 #pragma unroll
       for (int p = 0; p < P; ++p)
-        if (p >= u * P / U && p < (u + 1) * P / U) read_piece(nst, 0, p, sl[0]);
+        if (p >= u * P / U && p < (u + 1) * P / U) read_piece(nsta, nstb, 0, p, sl[0]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
+  // L steps a trip: a whole number of turns of both rings, so every slot is a constant
+  constexpr int L = kHybrid ? 6 : NSA;
+  auto stepc = [&](int k, auto i) __attribute__((always_inline)) {
+    constexpr int I = decltype(i)::value;
+    step(k, std::integral_constant<int, I % NSA>{}, std::integral_constant<int, I % NSB>{});
+  };
   int kt = 0;
-  for (; kt + NS <= nk; kt += NS) {
-    step(kt, Stg0{});
-    step(kt + 1, Stg1{});
-    if constexpr (NS > 2) step(kt + 2, Stg2{});
-    if constexpr (NS > 3) step(kt + 3, Stg3{});
+  for (; kt + L <= nk; kt += L) {
+    stepc(kt, I0{});
+    stepc(kt + 1, I1{});
+    stepc(kt + 2, I2{});
+    if constexpr (L > 3) stepc(kt + 3, I3{});
+    if constexpr (L > 4) stepc(kt + 4, I4{});
+    if constexpr (L > 5) stepc(kt + 5, I5{});
   }
-  if (kt < nk) step(kt, Stg0{});
-  if constexpr (NS > 2) {
-    if (kt + 1 < nk) step(kt + 1, Stg1{});
+  if (kt < nk) stepc(kt, I0{});
+  if (kt + 1 < nk) stepc(kt + 1, I1{});
+  if constexpr (L > 3) {
+    if (kt + 2 < nk) stepc(kt + 2, I2{});
   }
-  if constexpr (NS > 3) {
-    if (kt + 2 < nk) step(kt + 2, Stg2{});
+  if constexpr (L > 4) {
+    if (kt + 3 < nk) stepc(kt + 3, I3{});
+  }
+  if constexpr (L > 5) {
+    if (kt + 4 < nk) stepc(kt + 4, I4{});
   }
   wait_vmcnt<0>();
 
@@ -436,12 +486,12 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   }
 }
 
-// 256x128 tiles take 64-deep stages (whole-line A requests, three of 48 KB with the DMAs spread over
-// each step), the others 32-deep ones: two 64-deep stages of a 256x256 tile leave no free slot, and
-// bunching each stage's 16 DMAs a wave into one slice costs more than half-line A requests do
-// (4096x4096x12288 323 -> 318 us, SwiGLU 2048x4096x24576 318 -> 307 us, 2048x4096x6144 92 -> 88 us).
+// 256x256 and 256x128 tiles take 64-deep stages (whole-line A requests), 128x128 tiles 32-deep
+// ones.  For 256x256 tiles the 3 A + 2 B slot rings beat 32-deep stages in 4-slot rings (same box:
+// 4096x4096x12288 314.6 -> 306.8 us, SwiGLU 2048x4096x24576 305.7 -> 297.8 us, 2048x4096x6144
+// 89.7 -> 86.5 us).
 template <int WM, int WN>
-constexpr int kBKOf = WM * WN == 8 ? 64 : 32;
+constexpr int kBKOf = WM * WN >= 8 ? 64 : 32;
 
 template <int WM, int WN>
 int launch_gemm(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n, int64_t k,

@@ -188,21 +188,23 @@ def test_gemm_swiglu_fused(m, k, inter):
 
 
 @pytest.mark.parametrize("m,k,n,resid", [
-    (4096, 1088, 4096, False),   # 256x256 tiles, 34 steps of 32: the four-step loop's two-step remainder
+    (4096, 1088, 4096, False),   # 256x256 tiles, 17 steps of 64: the six-step loop's five-step remainder
+    (4096, 832, 4096, True),     # 256x256 tiles, 13 steps: a one-step remainder
     (2048, 4160, 4096, True),    # 256x128 tiles, 65 steps of 64: the three-step loop's two-step remainder
     (2048, 4224, 4096, True),    # 256x128 tiles, 66 steps: no remainder (4096 deep, 64 steps, leaves one)
 ])
 def test_gemm_odd_step_count(m, k, n, resid):
-    """The main loop runs as many K steps a trip as its ring has stages (four 32-deep for 256x256
-    tiles, three 64-deep for 256x128), so a step count that is not a multiple ends on remainder steps,
-    which must still read the right stages and drain the DMA stream."""
+    """The main loop runs a whole number of turns of its rings a trip (six 64-deep steps for 256x256
+    tiles, whose rings hold three A and two B stages; three for 256x128), so a step count that is
+    not a multiple ends on remainder steps, which must still read the right slots and drain the DMA
+    stream."""
     std = 1.0 / 64.0
     got, want = run_gemm(m, k, n, 1, std, std, resid)
     assert_close(got, want, RTOL, ATOL * rms(want), f"gemm {m}x{k}x{n}")
 
 
 def test_gemm_swiglu_odd_step_count():
-    """The SwiGLU-fused GEMM with K = 1088 (34 steps of 32: a remainder of two) equals the GEMM +
+    """The SwiGLU-fused GEMM with K = 1088 (17 steps of 64: a remainder of five) equals the GEMM +
     silu_mul pair."""
     a = randn((2048, 1088), 43, std=1 / 16).to(DEV)
     b = randn((1088, 2 * 6144), 44, std=1 / 4).to(DEV)
