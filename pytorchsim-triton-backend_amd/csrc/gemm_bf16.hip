@@ -428,61 +428,100 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   }
   wait_vmcnt<0>();
 
-  if constexpr (MODE == kSwiGLU) {
-    // pair jp of this wave: gate acc[i][2jp], up acc[i][2jp+1] -> output columns
-    // n0 + 32*(wn*WN/2 + jp) + 8*(r/4) + 4*(lane/32) + r%4 of C [M, N/2]
-    const int Nout = N / 2;
+  // ---- epilogue: accumulator (i, j, r) of lane holds C row m0 + wm*BM/2 + i*32 + lane%32,
+  //      column n0 + wn*BN/2 + j*32 + 8*(r/4) + 4*(lane/32) + r%4: 4 consecutive columns per r/4
+  if constexpr (MODE == kSplit) {
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
       const int row = m0 + wm * (BM / 2) + i * 32 + fr;
       if (row >= M) continue;
 #pragma unroll
-      for (int jp = 0; jp < WN / 2; ++jp) {
+      for (int j = 0; j < WN; ++j) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int col = n0 + 32 * (wn * (WN / 2) + jp) + 8 * g + 4 * h;
-          float o[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float gv = bf16_to_f32(f32_to_bf16(acc[i][2 * jp][4 * g + e]));
-            const float uv = bf16_to_f32(f32_to_bf16(acc[i][2 * jp + 1][4 * g + e]));
-            o[e] = (gv / (__builtin_amdgcn_exp2f(-gv * 1.4426950408889634f) + 1.0f)) * uv;
-          }
-          *reinterpret_cast<u32x2*>(C + int64_t(row) * Nout + col) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+          const int col = n0 + wn * (BN / 2) + j * 32 + 8 * g + 4 * h;
+          if (col >= N) continue;  // N % 8 == 0: a 4-column group is all in or all out
+          *reinterpret_cast<f32x4v*>(part + int64_t(blockIdx.y) * M * N + int64_t(row) * N + col) =
+              f32x4v{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
         }
       }
     }
     return;
   }
-
-  // ---- epilogue: accumulator (i, j, r) of lane -> C row m0 + wm*BM/2 + i*32 + lane%32,
-  //      column n0 + wn*BN/2 + j*32 + 8*(r/4) + 4*(lane/32) + r%4: 4 consecutive columns per r/4
+  // Plain, grouped and SwiGLU tiles leave through the LDS, which is free now (every DMA has landed
+  // and, past the barrier, no wave reads a stage): a wave writes one 32-row block of its fp32
+  // results (WJ 32-column blocks; value(i, jj, g) gives the 4 columns 8g + 4*(lane/32) .. +3 of
+  // block jj for row lane%32) into a private, padded region and reads it back 4 columns a lane, so
+  // each store writes whole rows of its block (in the accumulator layout one store instruction
+  // writes 16 bytes into each of 32 rows, which took 12% of a 256x256 tile's time) and the
+  // residual is read the same way.  The region is the wave's own and LDS operations of a wave
+  // complete in order, so no barrier separates its writes from its reads.  Rows past M and columns
+  // past `cols` fall outside the buffer resources (stores dropped, loads 0): no branches.
+  __syncthreads();
+  auto store_staged = [&](auto wj, auto value, uint16_t* out, int ldc, int cols, int col0) __attribute__((always_inline)) {
+    constexpr int WJ = decltype(wj)::value;
+    constexpr int WC = WJ * 32;           // columns of a wave's block
+    constexpr int kPitch = WC * 4 + 16;   // bytes per staged row: rows start 4 banks apart
+    constexpr int LPR = WC / 4;           // lanes per row, 4 columns each
+    constexpr int RPI = 64 / LPR;         // rows per instruction
+    static_assert(4 * 32 * kPitch <= Sh::kSmemBytes, "the staging regions fit in the ring's LDS");
+    uint8_t* const stage = smem + wave * (32 * kPitch);
+    const int rl = lane / LPR, c4 = lane % LPR;
+    const int gcol = col0 + 4 * c4;
+    const uint32_t tile_bytes = uint32_t(min(BM, M - m0)) * uint32_t(ldc) * 2u;
+    const __amdgpu_buffer_rsrc_t rsrc_c =
+        __builtin_amdgcn_make_buffer_rsrc(out + int64_t(m0) * ldc, 0, tile_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc_r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(RESID ? R + int64_t(m0) * ldc : out), 0, tile_bytes,
+                                          0x00020000);
 #pragma unroll
-  for (int i = 0; i < WM; ++i) {
-    const int row = m0 + wm * (BM / 2) + i * 32 + fr;
-    if (row >= M) continue;
+    for (int i = 0; i < WM; ++i) {
+      const int r0 = wm * (BM / 2) + i * 32 + rl;   // tile row of this lane's first row
+      uint32_t voff[32 / RPI];
 #pragma unroll
-    for (int j = 0; j < WN; ++j) {
+      for (int t = 0; t < 32 / RPI; ++t)
+        voff[t] = gcol < cols ? uint32_t(((r0 + t * RPI) * ldc + gcol) * 2) : 0x80000000u;
+      u32x2 rr[32 / RPI];
+      if constexpr (RESID) {   // issued before the staging writes so their latency overlaps them
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int col = n0 + wn * (BN / 2) + j * 32 + 8 * g + 4 * h;
-        if (col >= N) continue;  // N % 8 == 0: a 4-column group is all in or all out
-        const int64_t o = int64_t(row) * N + col;
-        float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1], v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
-        if constexpr (MODE == kSplit) {
-          *reinterpret_cast<f32x4v*>(part + int64_t(blockIdx.y) * M * N + o) = f32x4v{v0, v1, v2, v3};
-          continue;
-        }
+        for (int t = 0; t < 32 / RPI; ++t) rr[t] = __builtin_amdgcn_raw_buffer_load_b64(rsrc_r, voff[t], 0, 0);
+      }
+#pragma unroll
+      for (int jj = 0; jj < WJ; ++jj)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4v*>(stage + fr * kPitch + (jj * 32 + 8 * g + 4 * h) * 4) = value(i, jj, g);
+#pragma unroll
+      for (int t = 0; t < 32 / RPI; ++t) {
+        f32x4v v = *reinterpret_cast<const f32x4v*>(stage + (t * RPI + rl) * kPitch + c4 * 16);
         if constexpr (RESID) {
-          const u32x2 rr = *reinterpret_cast<const u32x2*>(R + o);
-          v0 += bf16_lo(rr[0]);
-          v1 += bf16_hi(rr[0]);
-          v2 += bf16_lo(rr[1]);
-          v3 += bf16_hi(rr[1]);
+          v[0] += bf16_lo(rr[t][0]);
+          v[1] += bf16_hi(rr[t][0]);
+          v[2] += bf16_lo(rr[t][1]);
+          v[3] += bf16_hi(rr[t][1]);
         }
-        *reinterpret_cast<u32x2*>(C + o) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, rsrc_c,
+                                              voff[t], 0, 0);
       }
     }
+  };
+  if constexpr (MODE == kSwiGLU) {
+    // pair jp of this wave: gate acc[i][2jp], up acc[i][2jp+1] -> output columns
+    // n0 + 32*(wn*WN/2 + jp) + 8*(r/4) + 4*(lane/32) + r%4 of C [M, N/2]
+    store_staged(std::integral_constant<int, WN / 2>{}, [&](int i, int jp, int g) __attribute__((always_inline)) {
+      f32x4v o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float gv = bf16_to_f32(f32_to_bf16(acc[i][2 * jp][4 * g + e]));
+        const float uv = bf16_to_f32(f32_to_bf16(acc[i][2 * jp + 1][4 * g + e]));
+        o[e] = (gv / (__builtin_amdgcn_exp2f(-gv * 1.4426950408889634f) + 1.0f)) * uv;
+      }
+      return o;
+    }, C, N / 2, N / 2, n0 + wn * (BN / 4));
+  } else {
+    store_staged(std::integral_constant<int, WN>{}, [&](int i, int j, int g) __attribute__((always_inline)) {
+      return f32x4v{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+    }, C, N, N, n0 + wn * (BN / 2));
   }
 }
 
