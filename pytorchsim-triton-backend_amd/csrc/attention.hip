@@ -387,21 +387,40 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     block(kb + 1, std::integral_constant<int, 1>{});
   }
   if (kb < nb) block(kb, std::integral_constant<int, 0>{});
+  __syncthreads();   // every wave is done with the last block's stage: the LDS is free
   if (!active) return;
 
   const float l = pair32_sum(w.l);
   const float inv = 1.f / l;
-  // O [batch*hq, S, D] (head-major), or with o_tokens O [batch, S, hq, D] (token-major)
-  uint16_t* orow = o_tokens ? O + ((int64_t(b) * S + qi) * hq + (kvh * G + g)) * D : op + int64_t(qi) * D;
+  // The output tile leaves through the LDS, 64 of the 128 dims at a time: the lane holding query
+  // row fr writes its 8 four-dim pieces into the wave's private, padded region, then each lane
+  // reads 16 bytes of one row back, so a store instruction writes 8 rows' 128-byte segments (in
+  // the accumulator layout it writes 8 bytes into each of 32 rows).  The region is the wave's own
+  // and LDS operations of a wave complete in order, so no barrier separates its writes from its
+  // reads.  O is [batch*hq, S, D] (head-major), or with o_tokens [batch, S, hq, D] (token-major).
+  constexpr int kOPitch = 64 * 2 + 16;   // bytes per staged half row
+  static_assert(WAVES * 32 * kOPitch <= 2 * kStageBytes, "the staging regions fit in the stages' LDS");
+  uint8_t* const ostage = smem + wave * (32 * kOPitch);
+  const int rl = lane >> 3, c8 = lane & 7;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int d0 = dt * 32 + 8 * g4 + 4 * h;
-      const u32x2 o = u32x2{pack_bf16x2(w.acc[dt][4 * g4] * inv, w.acc[dt][4 * g4 + 1] * inv),
-                            pack_bf16x2(w.acc[dt][4 * g4 + 2] * inv, w.acc[dt][4 * g4 + 3] * inv)};
-      *reinterpret_cast<u32x2*>(orow + d0) = o;
+    for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int dt = 2 * hf + dd;
+        *reinterpret_cast<u32x2*>(ostage + fr * kOPitch + (dd * 32 + 8 * g4 + 4 * h) * 2) =
+            u32x2{pack_bf16x2(w.acc[dt][4 * g4] * inv, w.acc[dt][4 * g4 + 1] * inv),
+                  pack_bf16x2(w.acc[dt][4 * g4 + 2] * inv, w.acc[dt][4 * g4 + 3] * inv)};
+      }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = 8 * t + rl, q = qw0 + r;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ostage + r * kOPitch + c8 * 16);
+      uint16_t* orow = o_tokens ? O + ((int64_t(b) * S + q) * hq + (kvh * G + g)) * D : op + int64_t(q) * D;
+      *reinterpret_cast<u32x4*>(orow + 64 * hf + 8 * c8) = v;
     }
+  }
 }
 
 }  // namespace
