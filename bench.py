@@ -13,6 +13,7 @@ figure at top level and, under ``configs``, one entry per BASELINE config (a bou
 workload, on all host threads and on one thread).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm_bf16,...]
+       python bench.py --decode-sweep   (decode attention over cache lengths; its own JSON line)
 """
 from __future__ import annotations
 
@@ -248,6 +249,42 @@ def bench_attention_decode(steps, warmup):
                          "frac": gbs / PEAK_HBM_GBS}}
 
 
+def decode_sweep(steps, warmup):
+    """Decode attention over cache lengths 512 .. 32768 (8 kv heads, 4 query rows each, D 128): time
+    per call, GB/s and the fraction of 8 TB/s at each length, cycling enough K/V copies (>= 400 MB)
+    that every call reads HBM.  A time that does not grow with the bytes names launch and latency,
+    not bandwidth, as the limit."""
+    import torch
+    from ptb_amd import _lib, ops
+
+    hkv, g, d = 8, 4, 128
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(hkv, g, d, generator=gen).to(torch.bfloat16).cuda()
+    o = torch.empty_like(q)
+    rows = []
+    for s in (512, 1024, 2048, 4096, 8192, 16384, 32768):
+        copies = max(3, int(400e6 // (2 * 2 * hkv * s * d)))
+        kvs = [(torch.randn(hkv, s, d, generator=gen).to(torch.bfloat16).cuda(),
+                torch.randn(hkv, s, d, generator=gen).to(torch.bfloat16).cuda()) for _ in range(copies)]
+        work = torch.empty(max(1, _lib.load().ptb_attn_decode_workspace_bytes(hkv, g, s)), dtype=torch.uint8,
+                           device="cuda")
+        it = [0]
+
+        def step():
+            k, v = kvs[it[0] % copies]
+            it[0] += 1
+            ops.attention_decode(q, k, v, out=o, workspace=work)
+
+        ms, _ = timed(step, steps * 4, warmup)
+        nbytes = 2.0 * (2 * hkv * s * d + 2 * hkv * g * d)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append({"seq": s, "us": ms * 1e3, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS, "copies": copies})
+        log(f"[sweep] S={s}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+        del kvs
+        torch.cuda.empty_cache()
+    return rows
+
+
 def bench_decode_layer(steps, warmup):
     """qwen3_8b_layer_decode_1x4096_bf16: the bundle's 8-launch decode layer over a 4096-token cache
     (issued here as 5 fused steps, 10 kernels: each GEMV and the attention keep their finish pass)."""
@@ -466,6 +503,8 @@ def main(argv=None):
     ap.add_argument("--only", default="", help="comma-separated subset of " + ",".join(BENCHES))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-driver", help="run one kernel 5x plus a 256 MiB copy (for rocprofv3 --pmc) and exit")
+    ap.add_argument("--decode-sweep", action="store_true",
+                    help="time decode attention over cache lengths 512..32768, print one JSON line and exit")
     ap.add_argument("--settle", type=float, default=SETTLE_S,
                     help="seconds of untimed back-to-back launches before the warmup steps")
     args = ap.parse_args(argv)
@@ -486,6 +525,9 @@ def main(argv=None):
     from ptb_amd import _lib
 
     _lib.load()   # fail loudly when the HIP library is missing
+    if args.decode_sweep:
+        print(json.dumps({"decode_sweep": decode_sweep(args.steps, args.warmup)}), flush=True)
+        return 0
     names = [n for n in (args.only.split(",") if args.only else BENCHES) if n]
     results = {}
     for name in names:
