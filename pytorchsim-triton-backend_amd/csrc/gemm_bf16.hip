@@ -38,6 +38,9 @@ constexpr int kThreads = 256;
 constexpr int kGroupM = 8;
 // K past the end the DMA stream may address (the deepest ring: 4 stages of 32 or 2 of 64)
 constexpr int kRunAhead = 128;
+// Widest C (columns) the epilogue addresses: a 256-row tile of it stays within 2^31 bytes, so its
+// 32-bit store offsets, and the 0x80000000 that marks a column outside C, stay in range.
+constexpr int64_t kMaxOutCols = int64_t(1) << 22;
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -480,7 +483,7 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
       uint32_t voff[32 / RPI];
 #pragma unroll
       for (int t = 0; t < 32 / RPI; ++t)
-        voff[t] = gcol < cols ? uint32_t(((r0 + t * RPI) * ldc + gcol) * 2) : 0x80000000u;
+        voff[t] = gcol < cols ? (uint32_t(r0 + t * RPI) * uint32_t(ldc) + uint32_t(gcol)) * 2u : 0x80000000u;
       u32x2 rr[32 / RPI];
       if constexpr (RESID) {   // issued before the staging writes so their latency overlaps them
 #pragma unroll
@@ -568,7 +571,8 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
   if (k % 64 || n % 8) return PTB_ERR_UNSUPPORTED;
   // buffer offsets are 32-bit: B and one 256-row panel of A must each stay under 4 GB
-  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(256) * k * 2 >= (int64_t(1) << 32))
+  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(256) * k * 2 >= (int64_t(1) << 32) ||
+      n > kMaxOutCols)
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
@@ -682,7 +686,8 @@ PTB_EXPORT int ptb_gemm_swiglu_bf16(const void* a, const void* b, void* c, int64
   if (k == 0 || k % 64 || inter % 128) return PTB_ERR_UNSUPPORTED;
   const int64_t n = 2 * inter;
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
-  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(256) * k * 2 >= (int64_t(1) << 32))
+  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(256) * k * 2 >= (int64_t(1) << 32) ||
+      n > kMaxOutCols)
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c)) return PTB_ERR_ALIGN;
   const int64_t tm = (m + 255) / 256, tn = inter / 128;
@@ -703,7 +708,8 @@ PTB_EXPORT int ptb_grouped_gemm_bf16(const void* a, const void* b, const int32_t
   if (!a || !b || !group || !start || !rows || !c) return PTB_ERR_NULL;
   if (k == 0 || k % 64 || n % 8 || nprog > kMaxPrograms) return PTB_ERR_UNSUPPORTED;
   if (weight_stride < k * n || a_rows > 0x7fffffff || ntab > 0x7fffffff || nweights > 0x7fffffff) return PTB_ERR_SHAPE;
-  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(128) * k * 2 >= (int64_t(1) << 32))
+  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(128) * k * 2 >= (int64_t(1) << 32) ||
+      n > kMaxOutCols)
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (weight_stride % 8)) return PTB_ERR_ALIGN;
   // a bound on the row tiles of every program together: each program's rows lie inside A

@@ -273,7 +273,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       const f32x4v v = *reinterpret_cast<const f32x4v*>(stage + (t * RPI + rl) * kPitch + c4 * 16);
       const float v0 = (v.x * sa[t]) * sw[0], v1 = (v.y * sa[t]) * sw[1];
       const float v2 = (v.z * sa[t]) * sw[2], v3 = (v.w * sa[t]) * sw[3];
-      const uint32_t off = gcol < N ? uint32_t(((r0 + t * RPI) * N + gcol) * 2) : 0x80000000u;
+      const uint32_t off = gcol < N ? (uint32_t(r0 + t * RPI) * uint32_t(N) + uint32_t(gcol)) * 2u : 0x80000000u;
       __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)}, rsrc_c, off, 0, 0);
     }
   }
@@ -515,6 +515,9 @@ int fp8_check(const void* aq, const float* sa, const void* wq_t, const float* sw
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
   if (k % 128 || n % 16) return PTB_ERR_UNSUPPORTED;
   if (int64_t(BM) * k >= (int64_t(1) << 32)) return PTB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
+  // a 256-row tile of C within 2^31 bytes: the epilogue's 32-bit store offsets, and the 0x80000000
+  // that marks a column outside C, stay in range
+  if (n > (int64_t(1) << 22)) return PTB_ERR_UNSUPPORTED;
   if (!aligned16(aq) || !aligned16(wq_t) || !aligned16(sw) || (reinterpret_cast<uintptr_t>(c) & 7u))
     return PTB_ERR_ALIGN;
   return 1;   // go on

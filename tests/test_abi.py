@@ -97,6 +97,10 @@ def test_32bit_buffer_offset_limits_refused(lib):
     assert lib.ptb_gemm_swiglu_bf16(P16, P16, P16, 256, 16384, 65536, None) == _lib.PTB_ERR_UNSUPPORTED
     # one 256-row panel of A at 4 GiB: 256 * 8388608 * 2 bytes
     assert lib.ptb_gemm_bf16(P16, P16, None, P16, 256, 8, 8388608, None) == _lib.PTB_ERR_UNSUPPORTED
+    # C wider than 2^22 columns: a 256-row tile of it would pass 2^31 bytes of store offsets
+    assert lib.ptb_gemm_bf16(P16, P16, None, P16, 256, (1 << 22) + 8, 64, None) == _lib.PTB_ERR_UNSUPPORTED
+    assert lib.ptb_gemm_swiglu_bf16(P16, P16, P16, 256, (1 << 21) + 128, 64, None) == _lib.PTB_ERR_UNSUPPORTED
+    assert lib.ptb_gemm_fp8_scaled(P16, P16, P16, P16, P16, 256, (1 << 22) + 16, 128, None) == _lib.PTB_ERR_UNSUPPORTED
     # fp8: a 256-row panel of e4m3 A at 4 GiB
     assert lib.ptb_gemm_fp8_scaled(P16, P16, P16, P16, P16, 256, 16, 1 << 24, None) == _lib.PTB_ERR_UNSUPPORTED
     # attention: one kv head's K at 4 GiB (2^24 keys x 256 bytes)
