@@ -149,7 +149,9 @@ int ptb_add_scalar_bf16(const void* x, void* y, int64_t n, float s, void* stream
 int ptb_slice_add_bf16(const void* x, float* out, int64_t first, int64_t count, float s, void* stream);
 
 /* Dense GEMM, row-major: C[m,n] = bf16( sum_k A[m,k] * B[k,n] (+ float(R[m,n])) ), fp32 accumulation.
- * residual may be NULL.  Requires k % 64 == 0 and n % 8 == 0; m is free.
+ * residual may be NULL.  Requires k % 64 == 0 and n % 8 == 0; m is free.  Operands are addressed
+ * with 32-bit byte offsets: (k + 128) * n * 2 and 256 * k * 2 below 4 GiB and n <= 2^22, else
+ * PTB_ERR_UNSUPPORTED.
  * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/01_..._fused_mm_ckb6aiys_triton.py:18-97 (and
  *           03, 09), the residual epilogues 08_..._utuycvlm_triton.py:18-99 and
  *           11_..._fjjozd2g_triton.py:18-66, and the gemm_<M>x<K>x<N>_bf16 bundle kernels. */
@@ -169,7 +171,8 @@ int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residual, void* c
  * (gate columns [0, inter), up columns [inter, 2*inter)), C [m, inter] = bf16( silu(g) * u ) with
  * g, u = bf16(A . B[:, j]) and bf16(A . B[:, inter + j]) and silu(g) = g / (1 + e^-g), fp32 --
  * bit for bit what ptb_gemm_bf16 followed by ptb_silu_mul_bf16 give, without the [m, 2*inter]
- * intermediate.  k % 64 == 0, inter % 128 == 0.
+ * intermediate.  k % 64 == 0, inter % 128 == 0, 2 * inter <= 2^22 (and the ptb_gemm_bf16 offset
+ * limits for n = 2 * inter).
  * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/09_..._fused__to_copy_add_mean_mm_mul_pow_rsqrt_5ojlpnva's
  *           gate_up product together with 10_..._fused__to_copy_mul_silu_slice_ktzl5s2h (the pair
  *           ptb_amd.qwen3's prefill layer launches back to back; the bundle's manifests keep them apart). */
@@ -189,7 +192,7 @@ int ptb_quant_weight_e4m3(const float* w, void* wq_t, float* scale, int64_t k, i
                           void* stream);
 
 /* fp8-weight GEMM: C[m,n] = bf16( (sum_k aq[m,k] * wq_t[n,k]) * sa[m] * sw[n] ), e4m3 operands,
- * fp32 accumulation.  Requires k % 128 == 0 and n % 16 == 0.
+ * fp32 accumulation.  Requires k % 128 == 0 and n % 16 == 0, 256 * k below 4 GiB and n <= 2^22.
  * Semantics: tests/cases/mechanism/ops/ops_fp8_e4m3_dot.py:13-60 and
  *            tests/cases/workloads/int8_dequant_matmul.py:59-69 (scale epilogue). */
 int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* wq_t, const float* sw, void* c,
