@@ -84,6 +84,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+  // the tile's row scales: one load a thread, issued ahead of the prologue's DMAs and held in a
+  // register until the epilogue puts it in LDS, so the epilogue waits on no global load per
+  // 32-row block (and nothing waits on this load before then)
+  static_assert(BM == kThreads, "one row scale per thread");
+  __shared__ float sa_tile[BM];
+  const float sa_mine = SA[min(m0 + tid, M - 1)];
 
   // loaders: rows past M (A) or N (W) read as zero through num_records; stages past K read other
   // rows' bytes or zeros into slots nobody reads any more (the DMA stream runs ahead without a branch)
@@ -244,6 +250,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // same for the whole tile.  The region is the wave's own and LDS operations of a wave complete in
   // order, so no barrier separates its writes from its reads.  Rows past M and columns past N fall
   // outside the output's buffer resource (stores dropped), so the stores need no branches.
+  sa_tile[tid] = sa_mine;
   __syncthreads();
   constexpr int WC = G::WNT * 32;       // columns of a wave's block
   constexpr int kPitch = WC * 4 + 16;   // bytes per staged row: rows start 4 banks apart
@@ -261,7 +268,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int r0 = wm * 128 + i * 32 + rl;   // tile row of this lane's first row
     float sa[32 / RPI];
 #pragma unroll
-    for (int t = 0; t < 32 / RPI; ++t) sa[t] = SA[min(m0 + r0 + t * RPI, M - 1)];
+    for (int t = 0; t < 32 / RPI; ++t) sa[t] = sa_tile[r0 + t * RPI];
 #pragma unroll
     for (int j = 0; j < G::WNT; ++j)
 #pragma unroll
