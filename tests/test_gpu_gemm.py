@@ -64,6 +64,25 @@ def test_gemm_ragged(m, k, n):
     assert_close(got, want, RTOL, ATOL, f"gemm {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("m,k,n", [
+    (4000, 256, 4000),    # 256x256 tiles, ragged in M and N
+    (2000, 512, 4088),    # 256x128 tiles, ragged in M and N
+])
+def test_gemm_ragged_residual_stays_inside_c(m, k, n):
+    """The epilogue stages each tile through the LDS and masks rows past M and columns past N with
+    buffer resources: on ragged last tiles the residual sum is right and nothing lands past C (a
+    NaN-filled guard after C's last element stays NaN)."""
+    a = randn((m, k), 5)
+    b = randn((k, n), 6, std=1.0 / k ** 0.5)
+    r = randn((m, n), 7)
+    guard = torch.full((m * n + 8192,), float("nan"), dtype=torch.bfloat16, device=DEV)
+    c = guard[: m * n].view(m, n)
+    ops.gemm(a.to(DEV), b.to(DEV), r.to(DEV), out=c)
+    assert bool(guard[m * n:].isnan().all()), "the GEMM wrote past C"
+    rows = sample_rows(m, 5)
+    assert_close(c.cpu()[rows], oracle.gemm(a[rows], b, r[rows]), RTOL, ATOL, f"gemm+R {m}x{k}x{n}")
+
+
 def test_gemm_bundle_inputs_exact_products():
     """bf16 operands from the bundle's make_inputs draw (randn): small enough that the fp32
     accumulation is exact for small K -> bit-exact output (tests/baselines/tpuv6e.txt:162 records
@@ -103,7 +122,9 @@ def test_quant_weight_exact(k, n, seed):
 
 @pytest.mark.parametrize("m,k,n", [(2048, 12288, 4096), (1, 128, 16), (300, 256, 272), (257, 1024, 512),
                                    (4096, 1152, 4096),   # 256x256 tiles, two-stage ring, an odd step count
-                                   (2048, 896, 4096)])   # 256x128 tiles, 7 steps: a one-step remainder
+                                   (2048, 896, 4096),    # 256x128 tiles, 7 steps: a one-step remainder
+                                   (4000, 256, 4000),    # 256x256 tiles, ragged in M and N
+                                   (2000, 512, 4080)])   # 256x128 tiles, ragged in M and N
 def test_gemm_fp8(m, k, n):
     """activations bf16 ~N(0,1) quantised per token, weights from N(0,0.02)
     quantised per output channel; the GPU GEMM and the oracle see the same quantised operands."""
