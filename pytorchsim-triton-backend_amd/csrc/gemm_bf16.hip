@@ -48,21 +48,22 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // Tile shape: the 4 waves sit 2x2, each owning WM x WN blocks of 32x32, so the workgroup tile is
-// BM = 64*WM rows by BN = 64*WN columns (256x256, 256x128 or 128x128).  A stage holds BK of K:
-// 32 (a 64-byte piece of every A row; 128x128 tiles) in rings of 4 slots, or 64 (a whole 128-byte
-// line of every A row: the L2 serves a request per line, and a half-line request costs a whole
-// one) in rings of 3 slots (256x128 tiles) or of 3 A slots and 2 B slots (256x256 tiles).  Stage
+// BM = 64*WM rows by BN = 64*WN columns (256x256, 256x192, 256x128, 128x128 or 64x128).  A stage
+// holds BK of K: 32 (a 64-byte piece of every A row; 128x128 and 64x128 tiles) in rings of 4 slots,
+// or 64 (a whole 128-byte line of every A row: the L2 serves a request per line, and a half-line
+// request costs a whole one) in rings of 3 slots (256x128 tiles) or of 3 A slots and 2 B slots
+// (256x256, 256x192).  Stage
 // kt + DIST, DIST = NSA - 1 = 2 or 3, refills the slots of stage kt-1, which the barrier of step
 // kt-1 freed, so the stage's DMAs spread over all of step kt's MFMAs; with two B slots, its B part
 // waits for the barrier of step kt and spreads over the slice after it.
 template <int WM, int WN, int BKT>
 struct Shape {
   static constexpr int BK = BKT;
-  // A and B live in rings of their own: NSA and NSB slots.  256x256 tiles with 64-deep stages have
-  // room for three A slots and two B slots only (160 KB), so their B ring refills a slot only after
-  // the barrier that frees it (the "hybrid" schedule below); every other ring is one slot deeper
-  // than its DMA distance.
-  static constexpr bool kHybrid = BK == 64 && WM * WN == 16;
+  // A and B live in rings of their own: NSA and NSB slots.  256x256 and 256x192 tiles with 64-deep
+  // stages have room for three A slots and two B slots only (160 / 144 KB), so their B ring
+  // refills a slot only after the barrier that frees it (the "hybrid" schedule below); every other
+  // ring is one slot deeper than its DMA distance.
+  static constexpr bool kHybrid = BK == 64 && WM * WN >= 12;
   static constexpr int NSA = BK == 64 ? 3 : 4;
   static constexpr int NSB = kHybrid ? 2 : NSA;
   static constexpr int NS = NSA;
@@ -79,16 +80,23 @@ struct Shape {
   static constexpr int kARowsPerKB = 1024 / kRowBytes;   // A rows per DMA instruction
   static constexpr int kMfma = WM * WN;                  // MFMAs per wave per 16-wide K slice
   static constexpr int kPieces = WM + 2 * WN;            // LDS reads per wave per K slice
-  static constexpr int kBRowsPerKB = 512 / BN;           // B rows per DMA instruction
   static constexpr int kBSlots = BN / 8;                 // 16-byte chunks per B row
   static constexpr int kSmemBytes = NSA * kABytes + NSB * kBBytes;
   static_assert(kSmemBytes <= 160 * 1024, "the rings fit the LDS");
+  static_assert(kABytes % 4096 == 0 && kBBytes % 4096 == 0, "whole 1 KB DMA instructions per wave");
   static_assert(DIST == NS - 1 && DIST >= 2, "the DMA refills the slot freed a step earlier");
 };
 // A row m keeps chunk c in slot c ^ swz: 4 chunks (BK 32) rotate by (m >> 2) & 3, 8 chunks (BK 64)
 // by (m >> 1) & 7; either way the 16 rows a 16-lane phase reads land in 16 distinct bank groups.
 template <int BKT>
 __device__ __forceinline__ int a_swz(int m) { return BKT == 64 ? (m >> 1) & 7 : (m >> 2) & 3; }
+// B row k keeps chunk c in slot c ^ b_swz(k).  A transposing read takes 64 bytes of each of 4
+// consecutive rows k0..k0+3 (k0 % 4 == 0) per 32 lanes.  Rows of 512 or 256 bytes all start at
+// bank 0, so the rows shift by 64 bytes each: 4 * (k & 3).  Rows of 384 bytes (BN 192) start 32
+// banks apart in turn, so only k0+2 and k0+3 shift, by 64 bytes: 4 * ((k >> 1) & 1).  Either way
+// the 4 rows' 64 bytes take 64 distinct banks, and the XOR stays inside the row's chunks.
+template <int BN>
+__device__ __forceinline__ int b_swz(int k) { return BN == 192 ? 4 * ((k >> 1) & 1) : 4 * (k & 3); }
 
 // Grouped mode (the MoE grouped GEMM): program p of the launch multiplies group g = grp[p]'s
 // rows [gstart[g], gstart[g] + grows[g]) of A by weight g of B (row-major K x N at B + g*sbg) into
@@ -116,7 +124,7 @@ constexpr int kMaxDedupGroups = 1024;   // group tables up to this size have rep
 enum { kPlain = 0, kGrouped = 1, kSplit = 2, kSwiGLU = 3 };
 
 template <int WM, int WN, bool RESID, int MODE, int BKT = 32>
-__global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_kernel(
+__global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A_in, const uint16_t* __restrict__ B_in, const uint16_t* __restrict__ R,
     uint16_t* __restrict__ C_in, int M_in, int N, int K, int tiles_m, int tiles_n, Groups gp,
     float* __restrict__ part, int kchunk) {
@@ -211,7 +219,8 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   const i32x4 rsrc_b = make_rsrc(B + n0, uint32_t((int64_t(K - koff) * N - n0) * 2));
   // A: instruction t of this wave covers rows kARowsPerKB*(kDmaA*wave + t) + lane/kChunks; lane ->
   //    slot lane%kChunks, holding chunk slot ^ a_swz(row)
-  // B: instruction t covers rows kBRowsPerKB*(kDmaB*wave + t) + lane/kBSlots; lane -> slot lane%kBSlots
+  // B: instruction t covers the stage's 16-byte pieces 64*(kDmaB*wave + t) + lane in row-major order,
+  //    piece i -> row i/kBSlots, slot i%kBSlots holding chunk slot ^ b_swz(row)
   uint32_t a_voff[Sh::kDmaA], b_voff[Sh::kDmaB];
 #pragma unroll
   for (int t = 0; t < Sh::kDmaA; ++t) {
@@ -221,8 +230,9 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
   }
 #pragma unroll
   for (int t = 0; t < Sh::kDmaB; ++t) {
-    const int k = Sh::kBRowsPerKB * (wave * Sh::kDmaB + t) + lane / Sh::kBSlots;
-    const int bchunk = (lane % Sh::kBSlots) ^ (4 * (k & 3));
+    const int piece = 64 * (wave * Sh::kDmaB + t) + lane;
+    const int k = piece / Sh::kBSlots;
+    const int bchunk = (piece % Sh::kBSlots) ^ b_swz<BN>(k);
     int bcol = bchunk * 8;
     if constexpr (MODE == kSwiGLU) {   // 32-wide block b: gate (b even) or up (b odd) of pair b / 2
       const int b = bchunk >> 2;
@@ -287,7 +297,7 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int k = 8 * h + 4 * r + jj;  // + 16*ks, which keeps k & 3
-      b_off[j][r] = k * (2 * BN) + ((chunk ^ (4 * (k & 3))) << 4) + (q & 1) * 8;
+      b_off[j][r] = k * (2 * BN) + ((chunk ^ b_swz<BN>(k)) << 4) + (q & 1) * 8;
     }
   }
 
@@ -466,10 +476,12 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
     constexpr int WC = WJ * 32;           // columns of a wave's block
     constexpr int kPitch = WC * 4 + 16;   // bytes per staged row: rows start 4 banks apart
     constexpr int LPR = WC / 4;           // lanes per row, 4 columns each
-    constexpr int RPI = 64 / LPR;         // rows per instruction
+    constexpr int RPI = 64 / LPR;         // rows per instruction (96 columns: 2 rows, 48 lanes)
+    static_assert(32 % RPI == 0, "whole instructions per 32-row block");
     static_assert(4 * 32 * kPitch <= Sh::kSmemBytes, "the staging regions fit in the ring's LDS");
     uint8_t* const stage = smem + wave * (32 * kPitch);
-    const int rl = lane / LPR, c4 = lane % LPR;
+    const bool lane_on = lane < RPI * LPR;     // lanes past the last whole row store nothing
+    const int rl = lane_on ? lane / LPR : 0, c4 = lane % LPR;
     const int gcol = col0 + 4 * c4;
     const uint32_t tile_bytes = uint32_t(min(BM, M - m0)) * uint32_t(ldc) * 2u;
     const __amdgpu_buffer_rsrc_t rsrc_c =
@@ -483,7 +495,8 @@ __global__ __launch_bounds__(kThreads, (WM * WN == 16 ? 1 : 2)) void gemm_bf16_k
       uint32_t voff[32 / RPI];
 #pragma unroll
       for (int t = 0; t < 32 / RPI; ++t)
-        voff[t] = gcol < cols ? (uint32_t(r0 + t * RPI) * uint32_t(ldc) + uint32_t(gcol)) * 2u : 0x80000000u;
+        voff[t] = lane_on && gcol < cols ? (uint32_t(r0 + t * RPI) * uint32_t(ldc) + uint32_t(gcol)) * 2u
+                                         : 0x80000000u;
       u32x2 rr[32 / RPI];
       if constexpr (RESID) {   // issued before the staging writes so their latency overlaps them
 #pragma unroll
@@ -578,11 +591,15 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
     return PTB_ERR_ALIGN;
   // the largest tile that still gives every CU a tile: 256x256, else 256x128; then 128x128 while its
   // tiles cover half the CUs, else 64x128 (column tiles stay 128 wide: the B swizzle spans 16 chunks).
-  // 256x256 also where 256x128 tiles would need a second round on the CUs: a 256x256 workgroup
-  // moves ~1.4x the flops per CU of a 256x128 one, so one round of it beats two of the smaller.
+  // Where 256x256 tiles leave CUs idle but 256x128 ones would need a second round, 256x192 tiles
+  // when one round of them covers more CUs (the fused q|k|v projection, 2048x4096x6144: 256 tiles
+  // against 192), else 256x256: a 256x256 workgroup moves ~1.4x the flops per CU of a 256x128 one,
+  // so one round of it beats two of the smaller.
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t cus = cu_count();
   auto tiles = [&](int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+  if (tiles(256, 256) < cus && tiles(256, 128) > cus && tiles(256, 192) <= cus && tiles(256, 192) > tiles(256, 256))
+    return launch_gemm<4, 3>(a, b, residual, c, m, n, k, s);
   if (tiles(256, 256) >= cus || tiles(256, 128) > cus) return launch_gemm<4, 4>(a, b, residual, c, m, n, k, s);
   if (tiles(256, 128) >= cus) return launch_gemm<4, 2>(a, b, residual, c, m, n, k, s);
   if (tiles(128, 128) * 2 >= cus) return launch_gemm<2, 2>(a, b, residual, c, m, n, k, s);

@@ -45,7 +45,7 @@ def run_gemm(m, k, n, seed, std_a, std_b, resid=False):
     (2048, 4096, 1024, False),    # L2048/03 k/v_proj
     (2048, 4096, 4096, True),     # L2048/08 o_proj + residual
     (2048, 12288, 4096, True),    # L2048/11 down + residual
-    (2048, 4096, 6144, False),    # fused q|k|v projection: 256x256 tiles (256x128 would take two rounds)
+    (2048, 4096, 6144, False),    # fused q|k|v projection: one round of 256x192 tiles
 ])
 def test_gemm_layer_shapes(m, k, n, resid):
     std = 1.0 / 64.0
@@ -58,6 +58,7 @@ def test_gemm_layer_shapes(m, k, n, resid):
     (1024, 2048, 128), (257, 64, 264), (128, 4096, 4096),
     (2000, 512, 4088),    # 256x128 tiles, ragged in M and N
     (4000, 256, 4000),    # 256x256 tiles, ragged in M and N
+    (2000, 256, 6000),    # 256x192 tiles, ragged in M and N
 ])
 def test_gemm_ragged(m, k, n):
     got, want = run_gemm(m, k, n, 3, 1.0, 1.0 / k ** 0.5)
@@ -67,6 +68,7 @@ def test_gemm_ragged(m, k, n):
 @pytest.mark.parametrize("m,k,n", [
     (4000, 256, 4000),    # 256x256 tiles, ragged in M and N
     (2000, 512, 4088),    # 256x128 tiles, ragged in M and N
+    (2000, 512, 6000),    # 256x192 tiles (one round of 256 where 256x256 would leave CUs idle), ragged
 ])
 def test_gemm_ragged_residual_stays_inside_c(m, k, n):
     """The epilogue stages each tile through the LDS and masks rows past M and columns past N with
@@ -211,12 +213,13 @@ def test_gemm_swiglu_fused(m, k, inter):
 @pytest.mark.parametrize("m,k,n,resid", [
     (4096, 1088, 4096, False),   # 256x256 tiles, 17 steps of 64: the six-step loop's five-step remainder
     (4096, 832, 4096, True),     # 256x256 tiles, 13 steps: a one-step remainder
+    (2048, 1088, 6144, False),   # 256x192 tiles (the same six-step loop), 17 steps
     (2048, 4160, 4096, True),    # 256x128 tiles, 65 steps of 64: the three-step loop's two-step remainder
     (2048, 4224, 4096, True),    # 256x128 tiles, 66 steps: no remainder (4096 deep, 64 steps, leaves one)
 ])
 def test_gemm_odd_step_count(m, k, n, resid):
     """The main loop runs a whole number of turns of its rings a trip (six 64-deep steps for 256x256
-    tiles, whose rings hold three A and two B stages; three for 256x128), so a step count that is
+    and 256x192 tiles, whose rings hold three A and two B stages; three for 256x128), so a step count that is
     not a multiple ends on remainder steps, which must still read the right slots and drain the DMA
     stream."""
     std = 1.0 / 64.0
