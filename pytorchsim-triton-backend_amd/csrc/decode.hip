@@ -102,6 +102,12 @@ __device__ __forceinline__ float prologue(const uint16_t* x, const uint16_t* add
   }
 }
 
+// 16 bytes of a weight row.  A GEMV reads each weight once per call: with the non-temporal
+// (streaming) cache policy the 4096x24576 RMSNorm-prologue GEMV measured 34.9 us against 38.3 us.
+__device__ __forceinline__ u32x4 ld_stream(const uint16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
 template <int MODE>
 __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ add,
@@ -122,7 +128,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __r
   u32x4 v[8];
   if (col < N && wave + 28 < rows) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const u32x4*>(wp + int64_t(wave + 4 * u) * N);
+    for (int u = 0; u < 8; ++u) v[u] = ld_stream(wp + int64_t(wave + 4 * u) * N);
   }
   float r = 0.f;
   if constexpr (MODE == kRms) {
@@ -161,7 +167,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __r
     for (; i + 28 < rows; i += 32) {
       if (i != wave) {   // the first eight rows are already loaded
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const u32x4*>(wp + int64_t(i + 4 * u) * N);
+        for (int u = 0; u < 8; ++u) v[u] = ld_stream(wp + int64_t(i + 4 * u) * N);
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -174,7 +180,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __r
       }
     }
     for (; i < rows; i += 4) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(wp + int64_t(i) * N);
+      const u32x4 v = ld_stream(wp + int64_t(i) * N);
       const float xv = xs[i];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -292,7 +298,7 @@ __global__ __launch_bounds__(kGemvThreads) void ggemv_partial(const uint16_t* __
   u32x4 v[kGgKb / 4];
 #pragma unroll
   for (int u = 0; u < kGgKb / 4; ++u)
-    v[u] = *reinterpret_cast<const u32x4*>(wp + int64_t(min(wave + 4 * u, krows - 1)) * N);
+    v[u] = ld_stream(wp + int64_t(min(wave + 4 * u, krows - 1)) * N);
   // the first pass below runs even for an empty row range (it then stores nothing): an exit or a
   // guarded loop would let the compiler move the weight loads after the table reads and wait for
   // those first
