@@ -344,7 +344,7 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_kernel(const uint16_t* __r
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = l + i * kWave;
-    v[i] = c < chunks ? xr[c] : u32x4{0u, 0u, 0u, 0u};
+    v[i] = c < chunks ? __builtin_nontemporal_load(xr + c) : u32x4{0u, 0u, 0u, 0u};   // read once: streaming policy
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(v[i][q])), fabsf(bf16_hi(v[i][q]))));
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_block(const uint16_t* __re
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = threadIdx.x + i * kQBlock;
-    v[i] = c < chunks ? xr[c] : u32x4{0u, 0u, 0u, 0u};
+    v[i] = c < chunks ? __builtin_nontemporal_load(xr + c) : u32x4{0u, 0u, 0u, 0u};   // read once: streaming policy
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(v[i][q])), fabsf(bf16_hi(v[i][q]))));
