@@ -1,5 +1,21 @@
-"""Seeded inputs and the tolerance check shared by the parity tests."""
+"""Seeded inputs and the tolerance check shared by the parity tests.
+
+With PTB_REPORT_ERRORS=1 in the environment the checks also print, for checks that pass, the
+largest absolute error and the largest relative error over outputs at least the absolute floor in
+size (run pytest with -s to see them)."""
+import os
+
 import torch
+
+
+def _report(what, g, w, atol):
+    if not os.environ.get("PTB_REPORT_ERRORS"):
+        return
+    diff = (g.double() - w.double()).abs().nan_to_num(0.0)
+    big = w.double().abs() >= atol
+    rel = float((diff[big] / w.double().abs()[big]).max()) if bool(big.any()) else 0.0
+    print(f"[errors] {what}: max_abs_err={float(diff.max()):.3g} max_rel_err={rel:.3g} "
+          f"(relative over |want| >= {atol:.3g}; {diff.numel()} outputs)", flush=True)
 
 
 def randn(shape, seed, dtype=torch.bfloat16, std=1.0, mean=0.0):
@@ -22,6 +38,8 @@ def assert_close(got, want, rtol, atol, what=""):
     w = want.detach().float().cpu()
     assert g.shape == w.shape, f"{what}: shape {tuple(g.shape)} != {tuple(w.shape)}"
     ok = torch.allclose(g, w, rtol=rtol, atol=atol, equal_nan=True)
+    if ok:
+        _report(what, g, w, atol)
     if not ok:
         diff = (g - w).abs().nan_to_num(0.0)
         rel = diff / w.abs().clamp_min(1e-12)
@@ -46,6 +64,7 @@ def rows_close(got, want, rtol, atol_frac):
     bound = atol_frac * scale + rtol * w2.abs()
     bad = diff > bound
     if not bool(bad.any()):
+        _report("per-row check", g2, w2, float(atol_frac * scale.mean()))
         return True, ""
     ratio = (diff / bound.clamp_min(1e-30)).reshape(-1)
     idx = int(ratio.argmax())
