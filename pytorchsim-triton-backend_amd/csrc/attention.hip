@@ -182,13 +182,39 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float (&f)[8]) {
   }
 }
 
+// A wave's 32 query rows (row r at base + r*ld, 128 bf16 each) in the MFMA B-fragment layout: lane
+// (fr, h) receives raw[kk] = chunk 2*kk + h (d = 16*kk + 8*h .. +7) of row fr.  Read in that layout
+// straight from memory, one instruction would touch 32 rows; here each instruction loads whole
+// 128-byte halves of 8 rows, and each half of the dims passes through the wave's own 4 KB LDS
+// region (row-major, 16-byte chunk c of row r in slot c ^ ((r >> 1) & 7), so that the writes and
+// the fragment reads are bank-conflict free).  A wave's LDS operations complete in order, so the
+// region needs no barrier between its writes and reads, nor between the two halves.
+__device__ __forceinline__ void load_q_rows(const uint16_t* __restrict__ base, int64_t ld, uint8_t* region, int lane,
+                                            u32x4 (&raw)[8]) {
+  const int r8 = lane >> 3, c8 = lane & 7, fr = lane & 31, h = lane >> 5;
+  u32x4 v[8];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      v[4 * p + t] = *reinterpret_cast<const u32x4*>(base + int64_t(8 * t + r8) * ld + 64 * p + 8 * c8);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int row = 8 * t + r8;
+      *reinterpret_cast<u32x4*>(region + row * 128 + ((c8 ^ ((row >> 1) & 7)) << 4)) = v[4 * p + t];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      raw[4 * p + j] = *reinterpret_cast<const u32x4*>(region + fr * 128 + (((2 * j + h) ^ ((fr >> 1) & 7)) << 4));
+  }
+}
+
 // One query row's 128 values as this lane holds them (chunks c = 2*kk + h, d = 8c .. 8c+7; the other
 // half of the row is in lane ^ 32), normalised and rotated, as the MFMA B fragments.
-__device__ __forceinline__ void qnorm_rope_row(const uint16_t* __restrict__ src, const QkvIn& in, int pos, int h,
+__device__ __forceinline__ void qnorm_rope_row(const u32x4 (&raw)[8], const QkvIn& in, int pos, int h,
                                                uint32_t flip, bf16x8 (&qf)[8]) {
-  u32x4 raw[8];
-#pragma unroll
-  for (int kk = 0; kk < 8; ++kk) raw[kk] = *reinterpret_cast<const u32x4*>(src + kk * 16);
   float s[8];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
@@ -336,19 +362,21 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   // the first K/V block's DMA goes out before the query loads: its latency overlaps theirs
   issue_block(0, std::integral_constant<int, 0>{});
 
+  // the query rows pass through stage 1, which the first block leaves free; the barrier at the top
+  // of that block (its fences wait for these LDS reads) comes before anything is loaded into it
+  static_assert(WAVES * 4096 <= kStageBytes, "the query staging regions fit in one stage");
   bf16x8 qf[8];
   if (active) {
     const uint32_t flip = negate ? 0x80008000u : 0u;
+    uint8_t* const qstage = smem + kStageBytes + wave * 4096;
+    u32x4 raw[8];
     if constexpr (QKV) {
-      qnorm_rope_row(Q + (int64_t(b) * S + qi) * qin.ld + (kvh * G + g) * D + h * 8, qin, qi, h, flip, qf);
+      load_q_rows(Q + (int64_t(b) * S + qw0) * qin.ld + (kvh * G + g) * D, qin.ld, qstage, lane, raw);
+      qnorm_rope_row(raw, qin, qi, h, flip, qf);
     } else {
-      const uint16_t* src = qp + int64_t(qi) * D + h * 8;
+      load_q_rows(qp + int64_t(qw0) * D, D, qstage, lane, raw);
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        u32x4 v = *reinterpret_cast<const u32x4*>(src + kk * 16);
-        v ^= flip;
-        qf[kk] = __builtin_bit_cast(bf16x8, v);
-      }
+      for (int kk = 0; kk < 8; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, raw[kk] ^ flip);
     }
   }
 
