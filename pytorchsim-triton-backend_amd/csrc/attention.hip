@@ -4,8 +4,9 @@
 // kv head b*HKV + h / (HQ/HKV).
 //
 // Workgroup = 8 waves = 256 query rows of one head (32 per wave), one workgroup per CU, two waves
-// per SIMD; or, when that gives fewer than two workgroups per CU, 4 waves = 128 rows, two
-// workgroups per CU.  Blocks of 64 keys move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR
+// per SIMD; or, when that gives fewer than two workgroups per CU, either (causal, when the units fill
+// at least 3/4 of the CUs) 8 waves over two 128-row tiles, a heavy one and its light complement, so
+// every workgroup carries the same causal work, or 4 waves = 128 rows, two workgroups per CU.  Blocks of 64 keys move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR
 // staging) into two 32 KB stages, one block ahead, shared by all the workgroup's rows.  Both tiles
 // keep their global [key][d] layout with the 16-byte chunks of each 256-byte row XOR-swizzled, so
 // every LDS read is bank-conflict free:
@@ -290,7 +291,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     g = pid % G;
     r = pid / G;
   }
-  const int tile = causal ? nt - 1 - r / nkv : r / nkv;
   const int kvi = r % nkv;
   const int b = kvi / hkv, kvh = kvi % hkv;
   const int64_t bh = int64_t(b) * hq + kvh * G + g;
@@ -303,10 +303,25 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, fr = lane & 31;
-  const int q0 = tile * BQ;
-  const int qw0 = q0 + wave * 32;
+  // Rows of this wave, and the end of the workgroup's query range (its last key, when causal).
+  // causal & 2 (8 waves; S a multiple of 128): work unit u pairs the 128-row tiles S/128 - 1 - u
+  // (waves 0-3) and u (waves 4-7), so every unit carries the same causal work and each SIMD holds
+  // one wave of the heavy tile beside one of the light tile; in the middle unit of an odd tile count
+  // both are the same tile and waves 4-7 stay idle.  Otherwise tile r / nkv, heaviest-first.
+  int qw0, qend;
+  bool active;
+  if (WAVES == 8 && (causal & 2)) {
+    const int u = r / nkv, ta = S / 128 - 1 - u, half = wave >> 2;
+    qw0 = (half ? u : ta) * 128 + (wave & 3) * 32;
+    active = !half || u < ta;
+    qend = (ta + 1) * 128;
+  } else {
+    const int tile = causal ? nt - 1 - r / nkv : r / nkv;
+    qw0 = tile * BQ + wave * 32;
+    active = qw0 < S;                  // S is a multiple of 32: a wave's rows are all in or all out
+    qend = min(tile * BQ + BQ, S);
+  }
   const int qi = qw0 + fr;             // this lane's query
-  const bool active = qw0 < S;         // S is a multiple of 32: a wave's rows are all in or all out
 
   // ---- K/V loaders: instruction t of this wave fills key rows 4*(kDmaT*wave + t) .. +3 of a tile;
   //      lane L writes row L/16, slot L%16, so it fetches the chunk that belongs in that slot
@@ -392,7 +407,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
   // causal: the workgroup needs keys up to its last row; a wave stops at the block holding its
   // diagonal (blocks past it are fully masked); inactive waves compute nothing
-  const int nb = causal ? min(q0 + BQ, S) / BKV : S / BKV;
+  const int nb = causal ? qend / BKV : S / BKV;
   const int last = !active ? -1 : causal ? (qw0 + 31) / BKV : nb - 1;
   auto block = [&](int kb, auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
@@ -471,8 +486,12 @@ static int flash_launch(const void* q, const void* k, const void* v, void* o, in
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   const bool wide = ((seq + 255) / 256) * batch * hq >= 2 * int64_t(cus);
+  // causal with too few 256-row tiles: 256-row workgroups that each pair a heavy and a light 128-row
+  // tile when those units fill at least 3/4 of the CUs in one round, else 128-row workgroups
+  const int64_t units = (seq / 128 + 1) / 2 * batch * hq;
+  const bool paired = causal && !wide && units <= cus && 4 * units >= 3 * int64_t(cus);
   const int64_t bq = wide ? 256 : 128;
-  const int64_t nt = (seq + bq - 1) / bq;
+  const int64_t nt = paired ? (seq / 128 + 1) / 2 : (seq + bq - 1) / bq;
   const int64_t total = nt * nkv * (hq / hkv);
   // K/V of one kv head are addressed through a 32-bit buffer range (v with its row stride)
   const int64_t vrow = fused ? qin.ld : D;
@@ -482,12 +501,12 @@ static int flash_launch(const void* q, const void* k, const void* v, void* o, in
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto qp = static_cast<const uint16_t*>(q), kp = static_cast<const uint16_t*>(k), vp = static_cast<const uint16_t*>(v);
   auto op = static_cast<uint16_t*>(o);
-  const int neg = scale < 0.f ? 1 : 0, cz = causal ? 1 : 0;
+  const int neg = scale < 0.f ? 1 : 0, cz = causal ? (paired ? 3 : 1) : 0;
   const unsigned grid = unsigned(total);
-  if (wide && fused)
+  if ((wide || paired) && fused)
     flash_fwd_kernel<8, true><<<grid, 512, 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv), int(nkv), int(nt), c,
                                                    neg, cz, o_tokens, qin);
-  else if (wide)
+  else if (wide || paired)
     flash_fwd_kernel<8><<<grid, 512, 0, s>>>(qp, kp, vp, op, int(seq), int(hq), int(hkv), int(nkv), int(nt), c, neg,
                                              cz, o_tokens, qin);
   else if (fused)

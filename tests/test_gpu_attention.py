@@ -30,7 +30,8 @@ def inputs(batch, hq, hkv, s, seed):
 
 @pytest.mark.parametrize("batch,hq,hkv,s,causal", [
     (1, 32, 8, 4096, True),     # BASELINE config 3 / attention_prefill_32x8x4096_bf16
-    (1, 32, 8, 2048, True),     # L2048/06 (the Qwen3-8B layer's attention)
+    (1, 32, 8, 2048, True),     # L2048/06 (the Qwen3-8B layer's attention): paired 128-row tiles
+    (1, 56, 8, 896, True),      # paired tiles, odd tile count (the middle unit's second half idle)
     (1, 16, 8, 1024, True),
     (1, 24, 8, 512, True),      # G = 3
     (1, 64, 8, 256, True),      # G = 8
