@@ -183,22 +183,26 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float (&f)[8]) {
   }
 }
 
-// A wave's 32 query rows (row r at base + r*ld, 128 bf16 each) in the MFMA B-fragment layout: lane
-// (fr, h) receives raw[kk] = chunk 2*kk + h (d = 16*kk + 8*h .. +7) of row fr.  Read in that layout
-// straight from memory, one instruction would touch 32 rows; here each instruction loads whole
-// 128-byte halves of 8 rows, and each half of the dims passes through the wave's own 4 KB LDS
-// region (row-major, 16-byte chunk c of row r in slot c ^ ((r >> 1) & 7), so that the writes and
-// the fragment reads are bank-conflict free).  A wave's LDS operations complete in order, so the
-// region needs no barrier between its writes and reads, nor between the two halves.
-__device__ __forceinline__ void load_q_rows(const uint16_t* __restrict__ base, int64_t ld, uint8_t* region, int lane,
-                                            u32x4 (&raw)[8]) {
-  const int r8 = lane >> 3, c8 = lane & 7, fr = lane & 31, h = lane >> 5;
-  u32x4 v[8];
+// A wave's 32 query rows (row r at base + r*ld, 128 bf16 each), loaded as whole 128-byte halves of
+// 8 rows per instruction: lane (r8, c8) = (lane / 8, lane % 8) receives v[4*p + t] = chunk 8*p + c8
+// (d = 64*p + 8*c8 .. +7) of row 8*t + r8.  (Read straight in the MFMA fragment layout, one
+// instruction would touch 32 rows.)
+__device__ __forceinline__ void load_q_rows(const uint16_t* __restrict__ base, int64_t ld, int lane, u32x4 (&v)[8]) {
+  const int r8 = lane >> 3, c8 = lane & 7;
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       v[4 * p + t] = *reinterpret_cast<const u32x4*>(base + int64_t(8 * t + r8) * ld + 64 * p + 8 * c8);
+}
+
+// The rows of load_q_rows in the MFMA B-fragment layout: lane (fr, h) receives raw[kk] = chunk
+// 2*kk + h (d = 16*kk + 8*h .. +7) of row fr.  Each half of the dims passes through the wave's own
+// 4 KB LDS region (row-major, 16-byte chunk c of row r in slot c ^ ((r >> 1) & 7), so that the
+// writes and the fragment reads are bank-conflict free).  A wave's LDS operations complete in
+// order, so the region needs no barrier between its writes and reads, nor between the two halves.
+__device__ __forceinline__ void q_rows_to_fragments(const u32x4 (&v)[8], uint8_t* region, int lane, u32x4 (&raw)[8]) {
+  const int r8 = lane >> 3, c8 = lane & 7, fr = lane & 31, h = lane >> 5;
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
 #pragma unroll
@@ -212,58 +216,59 @@ __device__ __forceinline__ void load_q_rows(const uint16_t* __restrict__ base, i
   }
 }
 
-// One query row's 128 values as this lane holds them (chunks c = 2*kk + h, d = 8c .. 8c+7; the other
-// half of the row is in lane ^ 32), normalised and rotated, as the MFMA B fragments.
-__device__ __forceinline__ void qnorm_rope_row(const u32x4 (&raw)[8], const QkvIn& in, int pos, int h,
-                                               uint32_t flip, bf16x8 (&qf)[8]) {
-  float s[8];
+// The fused form's per-head RMSNorm and rotate-half RoPE of the rows of load_q_rows (row 8*t + r8 at
+// position pos0 + 8*t + r8), in place, with the fp32 operations of qk_norm_rope in the same order:
+// each chunk's sum of squares by fma in element order, then the pairwise tree over the 16 chunks,
+// (c, c^1), (c, c^2) and (c, c^4) across the lane's 8-lane group by DPP (quad_perm pairs, then
+// row_half_mirror, whose partner quad holds one equal value per lane), then (c, c^8) within the
+// lane, which holds both halves 8p + c8; chunk c is rotated against chunk c ^ 8, also in the lane.
+// The fp32 cos/sin loads likewise cover 8 rows per instruction (a lane's 32 bytes in two halves).
+__device__ __forceinline__ void qnorm_rope_rows(u32x4 (&v)[8], const QkvIn& in, int pos0, int lane) {
+  const int r8 = lane >> 3, c8 = lane & 7;
+  float w[2][8];
+  unpack8(reinterpret_cast<const u32x4*>(in.w)[c8], w[0]);
+  unpack8(reinterpret_cast<const u32x4*>(in.w)[8 + c8], w[1]);
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) {
-    float f[8];
-    unpack8(raw[kk], f);
-    float ss = 0.f;
+  for (int t = 0; t < 4; ++t) {
+    float f[2][8], s[2];
+    unpack8(v[t], f[0]);
+    unpack8(v[4 + t], f[1]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
-    s[kk] = ss;
-  }
-  // qk_norm_rope's 16-lane tree over chunks 0..15: (c, c^1), then (c, c^2), then the halves of 8,
-  // then of 16; chunk c^1 is the partner lane's, c^2 and up this lane's kk^1, kk^2, kk^4
+    for (int p = 0; p < 2; ++p) {
+      s[p] = 0.f;
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(s[kk]), __float_as_uint(s[kk]), false, false);
-    s[kk] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-  const float ss = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
-  const float r = 1.0f / sqrtf(ss / 128.f + in.eps);
-  const float* cs = in.cos + int64_t(pos) * 128;
-  const float* sn = in.sin + int64_t(pos) * 128;
-#pragma unroll
-  for (int kk = 0; kk < 8; ++kk) {
-    const int c = 2 * kk + h, pc = c ^ 8;
-    float f[8], pf[8], wf[8], pw[8];
-    unpack8(raw[kk], f);
-    unpack8(raw[kk ^ 4], pf);
-    unpack8(reinterpret_cast<const u32x4*>(in.w)[c], wf);
-    unpack8(reinterpret_cast<const u32x4*>(in.w)[pc], pw);
-    const f32x4v c0 = reinterpret_cast<const f32x4v*>(cs + 8 * c)[0], c1 = reinterpret_cast<const f32x4v*>(cs + 8 * c)[1];
-    const f32x4v s0 = reinterpret_cast<const f32x4v*>(sn + 8 * c)[0], s1 = reinterpret_cast<const f32x4v*>(sn + 8 * c)[1];
-    const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    u32x4 o;
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      float y[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const float a = (f[e + u] * r) * wf[e + u];
-        const float p = (pf[e + u] * r) * pw[e + u];
-        const float rot = kk < 4 ? -p : p;
-        y[u] = fmaf(a, cv[e + u], rot * sv[e + u]);
-      }
-      o[e / 2] = pack_bf16x2(y[0], y[1]);
+      for (int e = 0; e < 8; ++e) s[p] = fmaf(f[p][e], f[p][e], s[p]);
+      s[p] += dpp_f32<0xb1>(s[p]);
+      s[p] += dpp_f32<0x4e>(s[p]);
+      s[p] += dpp_f32<0x141>(s[p]);
     }
-    o ^= flip;
-    qf[kk] = __builtin_bit_cast(bf16x8, o);
+    const float ss = s[0] + s[1];
+    const float r = 1.0f / sqrtf(ss / 128.f + in.eps);
+    const int64_t pos = pos0 + 8 * t + r8;
+    const float* cs = in.cos + pos * 128;
+    const float* sn = in.sin + pos * 128;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int d0 = 64 * p + 8 * c8;
+      const f32x4v c0 = reinterpret_cast<const f32x4v*>(cs + d0)[0], c1 = reinterpret_cast<const f32x4v*>(cs + d0)[1];
+      const f32x4v s0 = reinterpret_cast<const f32x4v*>(sn + d0)[0], s1 = reinterpret_cast<const f32x4v*>(sn + d0)[1];
+      const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float y[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const float a = (f[p][e + u] * r) * w[p][e + u];
+          const float q = (f[1 - p][e + u] * r) * w[1 - p][e + u];
+          const float rot = p == 0 ? -q : q;
+          y[u] = fmaf(a, cv[e + u], rot * sv[e + u]);
+        }
+        o[e / 2] = pack_bf16x2(y[0], y[1]);
+      }
+      v[4 * p + t] = o;
+    }
   }
 }
 
@@ -384,15 +389,16 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   if (active) {
     const uint32_t flip = negate ? 0x80008000u : 0u;
     uint8_t* const qstage = smem + kStageBytes + wave * 4096;
-    u32x4 raw[8];
+    u32x4 v[8], raw[8];
     if constexpr (QKV) {
-      load_q_rows(Q + (int64_t(b) * S + qw0) * qin.ld + (kvh * G + g) * D, qin.ld, qstage, lane, raw);
-      qnorm_rope_row(raw, qin, qi, h, flip, qf);
+      load_q_rows(Q + (int64_t(b) * S + qw0) * qin.ld + (kvh * G + g) * D, qin.ld, lane, v);
+      qnorm_rope_rows(v, qin, qw0, lane);
     } else {
-      load_q_rows(qp + int64_t(qw0) * D, D, qstage, lane, raw);
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, raw[kk] ^ flip);
+      load_q_rows(qp + int64_t(qw0) * D, D, lane, v);
     }
+    q_rows_to_fragments(v, qstage, lane, raw);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, raw[kk] ^ flip);
   }
 
   WaveState w;
