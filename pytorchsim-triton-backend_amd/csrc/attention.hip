@@ -4,9 +4,10 @@
 // kv head b*HKV + h / (HQ/HKV).
 //
 // Workgroup = 8 waves = 256 query rows of one head (32 per wave), one workgroup per CU, two waves
-// per SIMD; or, when that gives fewer than two workgroups per CU, either (causal, when the units fill
-// at least 3/4 of the CUs) 8 waves over two 128-row tiles, a heavy one and its light complement, so
-// every workgroup carries the same causal work, or 4 waves = 128 rows, two workgroups per CU.  Blocks of 64 keys move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR
+// per SIMD, when that gives at least two workgroups per CU (non-causal: one); otherwise either
+// (causal, when the units fill at least 3/4 of the CUs) 8 waves over two 128-row tiles, a heavy one
+// and its light complement, so every workgroup carries the same causal work, or 4 waves = 128 rows,
+// two workgroups per CU.  Blocks of 64 keys move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR
 // staging) into two 32 KB stages, one block ahead, shared by all the workgroup's rows.  Both tiles
 // keep their global [key][d] layout with the 16-byte chunks of each 256-byte row XOR-swizzled, so
 // every LDS read is bank-conflict free:
@@ -488,10 +489,11 @@ static int flash_launch(const void* q, const void* k, const void* v, void* o, in
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return PTB_ERR_ALIGN;
   const bool fused = qin.w != nullptr;
   const int64_t nkv = batch * hkv;
-  // 256-row workgroups when there are at least two per CU, else 128-row ones (two per CU)
+  // 256-row workgroups when there are at least two per CU (non-causal: one, since every workgroup
+  // then carries the same work), else 128-row ones (two per CU)
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  const bool wide = ((seq + 255) / 256) * batch * hq >= 2 * int64_t(cus);
+  const bool wide = ((seq + 255) / 256) * batch * hq >= (causal ? 2 : 1) * int64_t(cus);
   // causal with too few 256-row tiles: 256-row workgroups that each pair a heavy and a light 128-row
   // tile when those units fill at least 3/4 of the CUs in one round, else 128-row workgroups
   const int64_t units = (seq / 128 + 1) / 2 * batch * hq;

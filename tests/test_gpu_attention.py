@@ -39,6 +39,7 @@ def inputs(batch, hq, hkv, s, seed):
     (1, 8, 8, 128, True),       # MHA, a single (partial) tile
     (1, 8, 2, 640, True),       # S not a multiple of the 256-row tile
     (1, 8, 2, 512, False),      # non-causal path
+    (1, 32, 8, 2048, False),    # non-causal, one 256-row workgroup per CU
     (1, 4, 4, 384, False),      # non-causal, partial tile
 ])
 def test_flash_attention(batch, hq, hkv, s, causal):
