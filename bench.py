@@ -115,11 +115,22 @@ def bench_rmsnorm(steps, warmup):
         ys[i].copy_(xs[i])
 
     copy_ms, _ = timed(copy_step, steps * 4, warmup)
+
+    # the library's own stream of the same bytes: ptb_add_scalar_bf16 reads and writes 2 B per
+    # element over the same [2048, 4096] bf16 tensors, same cycling
+    def same_bytes_step():
+        i = it[0] % copies
+        it[0] += 1
+        ops.add_scalar(xs[i], 1.0, out=ys[i])
+
+    same_ms, _ = timed(same_bytes_step, steps * 4, warmup)
     return {"name": "rmsnorm", "config": "BASELINE config 1: x bf16 [2048x4096], w fp32",
             "us": ms * 1e3, "wall_us": wall * 1e3, "gbs": gbs,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS},
-            "device_copy_us": copy_ms * 1e3, "vs_device_copy": copy_ms / ms}
+            "device_copy_us": copy_ms * 1e3, "vs_device_copy": copy_ms / ms,
+            "same_bytes_us": same_ms * 1e3, "vs_same_bytes": same_ms / ms,
+            "same_bytes_frac": (nbytes - cols * 4) / (same_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
 
 
 def bench_gemm_fp8(steps, warmup):
@@ -179,11 +190,12 @@ def bench_layer(steps, warmup):
     flops = sum(f for _, f, _ in work)
     return {"name": "qwen3_8b_layer", "config": "BASELINE config 5: Qwen3-8B decoder layer prefill T=S=2048",
             "us": ms * 1e3, "wall_us": wall * 1e3, "tflops": flops / (ms * 1e-3) / 1e12,
-            # the layer is 14 launches of different bounds: frac = sum of per-launch roofline times
-            # (max of MFMA time and HBM time each) over the measured layer latency
+            # the reference's layer is 14 launches of different bounds: frac = the sum of their
+            # roofline times (max of MFMA time and HBM time each) over the measured layer latency;
+            # the forward issues them fused into 8 kernels
             "roofline": {"bound": "mixed", "roofline_us": roof_us, "measured_us": ms * 1e3, "unit": "us",
                          "frac": roof_us / (ms * 1e3)},
-            "launches": len(work)}
+            "launches": qwen3.PREFILL_KERNELS, "reference_launches": len(work)}
 
 
 def bench_gemv(steps, warmup):
@@ -327,12 +339,36 @@ def _median_seconds(fn, trials: int, min_s: float) -> float:
     return ts[len(ts) // 2]
 
 
+def golden_gemm_fp32(a, b, residual=None):
+    """The reference's CPU golden for its GEMMs: torch.matmul on fp32 operands
+    (tests/cases/smoke/gemm.py:45-47, tests/cases/mechanism/ops/ops_bf16_matmul.py's reference),
+    with the bf16 kernel's residual add and single bf16 rounding."""
+    import torch
+
+    acc = torch.matmul(a.float(), b.float())
+    if residual is not None:
+        acc = acc + residual.float()
+    return acc.to(torch.bfloat16)
+
+
+def golden_gemm_fp8_fp32(aq, sa, wq_t, sw):
+    """The reference's fp8 golden: torch.matmul of the e4m3 operands upcast to fp32
+    (tests/cases/mechanism/ops/ops_fp8_e4m3_dot.py:41-44), then the per-token x per-channel scale
+    epilogue (tests/cases/workloads/int8_dequant_matmul.py:59-69)."""
+    import torch
+
+    acc = torch.matmul(aq.float(), wq_t.float().t())
+    return ((acc * sa[:, None]) * sw[None, :]).to(torch.bfloat16)
+
+
 def cpu_baselines() -> list:
-    """The reference's CPU golden for each BASELINE config, timed on this host: the oracle's
-    functions (torch-CPU; GEMM and fp8 dots summed in fp64 and rounded once, as the golden
-    defines them) on a bounded sample of each workload, on all host threads (median of 3 trials, 1
-    for the layer) and on one thread (median of 3, 1 for the layer).  Throughput is the sample's
-    algorithmic work over its time, in the GPU line's unit; the layer also gives its latency."""
+    """The reference's CPU golden for each BASELINE config, timed on this host on a bounded sample
+    of each workload, on all host threads (median of 3 trials, 1 for the layer) and on one thread
+    (median of 3, 1 for the layer).  GEMMs (config 2, the fp8 dot of config 4, the layer's
+    projections) are the reference's golden, torch.matmul on fp32 operands; the vector ops and
+    attention are the oracle's torch-CPU restatements (the fp64 GEMM sums of the oracle stay the
+    parity checker only).  Throughput is the sample's algorithmic work over its time, in the GPU
+    line's unit; the layer also gives its latency."""
     import torch
     import oracle
     from ptb_amd import qwen3
@@ -342,9 +378,10 @@ def cpu_baselines() -> list:
     g = torch.Generator().manual_seed(0)
     out = []
 
-    def leg(name, unit, work, sample_all, sample_one, fn_all, fn_one, trials=3, min_s=1.0):
+    def leg(name, unit, work, sample_all, sample_one, fn_all, fn_one, trials=3, min_s=1.0,
+            golden="oracle (torch-CPU fp32)"):
         """work(sample) -> algorithmic units of one call (GB or GFLOP); fn_*() runs the sample."""
-        rec = {"config": name, "unit": unit, "cores": threads, "kind": "port"}
+        rec = {"config": name, "unit": unit, "cores": threads, "kind": "port", "golden": golden}
         for key, n, fn, samp in (("all", threads, fn_all, sample_all), ("one", 1, fn_one, sample_one)):
             torch.set_num_threads(n)
             if trials > 1:
@@ -371,7 +408,8 @@ def cpu_baselines() -> list:
     s2a = {"what": "256 of 4096 rows of A @ B[4096x12288]", "rows": 256}
     s2o = {"what": "32 of 4096 rows of A @ B[4096x12288]", "rows": 32}
     out.append(leg("2 gemm_bf16", "TFLOP/s", lambda s: 2.0 * s["rows"] * 4096 * 12288 / 1e9, s2a, s2o,
-                   lambda: oracle.gemm(a[:256], b), lambda: oracle.gemm(a[:32], b)))
+                   lambda: golden_gemm_fp32(a[:256], b), lambda: golden_gemm_fp32(a[:32], b),
+                   golden="fp32 torch"))
     del a, b
     # config 3: causal GQA attention, one kv head with its 4 query heads (1/8 of the heads), full S
     q = torch.randn(4, 4096, 128, generator=g).to(bf)
@@ -389,22 +427,23 @@ def cpu_baselines() -> list:
 
     def fp8(rows):
         aq, sa = oracle.quant_rows_e4m3(xs[:rows])
-        oracle.gemm_fp8(aq, sa, wq, sw)
+        golden_gemm_fp8_fp32(aq, sa, wq, sw)
 
     out.append(leg("4 gemm_fp8", "TFLOP/s", lambda s: 2.0 * s["rows"] * 12288 * 4096 / 1e9, s4a, s4o,
-                   lambda: fp8(64), lambda: fp8(16)))
+                   lambda: fp8(64), lambda: fp8(16), golden="fp32 torch (quantiser: oracle)"))
     del wq, sw
     # config 5: the layer; all threads run T = 2048, one thread the first 256 tokens (a causal
     # layer's first rows are exactly a shorter sequence)
     wts = qwen3.random_weights()
     xt = torch.randn(2048, 4096, generator=torch.Generator().manual_seed(1)).to(bf)
     cos, sin = oracle.rope_tables(2048, 128, 1.0e6)
-    lay = lambda t: oracle.qwen3_layer(xt[:t], wts, cos[:t], sin[:t], bq=min(t, 1024))  # noqa: E731
+    lay = lambda t: oracle.qwen3_layer(xt[:t], wts, cos[:t], sin[:t], bq=min(t, 1024),  # noqa: E731
+                                       gemm_fn=golden_gemm_fp32)
     flops = lambda s: sum(f for _, f, _ in qwen3.layer_work(s["t"])) / 1e9  # noqa: E731
     s5a = {"what": "the whole layer, T = S = 2048", "t": 2048}
     s5o = {"what": "the layer over the first 256 tokens", "t": 256}
     rec = leg("5 qwen3_8b_layer", "TFLOP/s", flops, s5a, s5o, lambda: lay(2048), lambda: lay(256),
-              trials=1, min_s=0.0)
+              trials=1, min_s=0.0, golden="fp32 torch GEMMs, oracle vector ops and attention")
     rec["layer_us"] = flops(s5a) / rec["value"] * 1e3   # GFLOP / (TFLOP/s) = ms
     out.append(rec)
     return out
@@ -543,7 +582,7 @@ def main(argv=None):
         per_config = cpu_baselines()
         c2 = next(r for r in per_config if r["config"].startswith("2 "))
         cpu = {"value": c2["value"], "unit": c2["unit"], "cores": c2["cores"], "kind": "port",
-               "sample": c2["sample"], "value_1_thread": c2["value_1_thread"],
+               "golden": c2["golden"], "sample": c2["sample"], "value_1_thread": c2["value_1_thread"],
                "sample_1_thread": c2["sample_1_thread"], "configs": per_config}
     kernels = []
     for r in results.values():

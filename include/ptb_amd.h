@@ -450,17 +450,20 @@ typedef struct ptb_tensor {
 } ptb_tensor;
 
 /* args [x, w, y] (L2048/00's in_ptr0, in_ptr1, out_ptr1), x/y bf16 with w bf16 or fp32, or all
- * fp32; ints [rows (xnumel), cols (r0_numel), programs]; floats [eps].
+ * fp32; or, all fp32, [x, w, o, c] with the column arm c[cols] = rsqrt(mean over the rows the grid
+ * covers of x^2 + eps); ints [rows (xnumel), cols (r0_numel), programs (, block)]; floats [eps].
+ * Row-block families (rmsnorm, softmax, silu_mul, add_scalar) run the leading gx blocks of `block`
+ * rows (elements) a program -- the kernel's XBLOCK when stated, else ceil(extent / programs).
  * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/00_..._gwdq6qer_triton.py:17-60 and
- *           tests/cases/workloads/rmsnorm.py:44-54 */
+ *           tests/cases/workloads/rmsnorm.py:44-57 (both arms) */
 int ptb_rmsnorm_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
                      int nfloats, const int32_t grid[3], void* stream);
-/* args [x, y]: bf16 -> bf16, bf16 -> fp32 or fp32 -> fp32; ints [rows, cols, programs].
+/* args [x, y]: bf16 -> bf16, bf16 -> fp32 or fp32 -> fp32; ints [rows, cols, programs (, block)].
  * Replaces: vector_softmax_<R>x<C>_bf16/00_..._triton.py:17-68, layer_layer_decode_1x1024_bf16/16
  *           (fp32 out), tests/cases/workloads/softmax.py:46-55 */
 int ptb_softmax_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
                      int nfloats, const int32_t grid[3], void* stream);
-/* args [gate_up, out] (bf16 or fp32); ints [rows, inter, programs].
+/* args [gate_up, out] (bf16 or fp32); ints [rows, inter, programs (, block of outputs)].
  * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/10_..._ktzl5s2h_triton.py:17-36 */
 int ptb_silu_mul_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
                       int nfloats, const int32_t grid[3], void* stream);
@@ -489,6 +492,37 @@ int ptb_qk_norm_rope_args(const ptb_tensor* args, int nargs, const int64_t* ints
  * Replaces: qwen3_8b_layer_prefill_2048x2048_bf16/05_..._ff5nvvqz_triton.py:17-27 and 07_..._ei42assc */
 int ptb_transpose_heads_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints,
                              const double* floats, int nfloats, const int32_t grid[3], void* stream);
+
+/* args [x, out] or [x, y, out] (x, y bf16 [n], out fp32 [1]); ints [n, programs]; only the whole
+ * grid.  Replaces: qwen3_8b_layer_decode_1x<S>_bf16/00_..._fused__to_copy_mean_pow_3iwn5auz_triton.py:17-41
+ *           and 05_..._fused__to_copy_add_mean_pow_tcz6sl32_triton.py:17-43 */
+int ptb_sumsq_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                   int nfloats, const int32_t grid[3], void* stream);
+/* ints [mode, k, n, extra, programs]; args, then a workspace descriptor of
+ * ptb_gemv_workspace_bytes(k, n) bytes (any dtype):
+ *   mode 0 (plain):   [x, W, y], extra 0
+ *   mode 1 (RMSNorm): [x, (add,) ss, g, W, y], extra = 1 with add; floats [eps]
+ *   mode 2 (silu):    [gate_up, W, (res_a, (res_b,)) y], extra = the residual count
+ * W [k, n] row-major bf16; only the whole grid.
+ * Replaces: gemm_1x2048x128_bf16/00_..._fused_mm_oyeae7au_triton.py:17-42 (the M = 1 mm template), decode
+ *           04_..._vumxrjnr_triton.py:17-42, 01_..._ddfn4f75_triton.py:17-55, 06_..._5gopcdje_triton.py:17-57,
+ *           07_..._3d4ocw7y_triton.py:17-56 of qwen3_8b_layer_decode_1x<S>_bf16 */
+int ptb_gemv_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                  int nfloats, const int32_t grid[3], void* stream);
+/* args [x (bf16 or fp32), out fp32 [1]] + a workspace descriptor of ptb_reduce_workspace_bytes(n)
+ * bytes; ints [n, op (PTB_REDUCE_SUM / PTB_REDUCE_MAX), programs]; only the whole grid.
+ * Replaces: vector_sum_<R>x<C>_bf16/00_..._2y6fwkvp_triton.py, vector_max_<R>x<C>_bf16/00_..._q47252w4_triton.py,
+ *           layer_layer_decode_1x<S>_bf16/18_..._fused_sum_7gslrk5a_triton.py:17-38 */
+int ptb_reduce_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                    int nfloats, const int32_t grid[3], void* stream);
+/* args [x, y] bf16 [n]; ints [n, programs (, block)]; floats [s]; a partial grid covers its leading
+ * blocks.  Replaces: vector_add1_<R>x<C>_bf16/00_..._du5rd5jd_triton.py */
+int ptb_add_scalar_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                        int nfloats, const int32_t grid[3], void* stream);
+/* args [x bf16, out fp32 [count]]; ints [first, count, programs]; floats [s]; first + count within
+ * x; only the whole grid.  Replaces: vector_slice_<R>x<C>_bf16/00_..._slnyinbt_triton.py:17-27 */
+int ptb_slice_add_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                       int nfloats, const int32_t grid[3], void* stream);
 
 #ifdef __cplusplus
 }

@@ -234,12 +234,14 @@ def rope_tables(tokens: int, head_dim: int = 128, theta: float = 1.0e6):
 
 
 def qwen3_layer(x: torch.Tensor, wts: dict, cos: torch.Tensor, sin: torch.Tensor, hq: int = 32, hkv: int = 8,
-                head_dim: int = 128, eps: float = 1e-6, bq: int = 1024) -> torch.Tensor:
+                head_dim: int = 128, eps: float = 1e-6, bq: int = 1024, gemm_fn=None) -> torch.Tensor:
     """The Qwen3-8B decoder layer as L2048/manifest.json's 14 launches compose it (data flow read
     from the kernels' index arithmetic): K00 rmsnorm -> K01/K03/K03 q/k/v projections -> K02/K04
     q/k norm + RoPE + head transpose -> K05 v transpose -> K06 causal GQA attention -> K07
     transpose back -> K08 o-projection + residual -> K00 rmsnorm -> K09 gate_up -> K10 silu_mul ->
-    K11 down projection + residual."""
+    K11 down projection + residual.  gemm_fn(a, b, residual=None) replaces the fp64-summed gemm
+    (the CPU baseline times the layer with the reference's fp32 matmul golden)."""
+    gemm = gemm_fn or globals()["gemm"]
     t = x.shape[0]
     xn = rmsnorm(x, wts["w_in"], eps)
     q = gemm(xn, wts["wq"])

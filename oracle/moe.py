@@ -107,21 +107,34 @@ def sort_rows(x: torch.Tensor, rows: int, descending: bool = False):
 
 
 def topk_rows(x: torch.Tensor, e: int, k: int, largest: bool = True):
-    """LOP_router_post/01__topk_kernel/_topk_kernel_triton.py:4-30: k rounds of: the row's max
-    (min), the lowest column holding it, that column marked spent (-inf / +inf) -- for rows of
-    numbers, the k largest (smallest) in order, equal values by lower column.  A NaN, which the
-    reference's comparisons leave to its backend, is ordered after every number and NaNs among
-    themselves by column (parity unpinned for NaN).  Restated as a stable two-key sort: by value,
-    then NaN-last.  Returns (values [rows*k] fp32, indices [rows*k] int64)."""
+    """LOP_router_post/01__topk_kernel/_topk_kernel_triton.py:4-28, round by round: columns past
+    the row and taken columns hold the spent value, -inf (+inf for the smallest, :10-14); each of
+    the k rounds takes the row's max (min, :18-21), the lowest column holding it (:22), records
+    both (:23-24) and marks that column spent (:25).  A column that holds the spent value itself is
+    therefore never reported by its own index: once only spent values remain, every further round
+    reports (spent, column 0), column 0 then holding the spent value.  Equal values (-0 == +0
+    included) go by lower column.  A NaN, which the reference's comparisons leave to its backend,
+    is ranked below every number and above the spent value, NaNs among themselves by column
+    (parity unpinned for NaN); a taken element is reported with its own value (for +-0 the
+    reference reports the max's zero, whose sign is the backend's).  Returns (values [rows*k]
+    fp32, indices [rows*k] int64)."""
     xr = x.reshape(-1, e).float()
-    v = xr.clone()
-    nan = torch.isnan(v)
-    v[nan] = 0.0
-    order = torch.sort(v, dim=1, descending=largest, stable=True).indices
-    order = torch.gather(order, 1, torch.sort(torch.gather(nan, 1, order).to(torch.int8), dim=1, stable=True).indices)
-    idxs = order[:, :k]
-    vals = torch.gather(xr, 1, idxs)
-    return vals.reshape(-1).contiguous(), idxs.to(I64).reshape(-1).contiguous()
+    rows = xr.shape[0]
+    spent = float("-inf") if largest else float("inf")
+    # the rounds run on fp64 keys, larger first: NaN sits below every fp32 number, above -inf
+    key = (xr if largest else -xr).double()
+    key = torch.where(torch.isnan(xr), torch.full_like(key, -1.7e308), key)
+    cols = torch.arange(e).expand(rows, e)
+    r = torch.arange(rows)
+    vals = torch.empty(rows, k, dtype=F32)
+    idxs = torch.empty(rows, k, dtype=I64)
+    for n in range(k):
+        best = key.max(dim=1).values
+        at = torch.where(key == best[:, None], cols, e).min(dim=1).values
+        vals[:, n] = torch.where(best == float("-inf"), torch.full((rows,), spent), xr[r, at])
+        idxs[:, n] = at
+        key[r, at] = float("-inf")
+    return vals.reshape(-1).contiguous(), idxs.reshape(-1).contiguous()
 
 
 def gather_rows(slot: torch.Tensor, x: torch.Tensor, k: int, cols: int) -> torch.Tensor:

@@ -56,6 +56,13 @@ int grid_programs(const int32_t* grid, int64_t bound, int64_t& gx) {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Rows (or elements) per program: ints[at] when the caller states it (the kernel's XBLOCK), else
+// the extent split evenly over the programs.  A program past the extent covers nothing.
+int block_of(const int64_t* ints, int nints, int at, int64_t extent, int64_t programs, int64_t& block) {
+  block = nints > at ? ints[at] : ceil_div(extent, programs);
+  return block > 0 || extent == 0 ? PTB_OK : PTB_ERR_SHAPE;
+}
+
 #define PTB_TRY(expr)           \
   do {                          \
     const int st_ = (expr);     \
@@ -67,23 +74,29 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 PTB_EXPORT int ptb_rmsnorm_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints,
                                 const double* floats, int nfloats, const int32_t grid[3], void* stream) {
   if (!args || !ints || !floats) return PTB_ERR_NULL;
-  if (nargs != 3 || nints != 3 || nfloats != 1) return PTB_ERR_SHAPE;
-  View x, w, y;
+  if ((nargs != 3 && nargs != 4) || (nints != 3 && nints != 4) || nfloats != 1) return PTB_ERR_SHAPE;
+  View x, w, y, c{nullptr, 0, 0};
   PTB_TRY(view_of(args[0], false, x));
   PTB_TRY(view_of(args[1], false, w));
   PTB_TRY(view_of(args[2], true, y));
+  if (nargs == 4) PTB_TRY(view_of(args[3], true, c));
   const int64_t rows = ints[0], cols = ints[1], programs = ints[2];
   if (rows < 0 || cols <= 0 || programs <= 0) return PTB_ERR_SHAPE;
-  if (x.n != rows * cols || y.n != x.n || w.n != cols) return PTB_ERR_SHAPE;
-  int64_t gx;
+  if (x.n != rows * cols || y.n != x.n || w.n != cols || (nargs == 4 && c.n != cols)) return PTB_ERR_SHAPE;
+  int64_t gx, block;
   PTB_TRY(grid_programs(grid, programs, gx));
-  const int64_t r = std::min(rows, gx * ceil_div(rows, programs));   // the row blocks the grid covers
+  PTB_TRY(block_of(ints, nints, 3, rows, programs, block));
+  const int64_t r = std::min(rows, gx * block);   // the row blocks the grid covers
   const float eps = float(floats[0]);
   if (x.dt == PTB_DTYPE_F32) {
-    if (w.dt != PTB_DTYPE_F32 || y.dt != PTB_DTYPE_F32) return PTB_ERR_DTYPE;
-    return ptb_rmsnorm_f32(static_cast<const float*>(x.p), static_cast<const float*>(w.p), static_cast<float*>(y.p),
-                           r, cols, eps, stream);
+    if (w.dt != PTB_DTYPE_F32 || y.dt != PTB_DTYPE_F32 || (nargs == 4 && c.dt != PTB_DTYPE_F32)) return PTB_ERR_DTYPE;
+    PTB_TRY(ptb_rmsnorm_f32(static_cast<const float*>(x.p), static_cast<const float*>(w.p), static_cast<float*>(y.p),
+                            r, cols, eps, stream));
+    // the column arm (tests/cases/workloads/rmsnorm.py:56-57): c = rsqrt(mean over the rows of x^2 + eps)
+    if (nargs == 4) return ptb_col_rms_f32(static_cast<const float*>(x.p), static_cast<float*>(c.p), r, cols, eps, stream);
+    return PTB_OK;
   }
+  if (nargs == 4) return PTB_ERR_DTYPE;   // the column arm exists in the fp32 case only
   if (x.dt != PTB_DTYPE_BF16 || y.dt != PTB_DTYPE_BF16) return PTB_ERR_DTYPE;
   if (w.dt != PTB_DTYPE_BF16 && w.dt != PTB_DTYPE_F32) return PTB_ERR_DTYPE;
   return ptb_rmsnorm_bf16(x.p, w.p, w.dt, y.p, r, cols, eps, stream);
@@ -93,16 +106,17 @@ PTB_EXPORT int ptb_softmax_args(const ptb_tensor* args, int nargs, const int64_t
                                 const double* floats, int nfloats, const int32_t grid[3], void* stream) {
   (void)floats;
   if (!args || !ints) return PTB_ERR_NULL;
-  if (nargs != 2 || nints != 3 || nfloats != 0) return PTB_ERR_SHAPE;
+  if (nargs != 2 || (nints != 3 && nints != 4) || nfloats != 0) return PTB_ERR_SHAPE;
   View x, y;
   PTB_TRY(view_of(args[0], false, x));
   PTB_TRY(view_of(args[1], true, y));
   const int64_t rows = ints[0], cols = ints[1], programs = ints[2];
   if (rows < 0 || cols <= 0 || programs <= 0) return PTB_ERR_SHAPE;
   if (x.n != rows * cols || y.n != x.n) return PTB_ERR_SHAPE;
-  int64_t gx;
+  int64_t gx, block;
   PTB_TRY(grid_programs(grid, programs, gx));
-  const int64_t r = std::min(rows, gx * ceil_div(rows, programs));
+  PTB_TRY(block_of(ints, nints, 3, rows, programs, block));
+  const int64_t r = std::min(rows, gx * block);
   if (x.dt == PTB_DTYPE_F32) {
     if (y.dt != PTB_DTYPE_F32) return PTB_ERR_DTYPE;
     return ptb_softmax_rows_f32(static_cast<const float*>(x.p), static_cast<float*>(y.p), r, cols, stream);
@@ -117,16 +131,17 @@ PTB_EXPORT int ptb_silu_mul_args(const ptb_tensor* args, int nargs, const int64_
                                  const double* floats, int nfloats, const int32_t grid[3], void* stream) {
   (void)floats;
   if (!args || !ints) return PTB_ERR_NULL;
-  if (nargs != 2 || nints != 3 || nfloats != 0) return PTB_ERR_SHAPE;
+  if (nargs != 2 || (nints != 3 && nints != 4) || nfloats != 0) return PTB_ERR_SHAPE;
   View gu, out;
   PTB_TRY(view_of(args[0], false, gu));
   PTB_TRY(view_of(args[1], true, out));
   const int64_t rows = ints[0], inter = ints[1], programs = ints[2];
   if (rows < 0 || inter <= 0 || programs <= 0) return PTB_ERR_SHAPE;
   if (gu.n != 2 * rows * inter || out.n != rows * inter || gu.dt != out.dt) return PTB_ERR_SHAPE;
-  int64_t gx;
+  int64_t gx, block;
   PTB_TRY(grid_programs(grid, programs, gx));
-  const int64_t n = std::min(rows * inter, gx * ceil_div(rows * inter, programs));   // outputs the grid covers
+  PTB_TRY(block_of(ints, nints, 3, rows * inter, programs, block));
+  const int64_t n = std::min(rows * inter, gx * block);   // outputs the grid covers
   if (n % inter) return PTB_ERR_UNSUPPORTED;             // a partial grid must end on a whole row
   if (gu.dt == PTB_DTYPE_F32)
     return ptb_silu_mul_f32(static_cast<const float*>(gu.p), static_cast<float*>(out.p), n / inter, inter, stream);
@@ -235,4 +250,151 @@ PTB_EXPORT int ptb_transpose_heads_args(const ptb_tensor* args, int nargs, const
   PTB_TRY(grid_programs(grid, programs, gx));
   if (gx != programs) return PTB_ERR_UNSUPPORTED;
   return ptb_transpose_heads_bf16(x.p, y.p, d0, d1, inner, stream);
+}
+
+namespace {
+
+// The whole grid only: these families reduce over, or address, every element of their tensors.
+int whole_grid(const int32_t* grid, int64_t programs) {
+  int64_t gx;
+  PTB_TRY(grid_programs(grid, programs, gx));
+  return gx == programs ? PTB_OK : PTB_ERR_UNSUPPORTED;
+}
+
+// A trailing workspace descriptor (any dtype), written by the entry: its pointer and bytes.
+int workspace_of(const ptb_tensor* args, int nargs, int at, void*& p, size_t& bytes) {
+  p = nullptr;
+  bytes = 0;
+  if (nargs == at) return PTB_OK;
+  if (nargs != at + 1) return PTB_ERR_SHAPE;
+  View ws;
+  PTB_TRY(view_of(args[at], true, ws));
+  p = ws.p;
+  bytes = size_t(ws.n * itemsize(ws.dt));
+  return PTB_OK;
+}
+
+}  // namespace
+
+PTB_EXPORT int ptb_sumsq_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints,
+                              const double* floats, int nfloats, const int32_t grid[3], void* stream) {
+  (void)floats;
+  if (!args || !ints) return PTB_ERR_NULL;
+  if ((nargs != 2 && nargs != 3) || nints != 2 || nfloats != 0) return PTB_ERR_SHAPE;
+  View x, y{nullptr, 0, PTB_DTYPE_BF16}, out;
+  PTB_TRY(view_of(args[0], false, x));
+  if (nargs == 3) PTB_TRY(view_of(args[1], false, y));
+  PTB_TRY(view_of(args[nargs - 1], true, out));
+  const int64_t n = ints[0], programs = ints[1];
+  if (n < 0 || programs <= 0) return PTB_ERR_SHAPE;
+  if (x.n != n || (nargs == 3 && y.n != n) || out.n != 1) return PTB_ERR_SHAPE;
+  if (x.dt != PTB_DTYPE_BF16 || y.dt != PTB_DTYPE_BF16 || out.dt != PTB_DTYPE_F32) return PTB_ERR_DTYPE;
+  PTB_TRY(whole_grid(grid, programs));
+  return ptb_sumsq_bf16(x.p, nargs == 3 ? y.p : nullptr, static_cast<float*>(out.p), n, stream);
+}
+
+PTB_EXPORT int ptb_gemv_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints, const double* floats,
+                             int nfloats, const int32_t grid[3], void* stream) {
+  if (!args || !ints) return PTB_ERR_NULL;
+  if (nints != 5) return PTB_ERR_SHAPE;
+  const int64_t mode = ints[0], k = ints[1], n = ints[2], extra = ints[3], programs = ints[4];
+  if (k <= 0 || n <= 0 || programs <= 0) return PTB_ERR_SHAPE;
+  // tensors before the workspace: plain [x, W, y]; rmsnorm [x, (add,) ss, g, W, y]; silu
+  // [gate_up, W, (res_a, (res_b,)) y]
+  int base;
+  if (mode == 0 && extra == 0) base = 3;
+  else if (mode == 1 && (extra == 0 || extra == 1)) base = 5 + int(extra);
+  else if (mode == 2 && extra >= 0 && extra <= 2) base = 3 + int(extra);
+  else return PTB_ERR_UNSUPPORTED;
+  if (nargs < base || nfloats != (mode == 1 ? 1 : 0) || (mode == 1 && !floats)) return PTB_ERR_SHAPE;
+  View v[6];
+  for (int i = 0; i < base; ++i) PTB_TRY(view_of(args[i], i == base - 1, v[i]));
+  void* ws;
+  size_t ws_bytes;
+  PTB_TRY(workspace_of(args, nargs, base, ws, ws_bytes));
+  const View& y = v[base - 1];
+  if (y.n != n || y.dt != PTB_DTYPE_BF16) return y.n != n ? PTB_ERR_SHAPE : PTB_ERR_DTYPE;
+  PTB_TRY(whole_grid(grid, programs));
+  if (mode == 0) {
+    const View &x = v[0], &w = v[1];
+    if (x.n != k || w.n != k * n) return PTB_ERR_SHAPE;
+    if (x.dt != PTB_DTYPE_BF16 || w.dt != PTB_DTYPE_BF16) return PTB_ERR_DTYPE;
+    return ptb_gemv_bf16(x.p, w.p, y.p, k, n, ws, ws_bytes, stream);
+  }
+  if (mode == 1) {
+    const View& x = v[0];
+    const View* add = extra ? &v[1] : nullptr;
+    const View &ss = v[1 + extra], &g = v[2 + extra], &w = v[3 + extra];
+    if (x.n != k || (add && add->n != k) || ss.n != 1 || g.n != k || w.n != k * n) return PTB_ERR_SHAPE;
+    if (x.dt != PTB_DTYPE_BF16 || (add && add->dt != PTB_DTYPE_BF16) || ss.dt != PTB_DTYPE_F32 ||
+        g.dt != PTB_DTYPE_BF16 || w.dt != PTB_DTYPE_BF16)
+      return PTB_ERR_DTYPE;
+    return ptb_gemv_rmsnorm_bf16(x.p, add ? add->p : nullptr, static_cast<const float*>(ss.p), g.p,
+                                 float(floats[0]), w.p, y.p, k, n, ws, ws_bytes, stream);
+  }
+  const View &gu = v[0], &w = v[1];
+  if (gu.n != 2 * k || w.n != k * n) return PTB_ERR_SHAPE;
+  for (int i = 2; i < 2 + extra; ++i)
+    if (v[i].n != n) return PTB_ERR_SHAPE;
+  for (int i = 0; i < base; ++i)
+    if (v[i].dt != PTB_DTYPE_BF16) return PTB_ERR_DTYPE;
+  return ptb_gemv_silu_bf16(gu.p, w.p, extra > 0 ? v[2].p : nullptr, extra > 1 ? v[3].p : nullptr, y.p, k, n, ws,
+                            ws_bytes, stream);
+}
+
+PTB_EXPORT int ptb_reduce_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints,
+                               const double* floats, int nfloats, const int32_t grid[3], void* stream) {
+  (void)floats;
+  if (!args || !ints) return PTB_ERR_NULL;
+  if ((nargs != 2 && nargs != 3) || nints != 3 || nfloats != 0) return PTB_ERR_SHAPE;
+  View x, out;
+  PTB_TRY(view_of(args[0], false, x));
+  PTB_TRY(view_of(args[1], true, out));
+  void* ws;
+  size_t ws_bytes;
+  PTB_TRY(workspace_of(args, nargs, 2, ws, ws_bytes));
+  const int64_t n = ints[0], op = ints[1], programs = ints[2];
+  if (n < 0 || programs <= 0) return PTB_ERR_SHAPE;
+  if (op != PTB_REDUCE_SUM && op != PTB_REDUCE_MAX) return PTB_ERR_UNSUPPORTED;
+  if (x.n != n || out.n != 1) return PTB_ERR_SHAPE;
+  if (out.dt != PTB_DTYPE_F32) return PTB_ERR_DTYPE;
+  PTB_TRY(whole_grid(grid, programs));
+  if (x.dt == PTB_DTYPE_BF16)
+    return ptb_reduce_bf16(x.p, static_cast<float*>(out.p), n, int(op), ws, ws_bytes, stream);
+  if (x.dt == PTB_DTYPE_F32)
+    return ptb_reduce_f32(static_cast<const float*>(x.p), static_cast<float*>(out.p), n, int(op), ws, ws_bytes,
+                          stream);
+  return PTB_ERR_DTYPE;
+}
+
+PTB_EXPORT int ptb_add_scalar_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints,
+                                   const double* floats, int nfloats, const int32_t grid[3], void* stream) {
+  if (!args || !ints || !floats) return PTB_ERR_NULL;
+  if (nargs != 2 || (nints != 2 && nints != 3) || nfloats != 1) return PTB_ERR_SHAPE;
+  View x, y;
+  PTB_TRY(view_of(args[0], false, x));
+  PTB_TRY(view_of(args[1], true, y));
+  const int64_t n = ints[0], programs = ints[1];
+  if (n < 0 || programs <= 0) return PTB_ERR_SHAPE;
+  if (x.n != n || y.n != n) return PTB_ERR_SHAPE;
+  if (x.dt != PTB_DTYPE_BF16 || y.dt != PTB_DTYPE_BF16) return PTB_ERR_DTYPE;
+  int64_t gx, block;   // programs over blocks of elements: a partial grid covers its leading blocks
+  PTB_TRY(grid_programs(grid, programs, gx));
+  PTB_TRY(block_of(ints, nints, 2, n, programs, block));
+  return ptb_add_scalar_bf16(x.p, y.p, std::min(n, gx * block), float(floats[0]), stream);
+}
+
+PTB_EXPORT int ptb_slice_add_args(const ptb_tensor* args, int nargs, const int64_t* ints, int nints,
+                                  const double* floats, int nfloats, const int32_t grid[3], void* stream) {
+  if (!args || !ints || !floats) return PTB_ERR_NULL;
+  if (nargs != 2 || nints != 3 || nfloats != 1) return PTB_ERR_SHAPE;
+  View x, out;
+  PTB_TRY(view_of(args[0], false, x));
+  PTB_TRY(view_of(args[1], true, out));
+  const int64_t first = ints[0], count = ints[1], programs = ints[2];
+  if (first < 0 || count < 0 || programs <= 0) return PTB_ERR_SHAPE;
+  if (out.n != count || first + count > x.n) return PTB_ERR_SHAPE;
+  if (x.dt != PTB_DTYPE_BF16 || out.dt != PTB_DTYPE_F32) return PTB_ERR_DTYPE;
+  PTB_TRY(whole_grid(grid, programs));
+  return ptb_slice_add_bf16(x.p, static_cast<float*>(out.p), first, count, float(floats[0]), stream);
 }

@@ -1,26 +1,32 @@
 // bf16 GEMM on gfx950 matrix cores: C[M,N] = A[M,K] * B[K,N] (+ R[M,N]), all row-major, fp32
 // accumulation, one bf16 rounding at the store.
 //
-// Workgroup tile 256x256, K step 32, 4 waves in a 2x2 arrangement, each wave owning a 128x128
-// sub-tile as 4x4 v_mfma_f32_32x32x16_bf16 accumulators (256 fp32 per lane, held in AGPRs).
+// Workgroup tiles of 256x256, 256x192, 256x128, 128x128 or 64x128 (Shape below), 4 waves in a 2x2
+// arrangement, each wave owning WM x WN v_mfma_f32_32x32x16_bf16 accumulators (256 fp32 per lane
+// for 256x256 tiles, held in AGPRs).
 //
-// Operands move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging) into a ring of four
-// 32 KB LDS stages, three K steps ahead of the matrix cores, so two to three microseconds of memory
-// latency stay hidden behind MFMA work.  Each stage holds the A tile [256 rows][32 k] and the B tile
-// [32 k][256 n] in their global layouts, with 16-byte chunks XOR-swizzled per row so that every LDS
-// read below is bank-conflict free:
-//   A fragments (8 consecutive k of one row per lane) are plain 128-bit LDS reads;
+// Operands move HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging).  256-row tiles stage
+// 64 K columns at a time (a whole 128-byte line of every A row) -- 256x128 tiles in a ring of three
+// slots, 256x256 and 256x192 tiles in rings of three A slots and two B slots (160 / 144 KB) -- and
+// 128x128 and smaller tiles 32 columns in rings of four slots.  Each stage's DMAs run two (or three)
+// stages ahead and spread over a whole K step's MFMAs, into the slots the previous step's barrier
+// freed.  A and B keep their global layouts in LDS with 16-byte chunks XOR-swizzled per row, so
+// every fragment read is bank-conflict free:
+//   A fragments (8 consecutive k of one row per lane) are plain 128-bit LDS reads; row m keeps
+//   chunk c in slot c ^ ((m >> 1) & 7) for 64-deep stages, c ^ ((m >> 2) & 3) for 32-deep ones;
 //   B fragments (8 consecutive k of one column per lane, while B is N-contiguous) come from two
-//   ds_read_b64_tr_b16 transposing reads: within each 16-lane group, lane 4j+q supplies row k+j,
-//   columns n+4q..n+4q+3, and lane i receives rows k..k+3 of column n+i.
-// Swizzles: A row m keeps chunk c in slot c ^ ((m >> 2) & 3); B row k keeps chunk c in slot
-// c ^ (4 * (k & 3)), so the 4 rows x 4 chunks a half-wave reads land in 16 distinct bank groups.
-// The fragments of the next 16-wide K slice are always read while the MFMAs of the current one
-// run (the last slice of a step reads the first slice of the next stage, behind the barrier that
-// publishes it), so LDS latency stays off the matrix cores' critical path.
-// The MFMA is issued with B as its first operand, so each accumulator holds a 32x32 block of C^T:
-// a lane's four consecutive registers are four consecutive columns of one row of C, stored (with
-// the residual read) as one 8-byte access.
+//   ds_read_b64_tr_b16 transposing reads; row k keeps chunk c in slot c ^ (4 * (k & 3)) (rows of
+//   384 bytes: c ^ (4 * ((k >> 1) & 1))).
+// The fragments of the next 16-wide K slice are read while the MFMAs of the current one run, and
+// the main loop runs a whole number of ring turns a trip, so every slot address is a constant.
+// The MFMA is issued with B as its first operand, so each accumulator holds a 32x32 block of C^T.
+// The epilogue stages each wave's 32-row blocks of fp32 results through a private, padded LDS
+// region (the rings are free by then) so that stores, and residual loads, cover whole rows; buffer
+// resources drop rows and columns outside C.
+//
+// Modes: plain (+ residual), split-K into fp32 partials (splitk_finish sums them), SwiGLU (the gate
+// and up columns of the same outputs meet in one wave; the epilogue stores silu(gate) * up) and
+// grouped (the MoE grouped GEMM: a program table maps row tiles to weights).
 //
 // Tile order is XCD-aware: hardware hands workgroup i to XCD i % 8, so ids are remapped to give
 // each XCD a contiguous range of tiles, walked in groups of 8 tile-rows for L2 reuse.

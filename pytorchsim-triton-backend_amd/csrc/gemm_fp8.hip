@@ -21,6 +21,7 @@
 // address unit and stall the MFMAs: config 4 85 -> 82 us); a two-stage ring refills the slot its
 // own barrier frees, during substep 1.  MFMAs take W as the first operand, so accumulators hold C^T blocks and each lane
 // stores 4 consecutive columns of a row of C at once.
+#include <algorithm>
 #include <type_traits>
 
 #include "ptb_common.h"
@@ -423,27 +424,122 @@ __global__ __launch_bounds__(kQBlock) void quant_rows_block(const uint16_t* __re
 }
 
 // ---- per-output-channel weight quantiser
-// absmax over K of each column j of W[K,N]: block = 64 columns x 4 K-slices.
-__global__ __launch_bounds__(256) void weight_absmax(const float* __restrict__ w, float* __restrict__ scale,
-                                                     int64_t K, int64_t N) {
-  __shared__ float red[4][64];
-  const int64_t j = int64_t(blockIdx.x) * 64 + (threadIdx.x & 63);
-  const int slice = threadIdx.x >> 6;
-  float amax = 0.f;
-  if (j < N)
-    for (int64_t i = slice; i < K; i += 4) amax = fmaxf(amax, fabsf(w[i * N + j]));
-  red[slice][threadIdx.x & 63] = amax;
+// Column absmax of W[K,N] as the bits of |w|: non-negative floats order like their bit patterns, and
+// a NaN's bits exceed every number's, so an unsigned max propagates NaN as torch's amax does (the
+// scale of such a column is then 1, as `amax > 0` fails).  The bits collect in amax[N] (zeroed
+// first) by one atomicMax per column and K slice.
+__global__ __launch_bounds__(256) void fill_zero_u32(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Block (64 columns, K slice of `rows` rows, a multiple of 16): lane l of wave v reads the 16 bytes of
+// columns 4*(l % 16) .. +3 of rows k0 + 16*t + 4*v + l/16, eight loads in flight; the 16 row lanes
+// sharing a column meet in LDS.  N % 4 == 0, W 16-byte aligned.
+__global__ __launch_bounds__(256) void weight_absmax_part(const float* __restrict__ w, uint32_t* __restrict__ amax,
+                                                          int64_t K, int64_t N, int64_t rows) {
+  __shared__ uint32_t red[16][65];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t c = int64_t(blockIdx.x) * 64 + 4 * (lane & 15);
+  const int64_t k0 = int64_t(blockIdx.y) * rows, k1 = min(K, k0 + rows);
+  const int rr = 4 * wv + (lane >> 4);
+  uint32_t m[4] = {0u, 0u, 0u, 0u};
+  if (c < N) {
+    for (int64_t kb = k0; kb < k1; kb += 16 * 8) {
+      f32x4v v[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int64_t k = kb + 16 * t + rr;
+        v[t] = k < k1 ? *reinterpret_cast<const f32x4v*>(w + k * N + c) : f32x4v{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m[e] = max(m[e], __float_as_uint(v[t][e]) & 0x7fffffffu);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red[rr][4 * (lane & 15) + e] = m[e];
   __syncthreads();
-  if (slice == 0 && j < N) {
-    const float m = fmaxf(fmaxf(red[0][threadIdx.x], red[1][threadIdx.x]), fmaxf(red[2][threadIdx.x], red[3][threadIdx.x]));
-    scale[j] = m > 0.f ? m / 448.0f : 1.0f;
+  if (threadIdx.x < 64) {
+    const int64_t j = int64_t(blockIdx.x) * 64 + threadIdx.x;
+    uint32_t r = red[0][threadIdx.x];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) r = max(r, red[i][threadIdx.x]);
+    if (j < N) atomicMax(amax + j, r);
   }
 }
 
-// quantise + transpose through a 64x64 LDS tile: read W[i0:i0+64, j0:j0+64] along j, write
-// Wt[j0:j0+64, i0:i0+64] along i.
-__global__ __launch_bounds__(256) void weight_quant_t(const float* __restrict__ w, const float* __restrict__ scale,
+__device__ __forceinline__ float weight_scale(uint32_t amax_bits) {
+  const float m = __uint_as_float(amax_bits);
+  return m > 0.f ? m / 448.0f : 1.0f;
+}
+
+// quantise + transpose: block (64 columns j, 256 rows i); each thread quantises 4 rows x 4 columns
+// (four 16-byte row loads) into four dwords of 4 consecutive i, which meet in an LDS tile [j][i/4];
+// then each wave stores 16 rows of Wt, 256 contiguous bytes a store instruction.  K % 4 == 0.
+__global__ __launch_bounds__(256) void weight_quant_t(const float* __restrict__ w, const uint32_t* __restrict__ amax,
                                                       uint8_t* __restrict__ wt, int64_t K, int64_t N) {
+  __shared__ uint32_t tile[64][65];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t i0 = int64_t(blockIdx.y) * 256, j0 = int64_t(blockIdx.x) * 64;
+  const int cq = lane & 15;
+  const int64_t c = j0 + 4 * cq;
+  float s[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s[e] = c + e < N ? weight_scale(amax[c + e]) : 1.0f;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int g = (lane >> 4) + 4 * wv + 16 * it;    // group of 4 consecutive rows
+    f32x4v v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t i = i0 + 4 * g + r;
+      v[r] = (i < K && c < N) ? *reinterpret_cast<const f32x4v*>(w + i * N + c) : f32x4v{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t q = 0u;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) q |= f32_to_e4m3(v[r][e] / s[e]) << (8 * r);
+      tile[4 * cq + e][g] = q;
+    }
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int r = 0; r < 16; ++r) {
+    const int jj = 16 * wv + r;
+    const int64_t i = i0 + 4 * lane;
+    if (j0 + jj < N && i < K) *reinterpret_cast<uint32_t*>(wt + (j0 + jj) * K + i) = tile[jj][lane];
+  }
+}
+
+// the scales from the collected absmax bits, in place
+__global__ __launch_bounds__(256) void weight_scales(uint32_t* __restrict__ amax, int64_t n) {
+  const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (j < n) amax[j] = __float_as_uint(weight_scale(amax[j]));
+}
+
+// Any shape: absmax over K of each column by one block of 64 columns x 4 K-slices, then quantise +
+// transpose through a 64x64 byte tile.
+__global__ __launch_bounds__(256) void weight_absmax_any(const float* __restrict__ w, float* __restrict__ scale,
+                                                         int64_t K, int64_t N) {
+  __shared__ uint32_t red[4][64];
+  const int64_t j = int64_t(blockIdx.x) * 64 + (threadIdx.x & 63);
+  const int slice = threadIdx.x >> 6;
+  uint32_t amax = 0u;
+  if (j < N)
+    for (int64_t i = slice; i < K; i += 4) amax = max(amax, __float_as_uint(w[i * N + j]) & 0x7fffffffu);
+  red[slice][threadIdx.x & 63] = amax;
+  __syncthreads();
+  if (slice == 0 && j < N) {
+    const uint32_t m = max(max(red[0][threadIdx.x], red[1][threadIdx.x]), max(red[2][threadIdx.x], red[3][threadIdx.x]));
+    scale[j] = weight_scale(m);
+  }
+}
+
+__global__ __launch_bounds__(256) void weight_quant_t_any(const float* __restrict__ w, const float* __restrict__ scale,
+                                                          uint8_t* __restrict__ wt, int64_t K, int64_t N) {
   __shared__ uint8_t tile[64][65];
   const int64_t i0 = int64_t(blockIdx.y) * 64, j0 = int64_t(blockIdx.x) * 64;
   const int tj = threadIdx.x & 63, ti = threadIdx.x >> 6;
@@ -497,11 +593,25 @@ PTB_EXPORT int ptb_quant_rows_e4m3(const void* x, void* xq, float* scale, int64_
 PTB_EXPORT int ptb_quant_weight_e4m3(const float* w, void* wq_t, float* scale, int64_t k, int64_t n, void* stream) {
   if (!w || !wq_t || !scale) return PTB_ERR_NULL;
   if (k <= 0 || n <= 0) return PTB_ERR_SHAPE;
-  const int64_t gx = (n + 63) / 64, gy = (k + 63) / 64;
-  if (gx > 0x7fffffff || gy > 65535) return PTB_ERR_GRID;
+  const int64_t gx = (n + 63) / 64;
+  if (gx > 0x7fffffff || (k + 63) / 64 > 65535) return PTB_ERR_GRID;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  weight_absmax<<<dim3(unsigned(gx)), dim3(256), 0, s>>>(w, scale, k, n);
-  weight_quant_t<<<dim3(unsigned(gx), unsigned(gy)), dim3(256), 0, s>>>(w, scale, static_cast<uint8_t*>(wq_t), k, n);
+  uint8_t* wt = static_cast<uint8_t*>(wq_t);
+  if (n % 4 || k % 4 || !aligned16(w) || (reinterpret_cast<uintptr_t>(wq_t) & 3u)) {
+    weight_absmax_any<<<dim3(unsigned(gx)), dim3(256), 0, s>>>(w, scale, k, n);
+    weight_quant_t_any<<<dim3(unsigned(gx), unsigned((k + 63) / 64)), dim3(256), 0, s>>>(w, scale, wt, k, n);
+    return launch_status();
+  }
+  // the column maxima split over K so that about 2048 blocks cover the chip: K slices of a
+  // multiple of 16 rows; the scale array holds the absmax bits until the last launch
+  uint32_t* amax = reinterpret_cast<uint32_t*>(scale);
+  const int64_t want = std::max<int64_t>(1, std::min<int64_t>((2048 + gx - 1) / gx, (k + 127) / 128));
+  const int64_t rows = ((k + want - 1) / want + 15) / 16 * 16;
+  const int64_t gy = (k + rows - 1) / rows;
+  fill_zero_u32<<<dim3(unsigned((n + 255) / 256)), dim3(256), 0, s>>>(amax, n);
+  weight_absmax_part<<<dim3(unsigned(gx), unsigned(gy)), dim3(256), 0, s>>>(w, amax, k, n, rows);
+  weight_quant_t<<<dim3(unsigned(gx), unsigned((k + 255) / 256)), dim3(256), 0, s>>>(w, amax, wt, k, n);
+  weight_scales<<<dim3(unsigned((n + 255) / 256)), dim3(256), 0, s>>>(amax, n);
   return launch_status();
 }
 

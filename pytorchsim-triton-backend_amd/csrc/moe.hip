@@ -464,26 +464,28 @@ __global__ __launch_bounds__(kB) void sort_emit(const int64_t* __restrict__ sk, 
 }
 
 // ---------------------------------------------------------------- top-k
-// Order of the elements (both kernels): value, larger first (smaller first for largest = false),
-// equal values by lower position; a NaN ranks after every number (for either direction) and NaNs
-// among themselves by position.  This is the order the reference's k rounds of "take the best, lowest
-// position first, mark it spent" give rows without NaN; for NaN, which the reference's comparisons
-// leave to the backend, it fixes one deterministic order (the 32-bit key below).
+// The reference's k rounds of "take the best, lowest position first, mark it spent (-inf for the
+// largest, +inf for the smallest)".  Elements other than the spent value come out in order of value,
+// larger first (smaller first for largest = false), equal values by lower position; a NaN, which
+// the reference's comparisons leave to the backend, ranks after every number (for either
+// direction) and NaNs among themselves by position (the 32-bit key below).  An element holding the
+// spent value is never taken as itself: once the others are used up, every further round finds
+// only spent values and reports (spent, position 0), as the reference's rounds do.
 // order-preserving bits of a float: larger value, larger unsigned key
 __device__ __forceinline__ uint32_t order_bits(float v) {
   const uint32_t u = __float_as_uint(v);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 // The key of element v of a row searched for its largest (v already negated for smallest-k): a NaN
-// gets 1, below every number's key and above 0 (taken or absent elements); -0 and +0 share a key, as
-// they compare equal.
+// gets 1, below every number's key and above 0, the key of taken, absent and spent (-inf) elements;
+// -0 and +0 share a key, as they compare equal.
 __device__ __forceinline__ uint32_t topk_key(float v) {
-  return v != v ? 1u : (v == 0.f ? 0x80000000u : order_bits(v));
+  return v != v ? 1u : (v == 0.f ? 0x80000000u : (v == -INFINITY ? 0u : order_bits(v)));
 }
 
 // One wave per row, the keys in LDS: element c's rank is the number of elements ordered before it
-// (a larger key, or an equal key at a lower position); the elements of rank < k are the k selected,
-// in order.
+// (a larger key, or an equal key at a lower position); the elements of rank < k other than spent
+// ones are the selected, in order, and ranks from the count of the others up to k report (spent, 0).
 constexpr int kTopkMax = 1024;   // row length
 constexpr int kTopkRows = kB / kWave;
 __global__ __launch_bounds__(kB) void topk_rows(const float* __restrict__ x, int64_t rows, int e, int k, bool largest,
@@ -511,10 +513,17 @@ __global__ __launch_bounds__(kB) void topk_rows(const float* __restrict__ x, int
         rank += int((o[t] > v) | ((o[t] == v) & (j < c)));   // bitwise: no short-circuit branches
       }
     }
-    if (rank < k) {
+    if (v != 0u && rank < k) {
       vals[row * k + rank] = x[row * e + c];
       idx[row * k + rank] = c;
     }
+  }
+  int present = 0;   // elements other than spent ones: at most 1024, exact in the fp32 sum
+  for (int c = lane; c < e; c += kWave) present += r[c] != 0u;
+  present = int(wave_sum(float(present)));
+  for (int n = present + lane; n < k; n += kWave) {
+    vals[row * k + n] = largest ? -INFINITY : INFINITY;
+    idx[row * k + n] = 0;
   }
 }
 
@@ -522,8 +531,8 @@ __global__ __launch_bounds__(kB) void topk_rows(const float* __restrict__ x, int
 // (lane l holds elements l, l + 64, ...), every load in flight at once, then k rounds of a wave
 // argmax over the elements not yet taken.  The 64-bit key (topk_key of the value, then the inverted
 // position) makes a round's winner the largest value and, among equal values, the lowest position:
-// the same selection and order as the rank kernel above.  Taken and absent elements hold key 0,
-// below every present one.
+// the same selection and order as the rank kernel above.  Taken, absent and spent elements hold key
+// 0, below every present one; a round whose winner is key 0 reports (spent, 0).
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xf, 0xf, false));
@@ -567,7 +576,7 @@ __global__ __launch_bounds__(kB) void topk_rows_wave(const float* __restrict__ x
   for (int r = 0; r < R; ++r) {
     const bool in = lane + kWave * r < e;
     kh[r] = in ? topk_key(sgn * raw[r]) : 0u;
-    kl[r] = in ? ~uint32_t(lane + kWave * r) : 0u;
+    kl[r] = kh[r] != 0u ? ~uint32_t(lane + kWave * r) : 0u;
   }
   float outv = 0.f;
   int outi = 0;
@@ -576,11 +585,11 @@ __global__ __launch_bounds__(kB) void topk_rows_wave(const float* __restrict__ x
 #pragma unroll
     for (int r = 1; r < R; ++r) key_max(bh, bl, kh[r], kl[r]);
     wave_key_max(bh, bl);
-    const int pos = int(~bl);
+    const int pos = bh != 0u ? int(~bl) : 0;   // only spent values left: (spent, 0)
     float mine = raw[0];   // the element at position pos, from the lane that holds it
 #pragma unroll
     for (int r = 1; r < R; ++r) mine = pos / kWave == r ? raw[r] : mine;
-    const float won = __shfl(mine, pos % kWave, kWave);
+    const float won = bh != 0u ? __shfl(mine, pos % kWave, kWave) : (largest ? -INFINITY : INFINITY);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const bool taken = lane + kWave * r == pos;

@@ -87,7 +87,7 @@ _ARGS_SIG = (ctypes.c_int, [ctypes.POINTER(PtbTensor), ctypes.c_int, ctypes.POIN
                             ctypes.POINTER(ctypes.c_double), ctypes.c_int, ctypes.POINTER(ctypes.c_int32),
                             ctypes.c_void_p])
 ARGS_FAMILIES = ("rmsnorm", "softmax", "silu_mul", "gemm", "flash_attn", "attn_decode", "qk_norm_rope",
-                 "transpose_heads")
+                 "transpose_heads", "sumsq", "gemv", "reduce", "add_scalar", "slice_add")
 
 # name -> (restype, argtypes), mirroring include/ptb_amd.h
 SIGNATURES = {

@@ -23,7 +23,9 @@ ROLE = {"in": _lib.PTB_ROLE_IN, "out": _lib.PTB_ROLE_OUT, "inout": _lib.PTB_ROLE
 # the families with a ptb_<family>_args entry, by the name kernels.resolve gives them
 FAMILY_ENTRY = {"rmsnorm": "rmsnorm", "softmax": "softmax", "silu_mul": "silu_mul", "gemm": "gemm",
                 "attention": "flash_attn", "attention_decode": "attn_decode", "qk_norm_rope": "qk_norm_rope",
-                "transpose": "transpose_heads"}
+                "transpose": "transpose_heads", "sumsq": "sumsq", "gemv": "gemv", "reduce": "reduce",
+                "add_scalar": "add_scalar", "slice_add": "slice_add"}
+_GEMV_MODE = {"plain": 0, "rms": 1, "silu": 2}
 
 
 def descriptor(t: torch.Tensor, role: str = "in") -> _lib.PtbTensor:
@@ -52,19 +54,21 @@ def call_args(family: str, tensors, roles, ints=(), floats=(), grid=(1, 1, 1), s
     _lib.call(f"ptb_{family}_args", descs, n, iv, len(ints), fv, len(floats), gv, stream)
 
 
-def plan_args(plan, programs: int):
+def plan_args(plan, programs: int, block: int | None = None):
     """(entry, tensor names in the entry's order, ints, floats) for a resolved plan whose compiled
-    kernel has `programs` programs along x; None for a family without a spec-driven entry."""
+    kernel has `programs` programs along x (of `block` rows or elements each, its XBLOCK, for the
+    row-block families when stated); None for a family without a spec-driven entry."""
     p, f = plan.params, plan.family
     if f not in FAMILY_ENTRY:
         return None
     e = FAMILY_ENTRY[f]
+    blk = [int(block)] if block else []
     if f == "rmsnorm":
-        return e, [p["x"], p["w"], p["y"]], [p["rows"], p["cols"], programs], [p["eps"]]
+        return e, [p["x"], p["w"], p["y"]], [p["rows"], p["cols"], programs] + blk, [p["eps"]]
     if f == "softmax":
-        return e, [p["x"], p["y"]], [p["rows"], p["cols"], programs], []
+        return e, [p["x"], p["y"]], [p["rows"], p["cols"], programs] + blk, []
     if f == "silu_mul":
-        return e, [p["x"], p["y"]], [p["rows"], p["inter"], programs], []
+        return e, [p["x"], p["y"]], [p["rows"], p["inter"], programs] + blk, []
     if f == "gemm":
         names = ([p["residual"]] if p["residual"] else []) + [p["a"], p["b"], p["c"]]
         return e, names, [p["m"], p["n"], p["k"], programs], []
@@ -78,10 +82,44 @@ def plan_args(plan, programs: int):
                 [p["eps"]])
     if f == "transpose":
         return e, [p["x"], p["y"]], [p["d0"], p["d1"], p["inner"], programs], []
+    if f == "sumsq":
+        return e, [p["x"]] + ([p["y"]] if p["y"] else []) + [p["out"]], [p["n"], programs], []
+    if f == "gemv":
+        mode = p["mode"]
+        if mode == "plain":
+            names, extra, floats = [p["x"], p["w"], p["y"]], 0, []
+        elif mode == "rms":
+            names = [p["x"]] + ([p["add"]] if p["add"] else []) + [p["ss"], p["g"], p["w"], p["y"]]
+            extra, floats = (1 if p["add"] else 0), [p["eps"]]
+        else:
+            res = [r for r in (p["res_a"], p["res_b"]) if r]
+            names, extra, floats = [p["x"], p["w"]] + res + [p["y"]], len(res), []
+        return e, names, [_GEMV_MODE[mode], p["k"], p["n"], extra, programs], floats
+    if f == "reduce":
+        op = _lib.PTB_REDUCE_SUM if p["op"] == "sum" else _lib.PTB_REDUCE_MAX
+        return e, [p["x"], p["y"]], [p["n"], op, programs], []
+    if f == "add_scalar":
+        return e, [p["x"], p["y"]], [p["n"], programs] + blk, [p["s"]]
+    if f == "slice_add":
+        return e, [p["x"], p["y"]], [p["first"], p["count"], programs], [p["s"]]
     return None
 
 
 def decode_workspace(nkv: int, group: int, seq: int, device) -> torch.Tensor | None:
     """The decode attention entry's workspace descriptor tensor (None when the cache needs none)."""
     need = _lib.load().ptb_attn_decode_workspace_bytes(nkv, group, seq)
+    return torch.empty(need, dtype=torch.uint8, device=device) if need else None
+
+
+def workspace_for(plan, device) -> torch.Tensor | None:
+    """The trailing workspace descriptor tensor a family's entry takes for this plan (None if none)."""
+    p, f, lib = plan.params, plan.family, _lib.load()
+    if f == "attention_decode":
+        return decode_workspace(p["nkv"], p["group"], p["seq"], device)
+    if f == "gemv":
+        need = lib.ptb_gemv_workspace_bytes(p["k"], p["n"])
+    elif f == "reduce":
+        need = lib.ptb_reduce_workspace_bytes(p["n"])
+    else:
+        return None
     return torch.empty(need, dtype=torch.uint8, device=device) if need else None

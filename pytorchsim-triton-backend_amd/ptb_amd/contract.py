@@ -178,14 +178,15 @@ def grid3(grid) -> tuple:
 
 
 def grid_bound(manifest_or_spec) -> tuple:
-    """The per-axis program bound a launch may not pass: kernel.json's ``grid_bound`` where the
-    manifest states one (None on an axis: unbounded there), else the spec's grid, which bounds the
-    compiled programs (driver/stage.py:95)."""
+    """The per-axis program bound a launch may not pass: kernel.json's ``grid_bound``, None on an
+    axis where it states none -- a null or absent grid_bound leaves every axis unbounded
+    (contract/kernel_object.py:98-100: ``bound or [None]*3``).  A spec launched without a manifest
+    is bounded by its grid, the extent its programs were compiled for (driver/stage.py:95)."""
     if isinstance(manifest_or_spec, KernelSpec):
         return grid3(manifest_or_spec.grid)
     bound = manifest_or_spec.get("grid_bound")
-    if bound is None:
-        return grid3(manifest_or_spec.get("grid", (1,)))
+    if not bound:
+        return (None, None, None)
     b = list(bound) + [1, 1, 1]
     return tuple(None if v is None else int(v) for v in b[:3])
 

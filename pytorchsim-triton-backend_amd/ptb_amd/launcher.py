@@ -12,9 +12,11 @@
   with nothing registered, a launch raises ``RuntimeError`` as the reference's driver does.
 
 Launch semantics follow the reference's kernel objects: a grid past the compiled bound (kernel.json's
-``grid_bound``, else the spec's grid) is refused (contract/kernel_object.py:93-107); a grid within it
-runs the programs it names -- the whole kernel at the spec's grid, a prefix of row blocks below it
-where the family's programs are row blocks -- through the family's spec-driven C entry
+``grid_bound``; a null bound, or a null axis, is unbounded; a spec launched without a manifest is
+bounded by its grid) is refused (contract/kernel_object.py:93-107); a grid within it runs the
+programs it names -- the whole kernel at its grid, a prefix of row blocks below it where the
+family's programs are row blocks, and programs past the kernel's extent, which the reference's
+masks make no-ops, not at all -- through the family's spec-driven C entry
 (``ptb_<family>_args``); runtime scalars are taken by name (contract/kernel_object.py:122-127) and a
 manifest that disagrees with the spec it is launched beside is refused (:264-286).  The whole grid
 is one HIP launch: the reference's per-program loop (codegen/wrapper.py:254-265) has no
@@ -74,6 +76,18 @@ def _with_scalars(spec: KernelSpec, scalars: dict | None) -> KernelSpec:
                       grid=spec.grid, extra=extra, graph_prefetch=spec.graph_prefetch)
 
 
+def _programs(spec: KernelSpec, bound) -> int:
+    """The kernel's programs along x for its current extents: ceil(xnumel / XBLOCK) for the
+    Inductor kernels that state both (the grid Inductor launches them with; a kernel object rebuilt
+    for other extents keeps its XBLOCK and takes the call's xnumel), else the bound, else the spec's
+    grid."""
+    ce, sv = spec.constexprs or {}, spec.scalar_values
+    xnumel, xblock = sv.get("xnumel", ce.get("xnumel")), ce.get("XBLOCK")
+    if xnumel is not None and xblock:
+        return max(1, -(-int(xnumel) // int(xblock)))
+    return bound[0] if bound[0] is not None else grid3(spec.grid)[0]
+
+
 def launch(spec_or_manifest, tensors, grid=None, source: str | None = None, scalars: dict | None = None,
            manifest: dict | None = None) -> kernels.Plan:
     """Run one reference kernel on the GPU (asynchronously, on the current stream).
@@ -97,21 +111,24 @@ def launch(spec_or_manifest, tensors, grid=None, source: str | None = None, scal
     spec = _with_scalars(spec, scalars)
     flat = {a.name: tensors[a.name].view(-1) for a in spec.args}
     plan = kernels.resolve(spec, source)
-    entry = capi.plan_args(plan, bound[0] if bound[0] is not None else grid3(spec.grid)[0])
+    programs = _programs(spec, bound)
+    # programs past the kernel's own extent (allowed where grid_bound leaves the axis unbounded or
+    # bounds it further) find no element inside the tensors: masked no-ops, so they are not run
+    g = (min(g[0], programs), min(g[1], grid3(spec.grid)[1]), min(g[2], grid3(spec.grid)[2]))
+    xblock = (spec.constexprs or {}).get("XBLOCK")
+    entry = capi.plan_args(plan, programs, int(xblock) if xblock else None)
     if entry is not None:
         fam, names, ints, floats = entry
         roles = {a.name: a.role for a in spec.args}
         ts = [flat[n] for n in names]
         rs = [roles[n] for n in names]
-        if plan.family == "attention_decode":
-            p = plan.params
-            ws = capi.decode_workspace(p["nkv"], p["group"], p["seq"], ts[0].device)
-            if ws is not None:
-                ts.append(ws)
-                rs.append("out")
+        ws = capi.workspace_for(plan, ts[0].device)
+        if ws is not None:
+            ts.append(ws)
+            rs.append("out")
         capi.call_args(fam, ts, rs, ints, floats, g)
         return plan
-    if g != grid3(spec.grid):
+    if g != (programs,) + grid3(spec.grid)[1:]:
         raise kernels.UnsupportedKernel(f"{spec.name}: family {plan.family} runs its whole grid "
                                         f"{grid3(spec.grid)} only, not {g}")
     kernels.run(plan, flat)

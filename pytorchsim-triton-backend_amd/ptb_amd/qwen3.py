@@ -145,6 +145,11 @@ class Qwen3Layer:
     __call__ = forward
 
 
+# kernels Qwen3Layer.forward issues for the reference's 14 launches (K01 + K03 as one GEMM, K02 + K05
+# + K06 + K07 in the attention kernel, K09 + K10 as one GEMM)
+PREFILL_KERNELS = 8
+
+
 class Qwen3DecodeLayer:
     """One decoder layer for a single new token over a KV cache, as the reference's decode bundle
     composes it (validation/pytorchsim/qwen3_8b_layer_decode_1x<S>_bf16/manifest.json, 8 launches):

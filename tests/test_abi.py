@@ -192,3 +192,45 @@ def test_args_entries_refuse_bad_calls(lib):
     # silu_mul: a partial grid has to end on a whole row
     gu, out = _desc(2 * 4 * 256), _desc(4 * 256, role=_lib.PTB_ROLE_OUT)
     assert _call(lib, "silu_mul", [gu, out], [4, 256, 8], [], (3, 1, 1)) == _lib.PTB_ERR_UNSUPPORTED
+
+
+def test_args_entries_refuse_bad_calls_more_families(lib):
+    f32, i64, outr = _lib.PTB_DTYPE_F32, _lib.PTB_DTYPE_I64, _lib.PTB_ROLE_OUT
+    # rmsnorm's fp32 column arm: only with fp32 tensors, c of cols elements
+    x32, w32 = _desc(16 * 64, dtype=f32), _desc(64, dtype=f32)
+    y32 = _desc(16 * 64, dtype=f32, role=outr)
+    assert _call(lib, "rmsnorm", [x32, w32, y32, _desc(63, dtype=f32, role=outr)], [16, 64, 1], [1e-5],
+                 (1, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "rmsnorm", [x32, w32, y32, _desc(64, dtype=f32)], [16, 64, 1], [1e-5],
+                 (1, 1, 1)) == _lib.PTB_ERR_SHAPE                       # c declared read-only
+    assert _call(lib, "rmsnorm", [_desc(16 * 64), _desc(64), _desc(16 * 64, role=outr),
+                                  _desc(64, dtype=f32, role=outr)], [16, 64, 1], [1e-5], (1, 1, 1)) == _lib.PTB_ERR_DTYPE
+    # sumsq: one fp32 output, bf16 inputs of n, the whole grid
+    one = _desc(1, dtype=f32, role=outr)
+    assert _call(lib, "sumsq", [_desc(64), one], [64, 1], [], (2, 1, 1)) == _lib.PTB_ERR_GRID
+    assert _call(lib, "sumsq", [_desc(64), _desc(63), one], [64, 1], [], (1, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "sumsq", [_desc(64), _desc(1, role=outr)], [64, 1], [], (1, 1, 1)) == _lib.PTB_ERR_DTYPE
+    # gemv: the layout its mode and extra count name, sizes against k and n
+    k, n = 64, 128
+    x, w, y = _desc(k), _desc(k * n), _desc(n, role=outr)
+    ss, g = _desc(1, dtype=f32), _desc(k)
+    assert _call(lib, "gemv", [x, w, y], [3, k, n, 0, 1], [], (1, 1, 1)) == _lib.PTB_ERR_UNSUPPORTED
+    assert _call(lib, "gemv", [x, w, y], [0, k, n, 1, 1], [], (1, 1, 1)) == _lib.PTB_ERR_UNSUPPORTED
+    assert _call(lib, "gemv", [x, _desc(k * n + 8), y], [0, k, n, 0, 1], [], (1, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "gemv", [x, ss, g, w, y], [1, k, n, 0, 1], [], (1, 1, 1)) == _lib.PTB_ERR_SHAPE   # no eps
+    assert _call(lib, "gemv", [x, g, g, w, y], [1, k, n, 0, 1], [1e-6], (1, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "gemv", [_desc(2 * k), w, _desc(n + 8), y], [2, k, n, 1, 1], [], (1, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "gemv", [x, w, y], [0, k, n, 0, 1], [], (2, 1, 1)) == _lib.PTB_ERR_GRID
+    assert _call(lib, "gemv", [x, w, y, _desc(8, role=_lib.PTB_ROLE_IN)], [0, k, n, 0, 1], [],
+                 (1, 1, 1)) == _lib.PTB_ERR_SHAPE                        # a read-only workspace
+    # reduce: a known op, one fp32 output
+    assert _call(lib, "reduce", [_desc(64), one], [64, 2, 1], [], (1, 1, 1)) == _lib.PTB_ERR_UNSUPPORTED
+    assert _call(lib, "reduce", [_desc(64), _desc(2, dtype=f32, role=outr)], [64, 0, 1], [], (1, 1, 1)) == \
+        _lib.PTB_ERR_SHAPE
+    assert _call(lib, "reduce", [_desc(64, dtype=i64), one], [64, 0, 1], [], (1, 1, 1)) == _lib.PTB_ERR_DTYPE
+    # add_scalar: one float, matching sizes; slice_add: the slice inside x
+    assert _call(lib, "add_scalar", [_desc(64), _desc(64, role=outr)], [64, 1], [], (1, 1, 1)) == _lib.PTB_ERR_SHAPE
+    assert _call(lib, "add_scalar", [_desc(64), _desc(64, role=outr)], [64, 2], [1.0], (3, 1, 1)) == _lib.PTB_ERR_GRID
+    assert _call(lib, "slice_add", [_desc(64), _desc(8, dtype=f32, role=outr)], [60, 8, 1], [1.0], (1, 1, 1)) == \
+        _lib.PTB_ERR_SHAPE
+    assert _call(lib, "slice_add", [_desc(64), _desc(8, role=outr)], [0, 8, 1], [1.0], (1, 1, 1)) == _lib.PTB_ERR_DTYPE

@@ -82,7 +82,9 @@ def test_flash_tokens_out_is_the_transposed_output(batch, hq, hkv, s):
 
 
 @pytest.mark.parametrize("batch,hq,hkv,s,causal,scale", [
-    (1, 32, 8, 2048, True, None),      # the prefill layer's shape (128-row workgroups)
+    (1, 32, 8, 2048, True, None),      # the prefill layer's shape: paired heavy/light 128-row tiles
+    (1, 56, 8, 896, True, None),       # paired tiles, odd tile count (the middle unit's second half idle)
+    (1, 32, 8, 1024, True, None),      # 128-row workgroups (4 waves), causal
     (1, 32, 8, 4096, True, None),      # 256-row workgroups
     (2, 8, 2, 256, False, -0.05),      # batches, no mask, a negative scale
 ])

@@ -451,3 +451,88 @@ def test_args_entry_attention_bundle_kernel():
     got = dev["o_ptr"].cpu().view(hq, s, d)[heads]
     from helpers import assert_close_rows
     assert_close_rows(got, want, 2e-2, 2e-2, "flash_attn_args")
+
+
+@pytest.mark.parametrize("workload,index", [
+    ("gemm_1x2048x128_bf16", 0),                  # gemv, plain (the M = 1 mm template)
+    ("qwen3_8b_layer_decode_1x1024_bf16", 0),     # sumsq of x
+    ("qwen3_8b_layer_decode_1x1024_bf16", 1),     # gemv, RMSNorm prologue
+    ("qwen3_8b_layer_decode_1x1024_bf16", 4),     # gemv, plain
+    ("qwen3_8b_layer_decode_1x1024_bf16", 5),     # sumsq of x + a
+    ("qwen3_8b_layer_decode_1x1024_bf16", 6),     # gemv, RMSNorm prologue over x + a
+    ("qwen3_8b_layer_decode_1x1024_bf16", 7),     # gemv, silu prologue + two residuals
+    ("layer_layer_decode_1x1024_bf16", 18),       # reduce (sum) over fp32
+    ("vector_max_1024x1024_bf16", 0),             # reduce (max) over bf16
+    ("vector_sum_1024x1024_bf16", 0),             # reduce (sum) over bf16
+    ("vector_add1_1024x1024_bf16", 0),            # add_scalar
+    ("vector_slice_4096x4096_bf16", 0),           # slice_add
+])
+def test_args_entry_more_families(workload, index):
+    """The sumsq, gemv, reduce, add_scalar and slice_add kernels through their ptb_<family>_args
+    entries, called directly with the spec's tensors (plus the entry's workspace descriptor) and
+    the whole grid, against the oracle."""
+    from ptb_amd import capi
+    man, spec, host, dev = _bundle(workload, index)
+    plan = kernels.resolve(spec)
+    fam, names, ints, floats = capi.plan_args(plan, spec.grid[0])
+    roles = {a.name: a.role for a in spec.args}
+    ts, rs = [dev[n] for n in names], [roles[n] for n in names]
+    ws = capi.workspace_for(plan, "cuda")
+    if ws is not None:
+        ts, rs = ts + [ws], rs + ["out"]
+    print(f"[case] {workload}/{man['dir']} {plan.family} -> ptb_{fam}_args", flush=True)
+    capi.call_args(fam, ts, rs, ints, floats, spec.grid)
+    torch.cuda.synchronize()
+    check_against_oracle(plan, host, {a.name: dev[a.name].cpu() for a in spec.outputs()})
+
+
+def test_args_entry_rmsnorm_column_arm():
+    """tests/cases/workloads/rmsnorm.py:44-57 (x, w, o, c all fp32, grid (1,)): o through the row
+    norm, c = rsqrt(mean over the rows of x^2 + eps) through the column arm, both within the
+    reference case's fp32 bar."""
+    from ptb_amd import capi
+    m, n, eps = 8, 64, 1e-5
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(m * n, generator=g)
+    w = torch.randn(n, generator=g)
+    o = torch.empty(m * n, device="cuda")
+    c = torch.empty(n, device="cuda")
+    capi.call_args("rmsnorm", [x.cuda(), w.cuda(), o, c], ["in", "in", "out", "out"], [m, n, 1], [eps], (1, 1, 1))
+    torch.cuda.synchronize()
+    xr = x.view(m, n).double()
+    want_o = (xr * torch.rsqrt(xr.pow(2).mean(-1, keepdim=True) + eps) * w.double()).float()
+    want_c = torch.rsqrt(xr.pow(2).mean(0) + eps).float()
+    assert_close(o.cpu().view(m, n), want_o, 1e-5, 1e-6, "rmsnorm_args o")
+    assert_close(c.cpu(), want_c, 1e-5, 1e-6, "rmsnorm_args c")
+    assert_close(c.cpu(), oracle.col_rms_f32(x.view(m, n), eps), 1e-5, 1e-6, "rmsnorm_args c vs oracle")
+
+
+def test_kernel_object_rebuilt_for_other_extents():
+    """A kernel object rebuilt for a launch's own extents, as the reference's _Launcher hands it over
+    (pytorchsim_triton_backend/driver.py:46-65, compiler.py:200-209: every argument's shape set to
+    the call's storage span, the stated scalars to the call's values): L2048/00's RMSNorm rebuilt for
+    1000 rows, with a null grid_bound, launched through the set_launcher hook over the grid
+    Inductor gives 1000 rows (ceil(1000 / XBLOCK)) and over a larger one (programs past the rows
+    are masked no-ops), both against the oracle."""
+    man = json.loads(json.dumps(MANIFESTS["qwen3_8b_layer_prefill_2048x2048_bf16"]["kernels"][0]))
+    rows, cols = 1000, 4096
+    for a in man["args"]:
+        a["shape"] = [cols] if a["name"] == "in_ptr1" else [rows * cols]
+    man["grid_bound"] = None
+    xblock = man["constexprs"]["XBLOCK"]
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(rows * cols, generator=g).to(torch.bfloat16)
+    w = (torch.randn(cols, generator=g) * 0.1 + 1).to(torch.bfloat16)
+    want = oracle.rmsnorm(x.view(rows, cols), w, 1e-6)
+    for grid in ((-(-rows // xblock), 1, 1), (8, 1, 1), (13, 1, 1)):
+        y = torch.empty(rows * cols, dtype=torch.bfloat16, device="cuda")
+        launcher.hip_launcher(b"", json.dumps(man), grid, [x.cuda(), w.cuda(), y, rows, cols])
+        torch.cuda.synchronize()
+        assert_close(y.cpu().view(rows, cols), want, 2e-2, 2e-2, f"rebuilt rmsnorm grid {grid}")
+    # a partial grid of the rebuilt kernel covers its leading XBLOCK-row blocks only
+    y = torch.empty(rows * cols, dtype=torch.bfloat16, device="cuda")
+    launcher.hip_launcher(b"", json.dumps(man), (2, 1, 1), [x.cuda(), w.cuda(), y, rows, cols])
+    torch.cuda.synchronize()
+    got = y.cpu().view(rows, cols)
+    assert_close(got[: 2 * xblock], want[: 2 * xblock], 2e-2, 2e-2, "rebuilt rmsnorm partial grid")
+    assert torch.isnan(got[2 * xblock:].float()).all()

@@ -113,9 +113,14 @@ def test_quant_rows_exact(rows, cols, seed):
     assert bits_equal(xq, wq)
 
 
-@pytest.mark.parametrize("k,n,seed", [(12288, 4096, 0), (128, 16, 1), (100, 70, 2)])
+@pytest.mark.parametrize("k,n,seed", [(12288, 4096, 0), (128, 16, 1), (100, 70, 2), (1000, 4100, 3), (36, 12, 4)])
 def test_quant_weight_exact(k, n, seed):
+    """The K-split absmax (K, N multiples of 4: ragged column blocks and K slices included) and the
+    any-shape path, bit for bit; a zero column takes scale 1, a column holding NaN scale 1 (torch's
+    amax propagates NaN and `amax > 0` fails), its NaN the e4m3 NaN."""
     w = randn((k, n), seed, dtype=torch.float32, std=0.02)
+    w[:, 3] = 0.0
+    w[k // 2, 5] = float("nan")
     wq, sc = ops.quant_weight_e4m3(w.to(DEV))
     owq, osc = oracle.quant_weight_e4m3(w)
     assert torch.equal(sc.cpu(), osc)

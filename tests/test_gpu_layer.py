@@ -1,6 +1,7 @@
 """The Qwen3-8B layer composed from the HIP kernels against the oracle's composition of the same
-14 launches (bf16 tolerance rtol = atol = 2e-2 on the O(1) output), and the full-size layer
-against a chain of the individually parity-tested GPU ops."""
+14 launches (bf16 tolerance rtol = 2e-2, absolute floor 2e-2 times the output's RMS), at T = 256
+and at the full T = 2048, and the full-size layer against a chain of the individually
+parity-tested GPU ops (bit for bit)."""
 import pytest
 import torch
 
@@ -28,6 +29,23 @@ def test_layer_matches_oracle_small():
     # bf16 bound 2e-2, with the absolute floor scaled to the output's RMS (y = h + mlp is not unit)
     rms = float(want.float().pow(2).mean().sqrt())
     assert_close(y, want, 2e-2, 2e-2 * max(1.0, rms), "qwen3 layer T=256")
+
+
+def test_layer_full_size_matches_oracle():
+    """T = S = 2048 at full size against the oracle's composition of the
+    manifest's 14 launches (validation/pytorchsim/qwen3_8b_layer_prefill_2048x2048_bf16/
+    manifest.json) on the same weights and input, under the T = 256 test's bound."""
+    cfg = qwen3.QWEN3_8B
+    t = 2048
+    w = qwen3.random_weights(cfg, seed=0)
+    x = randn((t, cfg.hidden), 3)
+    layer = qwen3.Qwen3Layer({k: v.to(DEV) for k, v in w.items()}, cfg)
+    y = layer(x.to(DEV)).cpu()
+    cos, sin = oracle.rope_tables(t, cfg.head_dim, cfg.rope_theta)
+    want = oracle.qwen3_layer(x, w, cos, sin, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.eps)
+    rms = float(want.float().pow(2).mean().sqrt())
+    assert torch.isfinite(y.float()).all()
+    assert_close(y, want, 2e-2, 2e-2 * max(1.0, rms), "qwen3 layer T=2048")
 
 
 def test_layer_full_size_is_its_launch_chain():

@@ -111,7 +111,8 @@ def test_topk_rows_nan_and_signed_zero(e, k, largest):
     """Rows holding NaNs (of either sign) and both zeros: both kernels (k <= 64 in registers, k > 64
     through the LDS ranks) take the numbers first in value order, equal values (-0 == +0 included) by
     lower position, then the NaNs by position -- the oracle's order -- and return the elements' own
-    values."""
+    values; a row of fewer than k elements other than the spent value ends in the reference's
+    (spent, 0) rounds."""
     rows = 6
     x = torch.randn(rows * e, generator=gen(e + k)).view(rows, e)
     x[0, 5] = float("nan")
@@ -121,6 +122,12 @@ def test_topk_rows_nan_and_signed_zero(e, k, largest):
     x[3, ::3] = float("nan")
     x[4, :] = 0.0
     x[4, 1::2] = -0.0
+    # mostly the spent value (-inf for the largest, +inf for the smallest), a few numbers and the
+    # opposite infinity: fewer than k elements to take, then the reference's (spent, 0) tail
+    spent = float("-inf") if largest else float("inf")
+    x[5, :] = spent
+    x[5, 3::17] = torch.randn(x[5, 3::17].numel(), generator=gen(k))
+    x[5, 5::37] = -spent
     x = x.reshape(-1)
     v, i = torch.empty(rows * k, device=DEV), torch.empty(rows * k, dtype=I64, device=DEV)
     moe.topk_rows(x.to(DEV), v, i, e, k, largest)

@@ -192,12 +192,22 @@ def test_device_registry_and_missing_inputs(tmp_path):
 
 
 def test_grid_bound_and_refusal():
-    """contract/kernel_object.py:93-107: the bound is kernel.json's grid_bound where stated, else the
-    spec's grid; an axis past it, below 1, or past the 21-bit program id is refused."""
+    """contract/kernel_object.py:93-107: the bound is kernel.json's grid_bound where stated (a null
+    or absent grid_bound, or a null axis, is unbounded: :98-100), a spec's own grid when no manifest
+    is launched; an axis past it, below 1, or past the 21-bit program id is refused."""
     spec = spec_of("qwen3_8b_layer_prefill_2048x2048_bf16", 0)
     assert contract.grid_bound(spec) == contract.grid3(spec.grid)
     man = spec.manifest()
     assert contract.grid_bound(dict(man, grid_bound=[16, None, 1])) == (16, None, 1)
+    assert contract.grid_bound(dict(man, grid_bound=None)) == (None, None, None)
+    assert contract.grid_bound({k: v for k, v in man.items() if k != "grid_bound"}) == (None, None, None)
+    # an unbounded kernel object takes a grid past its own: refused later for the CPU tensors only
+    cpu = {a.name: torch.zeros(a.numel, dtype=getattr(torch, a.dtype)) for a in spec.args}
+    with pytest.raises(ValueError) as e:
+        launcher.launch(dict(man, grid_bound=None), cpu, grid=(spec.grid[0] * 4, 3, 1))
+    assert not isinstance(e.value, launcher.GridMismatch)
+    with pytest.raises(launcher.GridMismatch):
+        launcher.launch(dict(man, grid_bound=list(spec.grid)), cpu, grid=(spec.grid[0] + 1, 1, 1))
     assert contract.refuse_grid_past_bound("k", (8,), (8, 1, 1)) == (8, 1, 1)
     assert contract.refuse_grid_past_bound("k", (3, 1, 1), (8, 1, 1)) == (3, 1, 1)
     for g in [(9, 1, 1), (8, 2, 1), (0, 1, 1), (8, 1, 1 << 22)]:

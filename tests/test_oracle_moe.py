@@ -104,6 +104,35 @@ def test_topk_against_library_and_ties():
     assert v.tolist() == [3.0, 3.0, 3.0, 2.0] and i.tolist() == [1, 2, 4, 3]    # ties: lowest position first
 
 
+def test_topk_spent_values_follow_the_reference_rounds():
+    """Rows holding the spent value itself (-inf for the largest, +inf for the smallest): worked
+    by hand through _topk_kernel_triton.py:17-25, a round that finds only spent values left
+    reports (spent, column 0) however often it runs, and a spent value is never reported by its
+    own column."""
+    inf = float("inf")
+    v, i = oracle.topk_rows(torch.tensor([1.0, -inf, 2.0, -inf]), 4, 4, True)
+    assert v.tolist() == [2.0, 1.0, -inf, -inf] and i.tolist() == [2, 0, 0, 0]
+    v, i = oracle.topk_rows(torch.tensor([1.0, inf, 2.0, inf]), 4, 4, False)
+    assert v.tolist() == [1.0, 2.0, inf, inf] and i.tolist() == [0, 2, 0, 0]
+    v, i = oracle.topk_rows(torch.tensor([-inf, 5.0, -inf]), 3, 3, True)
+    assert v.tolist() == [5.0, -inf, -inf] and i.tolist() == [1, 0, 0]
+    # the opposite infinity is an ordinary value
+    v, i = oracle.topk_rows(torch.tensor([inf, 1.0, inf]), 3, 3, True)
+    assert v.tolist() == [inf, inf, 1.0] and i.tolist() == [0, 2, 1]
+    # random rows with spent values sprinkled in: the rounds before the spent tail are torch.topk
+    # over the other values (stable: lower column first), the tail is (spent, 0)
+    x = torch.randn(40, 50, generator=gen(9))
+    x[torch.rand(40, 50, generator=gen(10)) < 0.5] = -inf
+    v, i = oracle.topk_rows(x.reshape(-1), 50, 30, True)
+    v, i = v.reshape(40, 30), i.reshape(40, 30)
+    for r in range(40):
+        live = torch.nonzero(x[r] > -inf).flatten()
+        n = min(30, live.numel())
+        order = live[torch.sort(x[r, live], descending=True, stable=True).indices][:n]
+        assert torch.equal(i[r, :n], order) and torch.equal(v[r, :n], x[r, order])
+        assert (i[r, n:] == 0).all() and (v[r, n:] == -inf).all()
+
+
 def test_gather_rows_floor_and_wrap():
     x = torch.arange(5 * 8, dtype=F32).to(BF16).reshape(5, 8)
     slot = torch.tensor([0, 7, 8, 39, -1, -8, -9, 40, -41], dtype=I64)
