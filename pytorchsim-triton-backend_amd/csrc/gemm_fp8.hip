@@ -32,7 +32,6 @@ namespace {
 
 constexpr int BM = 256, BK = 128;   // BK in bytes (= fp8 elements) per stage
 constexpr int kThreads = 256;
-constexpr int kGroupM = 8;
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
@@ -62,7 +61,8 @@ __device__ __forceinline__ int fp8_swz(int row) { return (row >> 1) & 7; }
 template <int BN>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_fp8_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ W,
-    const float* __restrict__ SW, uint16_t* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
+    const float* __restrict__ SW, uint16_t* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n,
+    int group_m) {
   using G = Cfg<BN>;
   constexpr int NS = G::NS;
   // stage kt+DIST refills the slot of stage kt+DIST-NS: with a three-stage ring that is stage kt-1,
@@ -75,9 +75,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int ntiles = tiles_m * tiles_n;
   int pid = blockIdx.x;
   if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
-  const int width = kGroupM * tiles_n;
-  const int first_m = (pid / width) * kGroupM;
-  const int gsize = min(tiles_m - first_m, kGroupM);
+  const int width = group_m * tiles_n;
+  const int first_m = (pid / width) * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
   const int tm = first_m + (pid % width) % gsize;
   const int tn = (pid % width) / gsize;
   const int m0 = tm * BM, n0 = tn * BN;
@@ -657,7 +657,16 @@ PTB_EXPORT int ptb_gemm_fp8_scaled(const void* aq, const float* sa, const void* 
   const uint8_t* a8 = static_cast<const uint8_t*>(aq);
   const uint8_t* w8 = static_cast<const uint8_t*>(wq_t);
   uint16_t* c16 = static_cast<uint16_t*>(c);
-  if (wide) gemm_fp8_kernel<256><<<grid, block, 0, s>>>(a8, sa, w8, sw, c16, int(m), int(n), int(k), int(tm), int(tn));
-  else gemm_fp8_kernel<128><<<grid, block, 0, s>>>(a8, sa, w8, sw, c16, int(m), int(n), int(k), int(tm), int(tn));
+  // Tile order: ids are spread so that each XCD takes a contiguous range of tiles, walked in groups
+  // of group_m tile-rows.  At 256x128 tiles a group of 4 rows makes an XCD's 32 resident tiles a 4x8
+  // block, whose A and W panels (4 x 256 rows + 8 x 128 rows of K) are the fewest bytes its L2 must
+  // fetch; 256x256 tiles keep groups of 8.
+  const int group_m = wide ? 8 : 4;
+  if (wide)
+    gemm_fp8_kernel<256><<<grid, block, 0, s>>>(a8, sa, w8, sw, c16, int(m), int(n), int(k), int(tm), int(tn),
+                                                group_m);
+  else
+    gemm_fp8_kernel<128><<<grid, block, 0, s>>>(a8, sa, w8, sw, c16, int(m), int(n), int(k), int(tm), int(tn),
+                                                group_m);
   return launch_status();
 }
