@@ -129,7 +129,10 @@ constexpr int kMaxDedupGroups = 1024;   // group tables up to this size have rep
 // bf16(silu(bf16(gate)) * bf16(up)), as a separate silu_mul would compute it from the bf16 GEMM.
 enum { kPlain = 0, kGrouped = 1, kSplit = 2, kSwiGLU = 3 };
 
-template <int WM, int WN, bool RESID, int MODE, int BKT = 32>
+// PERSIST (plain 256x256 tiles, no residual): one workgroup per CU walks the tiles
+// blockIdx.x, blockIdx.x + gridDim.x, ...; the next tile's first stage goes out halfway through the
+// current tile's epilogue, so its latency hides behind the stores (see the epilogue).
+template <int WM, int WN, bool RESID, int MODE, int BKT = 32, bool PERSIST = false>
 __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A_in, const uint16_t* __restrict__ B_in, const uint16_t* __restrict__ R,
     uint16_t* __restrict__ C_in, int M_in, int N, int K, int tiles_m, int tiles_n, Groups gp,
@@ -140,7 +143,20 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
   constexpr bool kHybrid = Sh::kHybrid;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[Sh::kSmemBytes];
 
-  // ---- tile selection
+  // ---- tile selection: tile id -> (first row, first column); ids are spread so that each XCD
+  //      takes a contiguous range of tiles, walked in groups of kGroupM tile-rows
+  const int ntiles = tiles_m * tiles_n;
+  auto tile_origin = [&](int id, int& tm0, int& tn0) __attribute__((always_inline)) {
+    int pid = id;
+    if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+    const int width = kGroupM * tiles_n;
+    const int first_m = (pid / width) * kGroupM;
+    const int gsize = min(tiles_m - first_m, kGroupM);
+    const int tm = first_m + (pid % width) % gsize;
+    const int tn = (pid % width) / gsize;
+    tm0 = tm * BM;
+    tn0 = MODE == kSwiGLU ? tn * (BN / 2) : tn * BN;   // SwiGLU: the output (and gate) column base
+  };
   const uint16_t* A = A_in;
   const uint16_t* B = B_in;
   uint16_t* C = C_in;
@@ -202,16 +218,7 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
       A = A_in + k0;
       B = B_in + int64_t(k0) * N;
     }
-    const int ntiles = tiles_m * tiles_n;
-    int pid = blockIdx.x;
-    if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
-    const int width = kGroupM * tiles_n;
-    const int first_m = (pid / width) * kGroupM;
-    const int gsize = min(tiles_m - first_m, kGroupM);
-    const int tm = first_m + (pid % width) % gsize;
-    const int tn = (pid % width) / gsize;
-    m0 = tm * BM;
-    n0 = MODE == kSwiGLU ? tn * (BN / 2) : tn * BN;   // SwiGLU: the output (and gate) column base
+    tile_origin(blockIdx.x, m0, n0);
   }
 
   const int tid = threadIdx.x;
@@ -221,8 +228,14 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
   // ---- loaders: A tile rows past M read as zero (num_records); B columns past N are read from
   //      the next row or as zero, and only feed columns of C that are never stored
   const int koff = MODE == kSplit ? int(blockIdx.y) * kchunk : 0;   // this split's first K column
-  const i32x4 rsrc_a = make_rsrc(A + int64_t(m0) * K, uint32_t(int64_t(min(BM, M - m0)) * K - koff) * 2u);
-  const i32x4 rsrc_b = make_rsrc(B + n0, uint32_t((int64_t(K - koff) * N - n0) * 2));
+  auto make_rsrc_a = [&](int tm0) __attribute__((always_inline)) {
+    return make_rsrc(A + int64_t(tm0) * K, uint32_t(int64_t(min(BM, M - tm0)) * K - koff) * 2u);
+  };
+  auto make_rsrc_b = [&](int tn0) __attribute__((always_inline)) {
+    return make_rsrc(B + tn0, uint32_t((int64_t(K - koff) * N - tn0) * 2));
+  };
+  i32x4 rsrc_a = make_rsrc_a(m0);
+  i32x4 rsrc_b = make_rsrc_b(n0);
   // A: instruction t of this wave covers rows kARowsPerKB*(kDmaA*wave + t) + lane/kChunks; lane ->
   //    slot lane%kChunks, holding chunk slot ^ a_swz(row)
   // B: instruction t covers the stage's 16-byte pieces 64*(kDmaB*wave + t) + lane in row-major order,
@@ -275,12 +288,6 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
   using I5 = std::integral_constant<int, 5>;
 
   f32x16 acc[WM][WN];
-#pragma unroll
-  for (int i = 0; i < WM; ++i)
-#pragma unroll
-    for (int j = 0; j < WN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   // ---- fragment addressing
   const int fr = lane & 31, h = lane >> 5;
@@ -350,15 +357,33 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
   }();
   const int nk = Kl / BK;
   const uint8_t* const smem_b = smem + NSA * kABytes;
+  static_assert(!PERSIST || (WM == 4 && WN == 4 && BKT == 64 && !RESID && MODE == kPlain),
+                "the persistent walk is for plain 256x256 tiles (the SwiGLU form has no registers to spare)");
+  // stores of the epilogue's second half, issued after the next tile's stage-0 DMAs
+  constexpr int kStoresAfter = (WM / 2) * 4 * (MODE == kSwiGLU ? WN / 2 : WN);
+  int tile_id = blockIdx.x;
+  bool pre0 = false;   // this tile's stage 0 went out during the previous tile's epilogue
+  for (;;) {
 #pragma unroll
-  for (int t = 0; t < D; ++t) dma_one(0, t, I0{}, I0{});
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  if (!pre0) {
+#pragma unroll
+    for (int t = 0; t < D; ++t) dma_one(0, t, I0{}, I0{});
+  }
 #pragma unroll
   for (int t = 0; t < D; ++t) dma_one(1, t, I1{}, std::integral_constant<int, 1 % NSB>{});
   if constexpr (DIST > 2) {
 #pragma unroll
     for (int t = 0; t < D; ++t) dma_one(2, t, I2{}, std::integral_constant<int, 2 % NSB>{});
   }
-  wait_vmcnt<(DIST - 1) * D>();     // stage 0 landed (this wave's part)
+  // stage 0 landed (this wave's part): after it went out, the stages above and, when it was
+  // prefetched, the epilogue's last kStoresAfter stores (memory operations count down in order)
+  if (pre0) wait_vmcnt<(DIST - 1) * D + (PERSIST ? kStoresAfter : 0)>();
+  else wait_vmcnt<(DIST - 1) * D>();
   __syncthreads();                  // ... and everyone's
   Slice sl[2];
 #pragma unroll
@@ -447,6 +472,21 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
   }
   wait_vmcnt<0>();
 
+  // the next tile of a persistent walk, and its stage-0 DMAs into A slot 0 and B slot 0 (free:
+  // every DMA has landed and, past the epilogue's barrier, no wave reads a stage)
+  const int next_id = tile_id + int(gridDim.x);
+  const bool has_next = PERSIST && next_id < ntiles;
+  int nm0 = 0, nn0 = 0;
+  if (has_next) tile_origin(next_id, nm0, nn0);
+  auto prefetch_next = [&]() __attribute__((always_inline)) {
+    if (has_next) {
+      rsrc_a = make_rsrc_a(nm0);
+      rsrc_b = make_rsrc_b(nn0);
+#pragma unroll
+      for (int t = 0; t < D; ++t) dma_one(0, t, I0{}, I0{});
+    }
+  };
+
   // ---- epilogue: accumulator (i, j, r) of lane holds C row m0 + wm*BM/2 + i*32 + lane%32,
   //      column n0 + wn*BN/2 + j*32 + 8*(r/4) + 4*(lane/32) + r%4: 4 consecutive columns per r/4
   if constexpr (MODE == kSplit) {
@@ -485,7 +525,13 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
     constexpr int RPI = 64 / LPR;         // rows per instruction (96 columns: 2 rows, 48 lanes)
     static_assert(32 % RPI == 0, "whole instructions per 32-row block");
     static_assert(4 * 32 * kPitch <= Sh::kSmemBytes, "the staging regions fit in the ring's LDS");
-    uint8_t* const stage = smem + wave * (32 * kPitch);
+    // a persistent walk keeps A slot 0 and B slot 0 free for the next tile's first stage: waves 0-2
+    // stage in A slots 1-2, wave 3 in B slot 1
+    static_assert(!PERSIST || (3 * 32 * kPitch <= 2 * kABytes && 32 * kPitch <= Sh::kBBytes),
+                  "the persistent staging regions fit beside the next tile's first stage");
+    uint8_t* const stage = !PERSIST ? smem + wave * (32 * kPitch)
+                           : wave < 3 ? smem + kABytes + wave * (32 * kPitch)
+                                      : smem + NSA * kABytes + Sh::kBBytes;
     const bool lane_on = lane < RPI * LPR;     // lanes past the last whole row store nothing
     const int rl = lane_on ? lane / LPR : 0, c4 = lane % LPR;
     const int gcol = col0 + 4 * c4;
@@ -525,6 +571,10 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
         __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, rsrc_c,
                                               voff[t], 0, 0);
       }
+      if constexpr (PERSIST) {
+        static_assert(32 / RPI * (WM - WM / 2) == kStoresAfter, "the prologue's wait counts these stores");
+        if (i == WM / 2 - 1) prefetch_next();   // half the stores out: the next tile's stage 0
+      }
     }
   };
   if constexpr (MODE == kSwiGLU) {
@@ -545,6 +595,13 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
       return f32x4v{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
     }, C, N, N, n0 + wn * (BN / 2));
   }
+  if (!has_next) break;
+  __syncthreads();   // every wave has read its staged rows back: the next stages may land there
+  tile_id = next_id;
+  m0 = nm0;
+  n0 = nn0;
+  pre0 = true;
+  }   // tile walk
 }
 
 // 256x256 and 256x128 tiles take 64-deep stages (whole-line A requests), 128x128 tiles 32-deep
@@ -554,6 +611,8 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
 template <int WM, int WN>
 constexpr int kBKOf = WM * WN >= 8 ? 64 : 32;
 
+int cu_count();
+
 template <int WM, int WN>
 int launch_gemm(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n, int64_t k,
                 hipStream_t s) {
@@ -562,6 +621,16 @@ int launch_gemm(const void* a, const void* b, const void* residual, void* c, int
   if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
   const dim3 grid(unsigned(tm * tn)), block(kThreads);
   const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
+  if constexpr (WM == 4 && WN == 4) {
+    // two or more rounds of 256x256 tiles: one workgroup per CU walks its tiles
+    const int64_t cus = cu_count();
+    if (!residual && tm * tn >= 2 * cus) {
+      gemm_bf16_kernel<4, 4, false, kPlain, 64, true><<<dim3(unsigned(cus)), block, 0, s>>>(
+          static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, static_cast<uint16_t*>(c),
+          int(m), int(n), int(k), int(tm), int(tn), none, nullptr, 0);
+      return launch_status();
+    }
+  }
   if (residual)
     gemm_bf16_kernel<WM, WN, true, kPlain, kBKOf<WM, WN>><<<grid, block, 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), static_cast<const uint16_t*>(residual),

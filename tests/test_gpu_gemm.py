@@ -85,6 +85,30 @@ def test_gemm_ragged_residual_stays_inside_c(m, k, n):
     assert_close(c.cpu()[rows], oracle.gemm(a[rows], b, r[rows]), RTOL, ATOL, f"gemm+R {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("m,k,n", [
+    (4096, 4096, 12288),   # three rounds of 256x256 tiles
+    (4300, 256, 8248),     # 561 tiles, ragged in M and N: some workgroups walk three tiles, most two
+])
+def test_gemm_persistent_walk_is_the_tile_by_tile_product(m, k, n):
+    """Two or more rounds of 256x256 tiles run as one workgroup per CU walking its tiles, the next
+    tile's first stage loading during the current tile's epilogue.  Every tile keeps its MFMA order
+    over K, so each 256-row band equals the product of that band of A alone (a one-round shape,
+    other tiles) bit for bit; the sampled rows against the oracle, and nothing written past C."""
+    a = randn((m, k), 8, std=1.0 / 64)
+    b = randn((k, n), 9, std=1.0 / 64)
+    guard = torch.full((m * n + 8192,), float("nan"), dtype=torch.bfloat16, device=DEV)
+    c = guard[: m * n].view(m, n)
+    ad, bd = a.to(DEV), b.to(DEV)
+    ops.gemm(ad, bd, out=c)
+    assert bool(guard[m * n:].isnan().all()), "the GEMM wrote past C"
+    for r0 in (0, 256 * ((m - 1) // 256)):
+        band = ops.gemm(ad[r0:r0 + 256].contiguous(), bd, split_k=False)
+        assert bits_equal(c[r0:r0 + 256], band), f"rows {r0}.. differ from the band's own product"
+    rows = sample_rows(m, 8)
+    want = oracle.gemm(a[rows], b)
+    assert_close(c.cpu()[rows], want, RTOL, ATOL * rms(want), f"gemm {m}x{k}x{n}")
+
+
 def test_gemm_bundle_inputs_exact_products():
     """bf16 operands from the bundle's make_inputs draw (randn): small enough that the fp32
     accumulation is exact for small K -> bit-exact output (tests/baselines/tpuv6e.txt:162 records
