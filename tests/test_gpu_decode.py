@@ -177,3 +177,33 @@ def test_qwen3_decode_layer_matches_oracle():
     want = oracle.qwen3_decode_layer(x, wts, kc, vc, cos, sin)
     rms = float(want.float().pow(2).mean().sqrt())
     assert_close(y, want, RTOL, 2e-2 * max(1.0, rms), "qwen3 decode layer")
+
+
+@pytest.mark.parametrize("s", [256, 4096])
+def test_decode_layer_graph_replays_match_eager(s):
+    """The decode layer (GEMVs with their workspaces, decode attention with its q-norm + RoPE
+    prologue and merge pass) captured as a HIP graph: each of several replays, with eager work and
+    synchronisations between them, reproduces the eager forward bit for bit (the bench times the
+    decode lines this way; no step of the layer records a memset node)."""
+    from ptb_amd import qwen3
+
+    layer = qwen3.Qwen3DecodeLayer({k: v.to(DEV) for k, v in qwen3.random_weights(seed=3).items()})
+    x = randn((4096,), 30).to(DEV)
+    kc = randn((8, s, 128), 31).to(DEV)
+    vc = randn((8, s, 128), 32).to(DEV)
+    cos_t, sin_t = qwen3.rope_tables(s + 1, 128, 1.0e6, DEV)
+    cos, sin = cos_t[s].contiguous(), sin_t[s].contiguous()
+    y = torch.empty(4096, dtype=torch.bfloat16, device=DEV)
+    want = layer.forward(x, kc, vc, cos, sin).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side), torch.cuda.graph(g, stream=side):
+        layer.forward(x, kc, vc, cos, sin, out=y)
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(3):
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert bits_equal(y, want), f"replay {i}"
+        assert bits_equal(layer.forward(x, kc, vc, cos, sin), want)   # eager work between replays
