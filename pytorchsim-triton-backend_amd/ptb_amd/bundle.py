@@ -44,6 +44,7 @@ class Workload:
     kernels: list = field(default_factory=list)   # BundleKernel, in first-launch order
     order: list = field(default_factory=list)     # kernel dirs in launch order (repeats kept)
     path: str = ""
+    ci: bool = True                               # under its suite's --ci cap (manifests files record it)
 
 
 def _literal(node):
@@ -177,7 +178,8 @@ def workloads_from_manifests(data: dict, suite: str | None = None, where=None) -
             continue
         if callable(where) and not where(dict(w["keys"], workload=name, suite=w["suite"])):
             continue
-        wl = Workload(name=name, suite=w["suite"], keys=dict(w["keys"]), order=list(w["order"]))
+        wl = Workload(name=name, suite=w["suite"], keys=dict(w["keys"]), order=list(w["order"]),
+                      ci=bool(w.get("ci", 1)))
         for man in w["kernels"]:
             wl.kernels.append(BundleKernel(dir=man["dir"], spec=spec_from_manifest(man), source="",
                                            launches=int(man.get("launches", 1))))

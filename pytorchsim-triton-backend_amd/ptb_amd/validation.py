@@ -28,6 +28,77 @@ from . import bundle, contract, kernels
 MI355X = {"name": "MI355X (gfx950)", "peak_bf16_tflops": 2500.0, "peak_fp8_tflops": 5000.0, "hbm_gbs": 8000.0}
 SUITES = tuple(bundle.SUITE_KEYS)
 
+#: --ci caps (reference: validation/layer/simulate_shapes.py:13 CI_TOKENS, :26 CI_OPS; validation/gemm/
+#: simulate_shapes.py:58-59 the table of Qwen3-30B-A3B GEMM shapes whose M the cap limits, and CI_M)
+CI_TOKENS = 4096
+CI_OPS = ("dispatch", "combine", "router_post", "gmm_gate_up", "gmm_down")
+CI_M = 4096
+CAPPED_TABLE = os.path.join("gemm", "tpu_v6e_qwen3moe_torchxla.csv")
+
+
+def read_capped(path) -> frozenset:
+    """The (M, K, N) shapes a measured GEMM table holds: the gemm suite's --ci caps these by M."""
+    import csv
+
+    with open(path, newline="") as fh:
+        return frozenset(tuple(int(r[k]) for k in ("M", "K", "N")) for r in csv.DictReader(fh))
+
+
+def _tokens(keys) -> int:
+    """A layer workload's tokens: a layer's context S, an op's T (validation/layer/simulate_shapes.py:16-18)."""
+    return int(keys["S"]) if keys["section"] == "layer" else int(keys["T"])
+
+
+def under_ci_cap(suite, keys, capped=frozenset()) -> bool:
+    """Whether the suite's --ci times a workload with these keys.  layer: a layer or one of CI_OPS of at most
+    CI_TOKENS tokens (validation/layer/simulate_shapes.py:30-32); qwen3_8b: a layer of at most CI_TOKENS tokens
+    (validation/qwen3_8b/simulate_shapes.py:27-30); gemm: a shape of the `capped` table at M <= CI_M, any other
+    shape always (validation/gemm/simulate_shapes.py:408-411); vector and attention have no cap."""
+    if suite == "layer":
+        return (keys["section"] == "layer" or keys["name"] in CI_OPS) and _tokens(keys) <= CI_TOKENS
+    if suite == "qwen3_8b":
+        return keys["section"] == "layer" and _tokens(keys) <= CI_TOKENS
+    if suite == "gemm":
+        shape = tuple(int(keys[k]) for k in ("M", "K", "N"))
+        return shape not in capped or shape[0] <= CI_M
+    return True
+
+
+def cost(suite, keys) -> int:
+    """What a workload is ranked by when shards are planned: attention the scores it computes
+    (validation/attention/simulate_shapes.py:13-17), the layer suites the query-key pairs of a layer or an op's
+    tokens (validation/layer/simulate_shapes.py:21-23), any other suite the product of its numeric keys
+    (validation/gemm/simulate_shapes.py:171-179)."""
+    if suite == "attention":
+        hq, sq = int(keys["Hq"]), int(keys["S"])
+        return hq * sq * (sq + 1) // 2 if keys["kind"] == "prefill" else hq * sq
+    if suite in ("layer", "qwen3_8b"):
+        return int(keys["T"]) * int(keys["S"]) if keys["section"] == "layer" else int(keys["T"])
+    n = 1
+    for v in keys.values():
+        n *= int(v) if str(v).isdigit() else 1
+    return n
+
+
+def shard(ws, k, n, suite) -> list:
+    """Part `k` (0-based) of `n`, by longest processing time: the workloads, costliest first (ties in key order),
+    each go to the part with the least cost so far (ties to the lower part), so the parts are disjoint, cover the
+    set and are fixed (validation/gemm/simulate_shapes.py:182-196)."""
+    if not 0 <= k < n:
+        raise ValueError(f"--shard {k}/{n}: K must be in 0..N-1")
+    names = bundle.SUITE_KEYS[suite]
+
+    def order(w):
+        return (-cost(suite, w.keys), tuple((0, int(w.keys[c])) if str(w.keys[c]).isdigit() else (1, w.keys[c])
+                                            for c in names))
+    load, mine = [0] * n, []
+    for w in sorted(ws, key=order):
+        i = min(range(n), key=lambda j: (load[j], j))
+        load[i] += cost(suite, w.keys)
+        if i == k:
+            mine.append(w)
+    return mine
+
 
 def time_kernel(bk, reps: int = 20, warmup: int = 3, seed: int = 0, settle: float = 0.02, graph: bool = True,
                 recorded: dict | None = None) -> dict:
@@ -137,13 +208,24 @@ def write_results(path, suite, done, total, part=None) -> None:
 
 
 def merge(paths, out) -> int:
-    parts = [json.load(open(p)) for p in paths]
+    """The results.json of shard runs as one run's at `out`: the parts must come from one suite and machine and
+    must not overlap; expected is the whole set's.  1 if a workload is missing (validation/gemm/
+    simulate_shapes.py:322-352)."""
+    parts = []
+    for p in paths:
+        with open(p) as fh:
+            parts.append(json.load(fh))
     suite = parts[0]["suite"]
     if any(p["suite"] != suite or p["machine"] != parts[0]["machine"] for p in parts):
         raise ValueError("shards of different suites or machines")
+    names = [s["kernel"] for p in parts for s in p["shapes"]]
+    if len(names) != len(set(names)):
+        raise ValueError("shards overlap: " + ", ".join(sorted({k for k in names if names.count(k) > 1})))
     shapes = [s for p in parts for s in p["shapes"]]
-    write_results(out, suite, shapes, parts[0]["expected"])
-    return 0 if len(shapes) == parts[0]["expected"] else 1
+    plan = parts[0].get("shard")
+    expected = plan["total"] if isinstance(plan, dict) else parts[0]["expected"]
+    write_results(out, suite, shapes, expected)
+    return 0 if len(shapes) == expected else 1
 
 
 def parse_where(items):
@@ -162,7 +244,8 @@ def main(argv=None) -> int:
     ap.add_argument("--out", default="results.json")
     ap.add_argument("--where", action="append", help="key=value filter on the workload's keys (repeatable)")
     ap.add_argument("--only", action="append", help="workload name (repeatable)")
-    ap.add_argument("--shard", help="K/N: run the K-th of N interleaved parts")
+    ap.add_argument("--ci", action="store_true", help="only the workloads under the suite's CI cap, where it has one")
+    ap.add_argument("--shard", help="K/N: time part K (0-based) of N disjoint parts of the set")
     ap.add_argument("--merge", nargs="+", help="join shard results.json files into --out")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -179,16 +262,30 @@ def main(argv=None) -> int:
     _lib.load()
     if args.bundle:
         ws = bundle.load_bundle(args.bundle, args.suite, parse_where(args.where) or None)
+        table = os.path.join(os.path.dirname(os.path.abspath(args.bundle)), CAPPED_TABLE)
+        capped = read_capped(table) if args.suite == "gemm" and os.path.isfile(table) else frozenset()
+        if args.ci and args.suite == "gemm" and not capped:
+            raise SystemExit(f"--ci: the gemm suite's cap reads {table}, which is not there")
+        for w in ws:
+            w.ci = under_ci_cap(w.suite, w.keys, capped)
     else:
         ws = bundle.workloads_from_manifests(bundle.read_manifests(args.manifests), args.suite,
                                              parse_where(args.where) or None)
     if args.only:
         ws = [w for w in ws if w.name in set(args.only)]
+    if args.ci:
+        skipped = [w.name for w in ws if not w.ci]
+        ws = [w for w in ws if w.ci]
+        print(f"--ci: {len(ws)} workloads, {len(skipped)} over the CI cap left out: {' '.join(skipped)}", flush=True)
     part = None
     if args.shard:
         k, n = (int(x) for x in args.shard.split("/"))
-        ws = ws[k - 1::n]
-        part = args.shard
+        total = len(ws)
+        try:
+            ws = shard(ws, k, n, args.suite)
+        except ValueError as e:
+            raise SystemExit(str(e)) from None
+        part = {"index": k, "of": n, "total": total}
     done = []
     write_results(args.out, args.suite, done, len(ws), part)
     for w in ws:

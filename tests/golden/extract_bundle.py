@@ -6,7 +6,9 @@ bundle's manifest.json and *_spec.py files with ptb_amd.bundle (ast, nothing imp
 and stores per kernel only data: name, args (name, role, dtype, flat shape), grid, scalars,
 constexprs, the launch count, the family that serves it (null when none does), the index facts
 the HIP families otherwise read from the Triton source (``extra.hints``) and the arguments the
-spec takes from its recorded inputs (``extra.recorded``).  The GPU tests and the validation runner
+spec takes from its recorded inputs (``extra.recorded``); per workload, ``ci`` says whether its
+suite's ``--ci`` times it (the gemm suite's cap reads the reference's measured Qwen3-30B-A3B
+GEMM table, validation/gemm/tpu_v6e_qwen3moe_torchxla.csv, which is not at hand elsewhere).  The GPU tests and the validation runner
 (``--manifests``) read these manifests where the bundle itself is absent.
 
 The recorded inputs themselves (the MoE kernels' index tables, ``*_inputs.pt`` beside their specs,
@@ -25,11 +27,12 @@ import torch
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parents[1] / "pytorchsim-triton-backend_amd"))
 
-from ptb_amd import bundle, kernels  # noqa: E402
+from ptb_amd import bundle, kernels, validation  # noqa: E402
 
 
 def main(ref="/root/reference"):
     root = os.path.join(ref, "validation", "pytorchsim")
+    capped = validation.read_capped(os.path.join(ref, "validation", validation.CAPPED_TABLE))
     out = {}
     recorded = {}
     for name in sorted(os.listdir(root)):
@@ -52,7 +55,8 @@ def main(ref="/root/reference"):
             man["dir"] = bk.dir
             man["family"] = plan.family if plan else None
             ks.append(man)
-        out[name] = {"suite": w.suite, "keys": w.keys, "order": w.order, "kernels": ks}
+        out[name] = {"suite": w.suite, "keys": w.keys, "order": w.order, "kernels": ks,
+                     "ci": int(validation.under_ci_cap(w.suite, w.keys, capped))}
     path = HERE / "bundle_manifests.json.gz"
     # mtime 0 keeps the file byte-identical across runs
     with gzip.GzipFile(path, "wb", mtime=0) as fh:

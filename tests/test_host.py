@@ -251,3 +251,81 @@ def test_hip_launcher_maps_scalars_by_name():
     s2 = launcher._with_scalars(spec, {"xnumel": 1024, "r0_numel": 4096})
     assert s2.scalar_values == {"xnumel": 1024, "r0_numel": 4096}
     assert spec.scalar_values["xnumel"] == 2048      # the spec itself is unchanged
+
+
+def test_ci_caps_follow_the_reference_suites():
+    """--ci: the layer suite times its layers and MoE ops up to 4096 tokens and none of the dense ops
+    (validation/layer/test_cap.py:16-24); qwen3_8b only its layers; gemm caps the measured MoE shapes
+    at M <= 4096; vector and attention have no cap."""
+    from ptb_amd import validation as v
+
+    assert v.under_ci_cap("layer", {"section": "layer", "name": "prefill", "T": 4096, "S": 4096})
+    assert v.under_ci_cap("layer", {"section": "op", "name": "combine", "T": 4096, "S": 0})
+    assert not v.under_ci_cap("layer", {"section": "op", "name": "combine", "T": 8192, "S": 0})
+    assert not v.under_ci_cap("layer", {"section": "op", "name": "rmsnorm", "T": 128, "S": 0})
+    assert not v.under_ci_cap("layer", {"section": "layer", "name": "prefill", "T": 8192, "S": 8192})
+    assert not v.under_ci_cap("qwen3_8b", {"section": "op", "name": "rmsnorm", "T": 1, "S": 0})
+    assert v.under_ci_cap("qwen3_8b", {"section": "layer", "name": "decode", "T": 1, "S": 4096})
+    capped = frozenset({(8192, 2048, 128), (4096, 2048, 128)})
+    assert not v.under_ci_cap("gemm", {"M": 8192, "K": 2048, "N": 128}, capped)
+    assert v.under_ci_cap("gemm", {"M": 4096, "K": 2048, "N": 128}, capped)
+    assert v.under_ci_cap("gemm", {"M": 8192, "K": 4096, "N": 4096}, capped)
+    assert v.under_ci_cap("vector", {"program": "sum", "R": 16384, "C": 8192})
+    # the manifests file records the flag: the layer suite's 12 layers and 5 MoE ops x 7 token counts,
+    # and the four 8192-row GEMMs the measured MoE table holds
+    ws = bundle.workloads_from_manifests(MANIFESTS)
+    by = {}
+    for w in ws:
+        by.setdefault(w.suite, []).append(w)
+    assert sum(w.ci for w in by["layer"]) == 12 + 5 * 7
+    assert {w.name for w in by["layer"] if w.ci and w.keys["section"] == "op"} == {
+        f"layer_op_{o}_{t}x0_bf16" for o in v.CI_OPS for t in (1, 128, 256, 512, 1024, 2048, 4096)}
+    assert sorted(w.name for w in by["gemm"] if not w.ci) == [
+        "gemm_8192x2048x128_bf16", "gemm_8192x2048x4096_bf16", "gemm_8192x2048x512_bf16",
+        "gemm_8192x4096x2048_bf16"]
+    assert all(w.ci for s in ("vector", "attention", "qwen3_8b") for w in by[s])
+    for w in ws:
+        assert w.ci == v.under_ci_cap(w.suite, w.keys, frozenset(
+            (int(x.keys["M"]), int(x.keys["K"]), int(x.keys["N"])) for x in by["gemm"] if not x.ci)), w.name
+
+
+def test_shards_are_disjoint_cover_the_set_and_balance_by_cost():
+    """--shard K/N (0-based): longest processing time over each suite's cost (validation/gemm/
+    simulate_shapes.py:182-196); --merge refuses overlapping parts and expects the whole set."""
+    from ptb_amd import validation as v
+
+    for suite, n in (("gemm", 4), ("attention", 3), ("layer", 5), ("vector", 7)):
+        ws = bundle.workloads_from_manifests(MANIFESTS, suite)
+        parts = [v.shard(ws, k, n, suite) for k in range(n)]
+        names = [w.name for p in parts for w in p]
+        assert sorted(names) == sorted(w.name for w in ws) and len(set(names)) == len(names)
+        loads = [sum(v.cost(suite, w.keys) for w in p) for p in parts]
+        # LPT: no part exceeds another by more than the costliest single workload
+        assert max(loads) - min(loads) <= max(v.cost(suite, w.keys) for w in ws)
+        assert [w.name for w in v.shard(ws, 1, n, suite)] == [w.name for w in parts[1]]
+    ws = bundle.workloads_from_manifests(MANIFESTS, "attention")
+    big = max(ws, key=lambda w: v.cost("attention", w.keys))
+    assert big.keys["kind"] == "prefill" and int(big.keys["S"]) == 8192 and int(big.keys["Hq"]) == 64
+    assert v.shard(ws, 0, 3, "attention")[0].name == big.name
+    with pytest.raises(ValueError):
+        v.shard(ws, 3, 3, "attention")
+    with pytest.raises(ValueError):
+        v.shard(ws, -1, 3, "attention")
+
+
+def test_merge_expects_the_whole_set(tmp_path):
+    from ptb_amd import validation as v
+
+    def part(k, names):
+        p = tmp_path / f"r{k}.json"
+        p.write_text(json.dumps({"machine": v.MI355X, "suite": "gemm", "expected": len(names),
+                                 "shard": {"index": k, "of": 2, "total": 3},
+                                 "shapes": [{"M": 1, "K": 2, "N": i, "kernel": n, "rc": 0} for i, n in
+                                            enumerate(names)]}))
+        return str(p)
+    out = str(tmp_path / "all.json")
+    assert v.merge([part(0, ["a", "b"]), part(1, ["c"])], out) == 0
+    assert json.loads(Path(out).read_text())["expected"] == 3
+    assert v.merge([part(0, ["a"]), part(1, ["c"])], out) == 1
+    with pytest.raises(ValueError, match="overlap"):
+        v.merge([part(0, ["a", "b"]), part(1, ["b"])], out)
