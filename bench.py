@@ -591,8 +591,8 @@ def main(argv=None):
         pmc_driver(args.pmc_driver)
         return 0
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
-              "multi-GPU sharding of the path is described in DESIGN.md, not benchmarked.", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); sharding the "
+              "path over several GPUs is a design, not a benchmarked configuration.", file=sys.stderr)
         return 2
 
     import torch
