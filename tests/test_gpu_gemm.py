@@ -266,6 +266,45 @@ def test_gemm_swiglu_odd_step_count():
     assert bits_equal(fused, pair)
 
 
+def test_gemm_swiglu_every_bf16_gate():
+    """The SwiGLU epilogue's quotient g / (1 + e^-g) against silu_mul's IEEE division for every bf16
+    gate value.  A = I (256 x 256) makes the gate accumulators B's gate columns, which hold the 65280
+    finite bf16 bit patterns (subnormals included) in columns 0-254 and the 256 infinities and NaNs
+    in column 255 (whose products with A's zeros make that column NaN); -0 becomes +0 in an
+    accumulator.  A second call, A = 2^-8 I, puts +inf and -inf alone in row 0 and reaches a -0 gate
+    (a subnormal product that rounds to -0 in bf16).  Bit-equal to GEMM + silu_mul, NaN for NaN."""
+    n = 256
+
+    def check(ad, bd):
+        fused = ops.gemm_swiglu(ad, bd).cpu()
+        g = ops.gemm(ad, bd, split_k=False)
+        pair = ops.silu_mul(g).cpu()
+        nan_f, nan_p = torch.isnan(fused.float()), torch.isnan(pair.float())
+        assert torch.equal(nan_f, nan_p)
+        assert bits_equal(fused[~nan_f], pair[~nan_p])
+        return g.cpu()[:, :n], nan_f
+
+    pats = torch.arange(65536, dtype=torch.int32)
+    special = ((pats >> 7) & 0xFF) == 0xFF
+    # gate[k, j] = pattern j*256 + k of the finite ones, then the specials: column 255
+    vals = torch.cat([pats[~special], pats[special]]).to(torch.int16)
+    gate = vals.view(torch.bfloat16).reshape(n, n).t().contiguous()
+    b = torch.cat([gate, randn((n, n), 45, std=1.0)], dim=1)          # B [K = 256, 2I = 512]: gate | up
+    a = torch.eye(n, dtype=torch.bfloat16)
+    g, nan_f = check(a.to(DEV), b.to(DEV))
+    want = b[:, :255].clone()
+    want[want.view(torch.int16) == -32768] = 0.0                          # -0 accumulates to +0
+    assert bits_equal(g[:, :255], want), "the gate accumulators are B's finite gate values"
+    assert nan_f[:, 255].all() and not nan_f[:, :255].any()
+    b2 = torch.ones((n, 2 * n), dtype=torch.bfloat16)
+    b2[0, 0], b2[0, 1] = float("inf"), float("-inf")
+    b2[0, 2], b2[0, 3] = -(2.0 ** -133), 2.0 ** -133                      # products +-2^-141: bf16 -0, +0
+    g2, _ = check((a * 2.0 ** -8).to(DEV), b2.to(DEV))
+    assert g2[0, 0].item() == float("inf") and g2[0, 1].item() == float("-inf")
+    # -0 is reached unless the matrix cores flush the subnormal product, in which case no gate is -0
+    assert int(g2[0:1, 2].view(torch.int16)) in (-32768, 0) and int(g2[0:1, 3].view(torch.int16)) == 0
+
+
 def test_gemm_swiglu_refusals():
     a = torch.zeros((64, 128), dtype=torch.bfloat16, device=DEV)
     b = torch.zeros((128, 2 * 192), dtype=torch.bfloat16, device=DEV)     # inter = 192: not a multiple of 128
