@@ -522,8 +522,10 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
     return;
   }
   // Plain, grouped and SwiGLU tiles leave through the LDS, which is free now (every DMA has landed
-  // and, past the barrier, no wave reads a stage): a wave writes one 32-row block of its fp32
-  // results (WJ 32-column blocks; value(i, jj, g) gives the 4 columns 8g + 4*(lane/32) .. +3 of
+  // and, past the barrier, no wave reads a stage): a wave writes one 32-row block of its results
+  // (bf16; fp32 where a residual is still to be added, and in the persistent walk) (WJ 32-column
+  // blocks; value(i, jj, g) gives
+  // the 4 fp32 columns 8g + 4*(lane/32) .. +3 of
   // block jj for row lane%32) into a private, padded region and reads it back 4 columns a lane, so
   // each store writes whole rows of its block (in the accumulator layout one store instruction
   // writes 16 bytes into each of 32 rows, which took 12% of a 256x256 tile's time) and the
@@ -534,7 +536,13 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
   auto store_staged = [&](auto wj, auto value, uint16_t* out, int ldc, int cols, int col0) __attribute__((always_inline)) {
     constexpr int WJ = decltype(wj)::value;
     constexpr int WC = WJ * 32;           // columns of a wave's block
-    constexpr int kPitch = WC * 4 + 16;   // bytes per staged row: rows start 4 banks apart
+    // without a residual to add, each value is rounded to bf16 before it is staged (the rounding
+    // the store would make anyway), halving the staged bytes; with one, the fp32 sum needs fp32.
+    // The persistent walk keeps fp32 staging: its bf16 form needs registers it does not have
+    // (632 bytes of spills)
+    constexpr bool kF32Stage = RESID || PERSIST;
+    constexpr int kEl = kF32Stage ? 4 : 2;   // bytes per staged value
+    constexpr int kPitch = WC * kEl + 16; // bytes per staged row: rows start 4 banks apart
     constexpr int LPR = WC / 4;           // lanes per row, 4 columns each
     constexpr int RPI = 64 / LPR;         // rows per instruction (96 columns: 2 rows, 48 lanes)
     static_assert(32 % RPI == 0, "whole instructions per 32-row block");
@@ -571,19 +579,30 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
 #pragma unroll
       for (int jj = 0; jj < WJ; ++jj)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<f32x4v*>(stage + fr * kPitch + (jj * 32 + 8 * g + 4 * h) * 4) = value(i, jj, g);
+        for (int g = 0; g < 4; ++g) {
+          const f32x4v v = value(i, jj, g);
+          if constexpr (kF32Stage)
+            *reinterpret_cast<f32x4v*>(stage + fr * kPitch + (jj * 32 + 8 * g + 4 * h) * 4) = v;
+          else
+            *reinterpret_cast<u32x2*>(stage + fr * kPitch + (jj * 32 + 8 * g + 4 * h) * 2) =
+                u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        }
 #pragma unroll
       for (int t = 0; t < 32 / RPI; ++t) {
-        f32x4v v = *reinterpret_cast<const f32x4v*>(stage + (t * RPI + rl) * kPitch + c4 * 16);
-        if constexpr (RESID) {
-          v[0] += bf16_lo(rr[t][0]);
-          v[1] += bf16_hi(rr[t][0]);
-          v[2] += bf16_lo(rr[t][1]);
-          v[3] += bf16_hi(rr[t][1]);
+        u32x2 packed;
+        if constexpr (kF32Stage) {
+          f32x4v v = *reinterpret_cast<const f32x4v*>(stage + (t * RPI + rl) * kPitch + c4 * 16);
+          if constexpr (RESID) {
+            v[0] += bf16_lo(rr[t][0]);
+            v[1] += bf16_hi(rr[t][0]);
+            v[2] += bf16_lo(rr[t][1]);
+            v[3] += bf16_hi(rr[t][1]);
+          }
+          packed = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        } else {
+          packed = *reinterpret_cast<const u32x2*>(stage + (t * RPI + rl) * kPitch + c4 * 8);
         }
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, rsrc_c,
-                                              voff[t], 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(packed, rsrc_c, voff[t], 0, 0);
       }
       if constexpr (PERSIST) {
         static_assert(32 / RPI * (WM - WM / 2) == kStoresAfter, "the prologue's wait counts these stores");
