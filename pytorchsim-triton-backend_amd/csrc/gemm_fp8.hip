@@ -243,46 +243,54 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   wait_vmcnt<0>();
 
   // accumulator (i, j, r) of lane holds C row m0 + wm*128 + i*32 + lane%32, columns
-  // n0 + wn*BN/2 + j*32 + 8*(r/4) + 4*(lane/32) + r%4.  The tile leaves through the LDS, which is
-  // free once every DMA has landed and, past the barrier, no wave reads a stage: a wave writes one
-  // 32-row block of its fp32 accumulators into a private, padded region and reads it back 4 columns
-  // a lane, so each store writes whole rows of its block (in the accumulator layout one store
-  // instruction writes 16 bytes into each of 32 rows) and each lane's 4 weight scales stay the
-  // same for the whole tile.  The region is the wave's own and LDS operations of a wave complete in
+  // n0 + wn*BN/2 + j*32 + 8*(r/4) + 4*(lane/32) + r%4.  Each value is scaled, (acc * sa) * sw, and
+  // rounded to bf16 where it sits, then the tile leaves through the LDS, which is free once every
+  // DMA has landed and, past the barrier, no wave reads a stage: a wave writes one 32-row block of
+  // its bf16 results into a private, padded region and reads it back 4 columns a lane, so each
+  // store writes whole rows of its block (in the accumulator layout one store instruction writes
+  // into each of 32 rows).  The region is the wave's own and LDS operations of a wave complete in
   // order, so no barrier separates its writes from its reads.  Rows past M and columns past N fall
   // outside the output's buffer resource (stores dropped), so the stores need no branches.
   sa_tile[tid] = sa_mine;
+  // the weight scales of this lane's accumulator columns: 4 consecutive ones per (j, g)
+  f32x4v swc[G::WNT][4];
+#pragma unroll
+  for (int j = 0; j < G::WNT; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c = n0 + wn * (BN / 2) + j * 32 + 8 * g + 4 * h;
+      swc[j][g] = *reinterpret_cast<const f32x4v*>(SW + (c < N ? c : 0));
+    }
   __syncthreads();
   constexpr int WC = G::WNT * 32;       // columns of a wave's block
-  constexpr int kPitch = WC * 4 + 16;   // bytes per staged row: rows start 4 banks apart
+  constexpr int kPitch = WC * 2 + 16;   // bytes per staged bf16 row: rows start 4 banks apart
   constexpr int LPR = WC / 4;           // lanes per row, 4 columns each
   constexpr int RPI = 64 / LPR;         // rows per instruction
   static_assert(4 * 32 * kPitch <= NS * G::kStageBytes, "the staging regions fit in the ring's LDS");
   uint8_t* const stage = smem + wave * (32 * kPitch);
   const int rl = lane / LPR, c4 = lane % LPR;
   const int gcol = n0 + wn * (BN / 2) + 4 * c4;
-  const f32x4v sw = *reinterpret_cast<const f32x4v*>(SW + (gcol < N ? gcol : 0));
   const __amdgpu_buffer_rsrc_t rsrc_c = __builtin_amdgcn_make_buffer_rsrc(
       C + int64_t(m0) * N, 0, uint32_t(min(BM, M - m0)) * uint32_t(N) * 2u, 0x00020000);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r0 = wm * 128 + i * 32 + rl;   // tile row of this lane's first row
-    float sa[32 / RPI];
-#pragma unroll
-    for (int t = 0; t < 32 / RPI; ++t) sa[t] = sa_tile[r0 + t * RPI];
+    const int r0 = wm * 128 + i * 32 + rl;   // tile row of this lane's first stored row
+    const float sa = sa_tile[wm * 128 + i * 32 + fr];
 #pragma unroll
     for (int j = 0; j < G::WNT; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<f32x4v*>(stage + fr * kPitch + (j * 32 + 8 * g + 4 * h) * 4) =
-            f32x4v{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+      for (int g = 0; g < 4; ++g) {
+        const f32x4v w4 = swc[j][g];
+        const float v0 = (acc[i][j][4 * g] * sa) * w4.x, v1 = (acc[i][j][4 * g + 1] * sa) * w4.y;
+        const float v2 = (acc[i][j][4 * g + 2] * sa) * w4.z, v3 = (acc[i][j][4 * g + 3] * sa) * w4.w;
+        *reinterpret_cast<u32x2*>(stage + fr * kPitch + (j * 32 + 8 * g + 4 * h) * 2) =
+            u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+      }
 #pragma unroll
     for (int t = 0; t < 32 / RPI; ++t) {
-      const f32x4v v = *reinterpret_cast<const f32x4v*>(stage + (t * RPI + rl) * kPitch + c4 * 16);
-      const float v0 = (v.x * sa[t]) * sw[0], v1 = (v.y * sa[t]) * sw[1];
-      const float v2 = (v.z * sa[t]) * sw[2], v3 = (v.w * sa[t]) * sw[3];
+      const u32x2 v = *reinterpret_cast<const u32x2*>(stage + (t * RPI + rl) * kPitch + c4 * 8);
       const uint32_t off = gcol < N ? (uint32_t(r0 + t * RPI) * uint32_t(N) + uint32_t(gcol)) * 2u : 0x80000000u;
-      __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)}, rsrc_c, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(v, rsrc_c, off, 0, 0);
     }
   }
 }
