@@ -158,10 +158,13 @@ int ptb_slice_add_bf16(const void* x, float* out, int64_t first, int64_t count, 
 int ptb_gemm_bf16(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n,
                   int64_t k, void* stream);
 
-/* The same GEMM with a caller workspace for split-K: when the 128x128 output tiles would fill at
- * most a quarter of the CUs (and K >= 1024), K is cut into slices multiplied by separate workgroups into
- * fp32 partials that a finish pass sums (+ residual) and rounds once.  ptb_gemm_bf16_workspace_bytes
- * is 0 for shapes that do not split; then ptb_gemm_bf16_ws is ptb_gemm_bf16.
+/* The same GEMM with a caller workspace for split-K: when the output's 64x128 tiles leave CUs idle
+ * (and K >= 1024), K may be cut into 2, 4 or 8 slices (at least 256 deep, tiles x slices within the
+ * CUs, as a fitted cost model of the workgroups' operand streaming and the partial traffic decides)
+ * multiplied by separate workgroups into fp32 partials that a finish pass sums (+ residual) and
+ * rounds once.  ptb_gemm_bf16_workspace_bytes is 0 for shapes that do not split; then
+ * ptb_gemm_bf16_ws is ptb_gemm_bf16.  A split shape refuses a NULL workspace (PTB_ERR_NULL) or one
+ * shorter than ptb_gemm_bf16_workspace_bytes (PTB_ERR_WORKSPACE).
  * Replaces: the same kernels as ptb_gemm_bf16 (the small M x N gemm_<M>x<K>x<N>_bf16 shapes). */
 size_t ptb_gemm_bf16_workspace_bytes(int64_t m, int64_t n, int64_t k);
 int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n, int64_t k,

@@ -30,6 +30,7 @@
 //
 // Tile order is XCD-aware: hardware hands workgroup i to XCD i % 8, so ids are remapped to give
 // each XCD a contiguous range of tiles, walked in groups of 8 tile-rows for L2 reuse.
+#include <algorithm>
 #include <type_traits>
 
 #include "ptb_common.h"
@@ -691,6 +692,69 @@ int cu_count() {
   return cus;
 }
 
+// Tile shape (wm x wn waves of 64x64 blocks: 4x4 = 256x256, 4x3 = 256x192, 4x2 = 256x128,
+// 2x2 = 128x128, 1x2 = 64x128) and K split of a GEMM.
+struct GemmPlan {
+  int wm, wn, splits;
+  int64_t kchunk;   // K columns per split
+};
+
+// Split-K cost model for 64x128 tiles, fitted to the bundle's 97 GEMM shapes with M >= 8 (each
+// (tile, split) timed on MI355X by HIP-graph replay): a launch costs kLaunchUs; a workgroup streams
+// its (64 + 128) x K/S operand bytes at min(kWgBpus, kChipBpus / workgroups); a split adds the
+// finish launch and 8 bytes of partial traffic (written, then read) per output per slice.
+constexpr double kLaunchUs = 2.5, kFinishUs = 1.5;
+constexpr double kWgBpus = 90e3;       // bytes per us one workgroup streams
+constexpr double kChipBpus = 25e6;     // L2 -> CU bytes per us over the chip
+constexpr double kPartialBpus = 2.5e6;
+
+// The largest tile that still gives every CU a tile: 256x256, else 256x128 (from 3/4 of the CUs:
+// one round of them beats 1.5 rounds of 128x128 tiles, 8192x3072x768 48.6 -> 35.3 us); then
+// 128x128 while its tiles cover 3/4 of the CUs (or 64x128 ones would need a second round); else
+// 64x128 (column tiles stay 128 wide: the B swizzle spans 16 chunks), its K split S ways (S fills at
+// most one round, slices at least 256 deep, K >= 1024) when the model above says the split pays:
+// over those 97 shapes the model's plans run 1.13x faster (geometric mean) than one pass of
+// 128x128 tiles or 128x128 splits, within 0.3% of the best measured plan.  Where 256x256 tiles
+// leave CUs idle but 256x128 ones would need a second round, 256x192 tiles when one round of them
+// covers more CUs (the fused q|k|v projection, 2048x4096x6144: 256 tiles against 192), else 256x256:
+// a 256x256 workgroup moves ~1.4x the flops per CU of a 256x128 one, so one round of it beats two
+// of the smaller.
+GemmPlan gemm_plan(int64_t m, int64_t n, int64_t k, bool may_split) {
+  const int64_t cus = cu_count();
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+  const int64_t t256 = tiles(256, 256), t256x192 = tiles(256, 192), t256x128 = tiles(256, 128);
+  const int64_t t128 = tiles(128, 128), t64 = tiles(64, 128);
+  if (t256 < cus && t256x128 > cus && t256x192 <= cus && t256x192 > t256) return {4, 3, 1, k};
+  if (t256 >= cus || t256x128 > cus) return {4, 4, 1, k};
+  if (4 * t256x128 >= 3 * cus) return {4, 2, 1, k};
+  if (4 * t128 >= 3 * cus || (t64 > cus && 2 * t128 >= cus)) return {2, 2, 1, k};
+  int best_s = 1;
+  double best_t = 0.0;
+  for (int sp = 1; sp <= 8; sp *= 2) {
+    if (sp > 1 && (!may_split || k < 1024 || k / sp < 256 || t64 * sp > cus)) continue;
+    const double wgs = double(t64 * sp);
+    const double rate = std::min(kWgBpus, kChipBpus / std::min(wgs, double(cus)));
+    double t = kLaunchUs + double(k) / sp * (64 + 128) * 2 / rate;
+    if (sp > 1) t += kFinishUs + sp * double(m) * double(n) * 8 / kPartialBpus;
+    if (sp == 1 || t < best_t) {
+      best_t = t;
+      best_s = sp;
+    }
+  }
+  if (best_s == 1) return {1, 2, 1, k};
+  const int64_t kc = ((k + best_s - 1) / best_s + 63) / 64 * 64;
+  return {1, 2, int((k + kc - 1) / kc), kc};
+}
+
+int launch_planned(const GemmPlan& p, const void* a, const void* b, const void* residual, void* c, int64_t m,
+                   int64_t n, int64_t k, hipStream_t s) {
+  if (p.wm == 4 && p.wn == 3) return launch_gemm<4, 3>(a, b, residual, c, m, n, k, s);
+  if (p.wm == 4 && p.wn == 4) return launch_gemm<4, 4>(a, b, residual, c, m, n, k, s);
+  if (p.wm == 4 && p.wn == 2) return launch_gemm<4, 2>(a, b, residual, c, m, n, k, s);
+  if (p.wm == 2 && p.wn == 2) return launch_gemm<2, 2>(a, b, residual, c, m, n, k, s);
+  return launch_gemm<1, 2>(a, b, residual, c, m, n, k, s);
+}
+
 }  // namespace
 
 PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual, void* c, int64_t m,
@@ -707,21 +771,7 @@ PTB_EXPORT int ptb_gemm_bf16(const void* a, const void* b, const void* residual,
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
-  // the largest tile that still gives every CU a tile: 256x256, else 256x128; then 128x128 while its
-  // tiles cover half the CUs, else 64x128 (column tiles stay 128 wide: the B swizzle spans 16 chunks).
-  // Where 256x256 tiles leave CUs idle but 256x128 ones would need a second round, 256x192 tiles
-  // when one round of them covers more CUs (the fused q|k|v projection, 2048x4096x6144: 256 tiles
-  // against 192), else 256x256: a 256x256 workgroup moves ~1.4x the flops per CU of a 256x128 one,
-  // so one round of it beats two of the smaller.
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t cus = cu_count();
-  auto tiles = [&](int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
-  if (tiles(256, 256) < cus && tiles(256, 128) > cus && tiles(256, 192) <= cus && tiles(256, 192) > tiles(256, 256))
-    return launch_gemm<4, 3>(a, b, residual, c, m, n, k, s);
-  if (tiles(256, 256) >= cus || tiles(256, 128) > cus) return launch_gemm<4, 4>(a, b, residual, c, m, n, k, s);
-  if (tiles(256, 128) >= cus) return launch_gemm<4, 2>(a, b, residual, c, m, n, k, s);
-  if (tiles(128, 128) * 2 >= cus) return launch_gemm<2, 2>(a, b, residual, c, m, n, k, s);
-  return launch_gemm<1, 2>(a, b, residual, c, m, n, k, s);   // 64 x 128: twice the tiles of 128 x 128
+  return launch_planned(gemm_plan(m, n, k, false), a, b, residual, c, m, n, k, static_cast<hipStream_t>(stream));
 }
 
 namespace {
@@ -757,56 +807,38 @@ __global__ __launch_bounds__(256) void splitk_finish(const float* __restrict__ P
   *reinterpret_cast<u32x2*>(C + q) = u32x2{pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w)};
 }
 
-// Split-K plan for a GEMM whose 128x128 tiles would fill at most a quarter of the CUs: S slices of kchunk
-// (a multiple of 64, at least 256) columns so that tiles * S roughly covers the chip once.  (Where
-// 256x128 tiles fill the CUs once, one pass over K beats splitting 256x256 tiles: 2048x12288x4096 +
-// residual 180 us as two 6144-deep slices + the finish, 162 us in one pass.)
-bool split_plan(int64_t m, int64_t n, int64_t k, int* splits, int* kchunk) {
-  const int64_t cus = cu_count();
-  const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-  // measured over the bundle's GEMM shapes: below K = 1024 one pass over K (about 7 us) beats
-  // partials plus the finish launch; slices under 256 deep cost more in pipeline fill than they save
-  if (k < 1024 || tiles * 4 > cus) return false;   // a quarter of the CUs or more: 64x128 tiles instead
-  int64_t s = (cus + tiles - 1) / tiles;
-  if (s > k / 256) s = k / 256;
-  if (s < 2) return false;
-  int64_t kc = ((k + s - 1) / s + 63) / 64 * 64;
-  s = (k + kc - 1) / kc;
-  if (s < 2) return false;
-  *splits = int(s);
-  *kchunk = int(kc);
-  return true;
-}
-
 }  // namespace
 
 PTB_EXPORT size_t ptb_gemm_bf16_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-  int s, kc;
-  if (m <= 0 || n <= 0 || k <= 0 || !split_plan(m, n, k, &s, &kc)) return 0;
-  return size_t(s) * size_t(m) * size_t(n) * sizeof(float);
+  if (m <= 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return 0;
+  const GemmPlan p = gemm_plan(m, n, k, true);
+  if (p.splits < 2) return 0;
+  return size_t(p.splits) * size_t(m) * size_t(n) * sizeof(float);
 }
 
 PTB_EXPORT int ptb_gemm_bf16_ws(const void* a, const void* b, const void* residual, void* c, int64_t m, int64_t n,
                                 int64_t k, void* workspace, size_t workspace_bytes, void* stream) {
-  int splits, kchunk;
-  if (m <= 0 || n <= 0 || k <= 0 || k % 64 || n % 8 || !split_plan(m, n, k, &splits, &kchunk))
-    return ptb_gemm_bf16(a, b, residual, c, m, n, k, stream);   // no split for this shape (or it is refused there)
-  if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return PTB_ERR_SHAPE;
+  if (m <= 0 || n <= 0 || k <= 0 || k % 64 || n % 8 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff)
+    return ptb_gemm_bf16(a, b, residual, c, m, n, k, stream);   // refused or trivial there
+  const GemmPlan p = gemm_plan(m, n, k, true);
+  if (p.splits < 2) return ptb_gemm_bf16(a, b, residual, c, m, n, k, stream);   // no split for this shape
   if (!a || !b || !c || !workspace) return PTB_ERR_NULL;
   if (workspace_bytes < ptb_gemm_bf16_workspace_bytes(m, n, k)) return PTB_ERR_WORKSPACE;
-  const int64_t bt = 128;   // tile rows and columns
-  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || bt * k * 2 >= (int64_t(1) << 32))
+  using Sh = Shape<1, 2, kBKOf<1, 2>>;   // the split plans use 64x128 tiles
+  if ((k + kRunAhead) * n * 2 >= (int64_t(1) << 32) || int64_t(Sh::BM) * k * 2 >= (int64_t(1) << 32))
     return PTB_ERR_UNSUPPORTED;
   if (!aligned16(a) || !aligned16(b) || !aligned16(c) || !aligned16(workspace) || (residual && !aligned16(residual)))
     return PTB_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t tm = (m + bt - 1) / bt, tn = (n + bt - 1) / bt;
+  const int64_t tm = (m + Sh::BM - 1) / Sh::BM, tn = (n + Sh::BN - 1) / Sh::BN;
+  if (tm * tn > 0x7fffffff) return PTB_ERR_GRID;
   const Groups none{nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
   float* part = static_cast<float*>(workspace);
+  const int splits = p.splits;
   const dim3 grid(unsigned(tm * tn), unsigned(splits));
-  gemm_bf16_kernel<2, 2, false, kSplit><<<grid, dim3(kThreads), 0, s>>>(
+  gemm_bf16_kernel<1, 2, false, kSplit, kBKOf<1, 2>><<<grid, dim3(kThreads), 0, s>>>(
         static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), nullptr, nullptr, int(m), int(n), int(k),
-        int(tm), int(tn), none, part, kchunk);
+        int(tm), int(tn), none, part, int(p.kchunk));
   const int64_t mn = m * n;
   splitk_finish<<<dim3(unsigned((mn / 4 + 255) / 256)), dim3(256), 0, s>>>(
       part, splits, mn, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(c));

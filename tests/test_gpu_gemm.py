@@ -195,8 +195,9 @@ def test_split_k_gemm(m, k, n, resid):
                                    (1800, 24576, 2000)])
 def test_no_split_below_1024(m, k, n):
     """Below K = 1024 a single pass over K is faster than partials plus a finish, and so is a GEMM
-    whose 128x128 tiles fill a quarter of the CUs or more (the o- and down projections, and a ragged
-    24576-deep one): no workspace is asked for, and the result matches the oracle."""
+    whose 256x256, 256x128 or 128x128 tiles cover 3/4 of the CUs (the o- and down projections, and
+    a ragged 24576-deep one with 240 128x128 tiles): no workspace is asked for, and the result
+    matches the oracle."""
     assert _lib.load().ptb_gemm_bf16_workspace_bytes(m, n, k) == 0
     a, b = randn((m, k), 35, std=1 / 32), randn((k, n), 36)
     got = ops.gemm(a.to(DEV), b.to(DEV)).cpu()
@@ -216,11 +217,20 @@ def test_split_k_exact_on_small_integers():
 
 
 @pytest.mark.parametrize("m,k,n,resid", [(2048, 768, 768, False), (1000, 768, 264, True), (768, 3072, 1024, False),
-                                         (4000, 384, 512, True)])
+                                         (4000, 384, 512, True), (2048, 4096, 1024, True)])
 def test_gemm_64x128_tiles(m, k, n, resid):
-    """Mid-size shapes whose 128x128 tiles leave CUs idle but too many to split run 64x128 tiles."""
+    """Mid-size shapes whose 128x128 tiles cover less than 3/4 of the CUs run 64x128 tiles (K split
+    when the plan's cost model says so: 768x3072x1024)."""
     c, want = run_gemm(m, k, n, 41, 1 / 32, 1 / 16, resid)
     assert_close(c, want, RTOL, 2e-2 * float(want.float().abs().mean()), f"64x128 {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,k,n,resid", [(6144, 1024, 1024, False), (6000, 768, 1000, True)])
+def test_gemm_256x128_tiles_from_three_quarters(m, k, n, resid):
+    """256x128 tiles that cover 3/4 of the CUs or more run as one round of them (192 tiles here),
+    ragged rows and columns included."""
+    c, want = run_gemm(m, k, n, 43, 1 / 32, 1 / 16, resid)
+    assert_close(c, want, RTOL, 2e-2 * float(want.float().abs().mean()), f"256x128 {m}x{k}x{n}")
 
 
 @pytest.mark.parametrize("m,k,inter", [(2048, 4096, 12288), (300, 512, 256), (64, 128, 128), (1000, 1024, 384)])
