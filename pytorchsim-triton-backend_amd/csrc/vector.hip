@@ -132,6 +132,25 @@ __device__ __forceinline__ void store8(OutT* __restrict__ yrow, int c, const flo
   }
 }
 
+// f[e] / s for the 8 exponentials of a chunk, s a row's sum (s >= 1: the row's maximum contributes
+// exp(0); NaN for a row holding a NaN) and r = 1/s correctly rounded.  q0 = f*r, then one fma
+// correction of the quotient (Markstein), which rounds exactly as the IEEE quotient does while q0
+// and the residual stay normal: every f >= 2^-64 (s <= 2^30, so q0 >= 2^-94).  A chunk holding a
+// smaller f (exp of an argument below -44, zeros of -inf entries) takes the IEEE division.
+__device__ __forceinline__ void div8_by_sum(float (&f)[8], float s, float r) {
+  const float lo = fminf(fminf(fminf(f[0], f[1]), fminf(f[2], f[3])), fminf(fminf(f[4], f[5]), fminf(f[6], f[7])));
+  if (__builtin_expect(lo < 0x1p-64f, 0)) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = f[e] / s;
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float q0 = f[e] * r;
+    f[e] = __builtin_fmaf(__builtin_fmaf(-s, q0, f[e]), r, q0);
+  }
+}
+
 template <int TPR, int VPT, typename OutT>
 __global__ __launch_bounds__(kBlock) void softmax_rows(const uint16_t* __restrict__ x,
                                                        OutT* __restrict__ y, int64_t rows, int cols) {
@@ -156,29 +175,30 @@ __global__ __launch_bounds__(kBlock) void softmax_rows(const uint16_t* __restric
     }
   }
   mx = team_max<TPR>(mx, red);
+  // the exponentials stay in registers between the sum and the stores
+  float ex[VPT][8];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = lt + i * TPR;
-    if (live && c < chunks) {
-      float f[8];
-      unpack8(v[i], f);
+    unpack8(v[i], ex[i]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s += exp_e(f[e] - mx);
+    for (int e = 0; e < 8; ++e) ex[i][e] = exp_e(ex[i][e] - mx);
+    if (live && c < chunks) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += ex[i][e];
     }
   }
   s = team_sum<TPR>(s, red);
   if (!live) return;
+  const float r = 1.0f / s;
   OutT* yr = y + row * int64_t(cols);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = lt + i * TPR;
     if (c >= chunks) continue;
-    float f[8];
-    unpack8(v[i], f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = exp_e(f[e] - mx) / s;
-    store8(yr, c, f);
+    div8_by_sum(ex[i], s, r);
+    store8(yr, c, ex[i]);
   }
 }
 
@@ -204,12 +224,14 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_long(const uint16_t* __re
     for (int e = 0; e < 8; ++e) s += exp_e(f[e] - mx);
   }
   s = block_sum<kBlock / kWave>(s, red);
+  const float r = 1.0f / s;
   OutT* yr = y + row * int64_t(cols);
   for (int c = threadIdx.x; c < chunks; c += kBlock) {
     float f[8];
     unpack8(xr[c], f);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = exp_e(f[e] - mx) / s;
+    for (int e = 0; e < 8; ++e) f[e] = exp_e(f[e] - mx);
+    div8_by_sum(f, s, r);
     store8(yr, c, f);
   }
 }
