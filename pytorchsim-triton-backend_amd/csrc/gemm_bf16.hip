@@ -130,19 +130,6 @@ constexpr int kMaxDedupGroups = 1024;   // group tables up to this size have rep
 // bf16(silu(bf16(gate)) * bf16(up)), as a separate silu_mul would compute it from the bf16 GEMM.
 enum { kPlain = 0, kGrouped = 1, kSplit = 2, kSwiGLU = 3 };
 
-// The SwiGLU epilogue's quotient g / b, b = 2^(-g log2 e) + 1 (>= 1, +inf or NaN), for g a bf16
-// value: the reciprocal, one correction of the quotient by its fma residual (Markstein), then the
-// hardware's special-operand fixup (infinite or NaN operands, the sign of a zero).  Equal to the
-// IEEE quotient -- the division silu_mul performs -- for every bf16 value of g whose b is below
-// 2^126 (checked through the product entry point against GEMM + silu_mul); a larger b (g in about
-// [-88.7, -87.3]) has a subnormal reciprocal, which v_rcp_f32 flushes to zero, so the caller
-// divides those in IEEE arithmetic.  5 instructions where the IEEE sequence takes 9.
-__device__ __forceinline__ float silu_quotient(float g, float b) {
-  const float r = __builtin_amdgcn_rcpf(b);
-  const float q0 = g * r;
-  const float e = __builtin_fmaf(-b, q0, g);
-  return __builtin_amdgcn_div_fixupf(__builtin_fmaf(e, r, q0), b, g);
-}
 
 // PERSIST (plain 256x256 tiles, no residual): one workgroup per CU walks the tiles
 // blockIdx.x, blockIdx.x + gridDim.x, ...; the next tile's first stage goes out halfway through the

@@ -39,6 +39,20 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
 }
 
+// silu's quotient g / b, b = 2^(-g log2 e) + 1 (>= 1, +inf or NaN), for g a bf16 value (the SwiGLU
+// GEMM epilogue and silu_mul): the reciprocal, one correction of the quotient by its fma residual
+// (Markstein), then the hardware's special-operand fixup (infinite or NaN operands, the sign of a
+// zero).  Equal to the IEEE quotient for every bf16 value of g whose b is below 2^126 (checked on
+// the device for all 65536 bf16 patterns of g); a larger b (g in about [-88.7, -87.3]) has a
+// subnormal reciprocal, which v_rcp_f32 flushes to zero, so the caller divides those in IEEE
+// arithmetic.  5 instructions where the IEEE sequence takes 9.
+__device__ __forceinline__ float silu_quotient(float g, float b) {
+  const float r = __builtin_amdgcn_rcpf(b);
+  const float q0 = g * r;
+  const float e = __builtin_fmaf(-b, q0, g);
+  return __builtin_amdgcn_div_fixupf(__builtin_fmaf(e, r, q0), b, g);
+}
+
 // NaN-propagating max (triton's tl.maximum(..., PropagateNan.ALL)): NaN if either input is NaN
 // (a's NaN if a is one, else b's).  Written as two selects on the bit patterns: nested ternaries
 // on float compares compile to branches.

@@ -249,7 +249,10 @@ __global__ __launch_bounds__(kBlock) void silu_mul(const uint16_t* __restrict__ 
   for (int i = 0; i < kPer; ++i) {
     id[i] = idx + i * stride;
     if (id[i] < total_chunks) {
-      const int64_t r = id[i] / inter_chunks, c = id[i] - r * inter_chunks;
+      // 32-bit division where the chunk count allows (a 64-bit one is a long instruction sequence)
+      const int64_t r = total_chunks <= 0xffffffffll ? int64_t(uint32_t(id[i]) / uint32_t(inter_chunks))
+                                                     : id[i] / inter_chunks;
+      const int64_t c = id[i] - r * inter_chunks;
       const u32x4* src = reinterpret_cast<const u32x4*>(gu) + r * 2 * inter_chunks;
       g[i] = src[c];
       u[i] = src[inter_chunks + c];
@@ -261,8 +264,21 @@ __global__ __launch_bounds__(kBlock) void silu_mul(const uint16_t* __restrict__ 
     float fg[8], fu[8];
     unpack8(g[i], fg);
     unpack8(u[i], fu);
+    float b[8], q[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) fg[e] = (fg[e] / (exp_e(-fg[e]) + 1.0f)) * fu[e];
+    for (int e = 0; e < 8; ++e) {
+      b[e] = exp_e(-fg[e]) + 1.0f;
+      q[e] = silu_quotient(fg[e], b[e]);
+    }
+    // the IEEE division where a denominator reaches 2^126 (fmaxf skips a NaN b, whose quotient the
+    // fixup already made NaN)
+    const float bmax = fmaxf(fmaxf(fmaxf(b[0], b[1]), fmaxf(b[2], b[3])), fmaxf(fmaxf(b[4], b[5]), fmaxf(b[6], b[7])));
+    if (__builtin_expect(bmax >= 0x1p126f, 0)) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[e] = fg[e] / b[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) fg[e] = q[e] * fu[e];
     reinterpret_cast<u32x4*>(out)[id[i]] = pack8(fg);
   }
 }
