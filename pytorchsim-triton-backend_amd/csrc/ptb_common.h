@@ -53,23 +53,14 @@ __device__ __forceinline__ float silu_quotient(float g, float b) {
   return __builtin_amdgcn_div_fixupf(__builtin_fmaf(e, r, q0), b, g);
 }
 
-// NaN-propagating max (triton's tl.maximum(..., PropagateNan.ALL)): NaN if either input is NaN
-// (a's NaN if a is one, else b's).  Written as two selects on the bit patterns: nested ternaries
-// on float compares compile to branches.
-__device__ __forceinline__ float max_nan(float a, float b) {
-  const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
-  const uint32_t m = __float_as_uint(fmaxf(a, b));
-  const uint32_t t = (ub & 0x7fffffffu) > 0x7f800000u ? ub : m;
-  return __uint_as_float((ua & 0x7fffffffu) > 0x7f800000u ? ua : t);
-}
+// NaN-propagating max (triton's tl.maximum(..., PropagateNan.ALL)): NaN if either input is NaN.
+// The IEEE 754-2019 maximum, which gfx950 executes as v_maximum3_f32 (three operands, so a chain of
+// them takes two new values an instruction); it also orders -0 below +0.
+__device__ __forceinline__ float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
-// NaN-propagating max of 8 values: an fmaxf tree (v_max3) and the isnan flags OR-ed as lane masks,
-// one select at the end (a NaN result is the canonical quiet NaN).
+// NaN-propagating max of 8 values: four v_maximum3_f32.
 __device__ __forceinline__ float max8_nan(const float (&f)[8]) {
-  const float m = fmaxf(fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3])), fmaxf(fmaxf(f[4], f[5]), fmaxf(f[6], f[7])));
-  const bool nan = __builtin_isnan(f[0]) | __builtin_isnan(f[1]) | __builtin_isnan(f[2]) | __builtin_isnan(f[3]) |
-                   __builtin_isnan(f[4]) | __builtin_isnan(f[5]) | __builtin_isnan(f[6]) | __builtin_isnan(f[7]);
-  return nan ? __builtin_nanf("") : m;
+  return max_nan(max_nan(max_nan(f[0], f[1]), max_nan(f[2], f[3])), max_nan(max_nan(f[4], f[5]), max_nan(f[6], f[7])));
 }
 
 // fp32 -> OCP e4m3fn bits with round-to-nearest-even, following torch's float8_e4m3fn cast:
