@@ -127,10 +127,11 @@ def test_qk_norm_rope(tokens, heads, tables, seed):
 
 
 @pytest.mark.parametrize("n,seed", [(12288 * 4096, 0), (1024 * 1024, 1), (8 * 128 + 5, 2), (3, 3),
-                                    (32768, 4), (32769, 5), (4096 + 8, 6), (16384, 7), (517, 8)])
+                                    (98304, 4), (98305, 5), (4096 + 8, 6), (16384, 7), (517, 8),
+                                    (65536 + 13, 9)])
 def test_reduce(n, seed):
-    """Two passes above 32768 elements, one workgroup of 64..512 threads at or below (skipped
-    slots, a tail of n % 8 elements)."""
+    """Two passes above 98304 elements, one workgroup of 64..1024 threads at or below (batches of
+    65536 elements, skipped slots, a tail of n % 8 elements)."""
     x = randn((n,), seed)
     xd = x.to(DEV)
     got_max = ops.reduce(xd, "max").cpu()
