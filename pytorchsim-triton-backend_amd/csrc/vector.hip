@@ -543,6 +543,13 @@ int softmax_launch(const void* x, void* y, int64_t rows, int64_t cols, void* str
   OutT* yo = static_cast<OutT*>(y);
   int tpr, vpt;
   if (row_shape(c, &tpr, &vpt)) {
+    // at most one workgroup per CU's worth of rows: a 256-thread team per row, so each lane holds
+    // as few chunks as it can (the row's latency, not the throughput, sets the time)
+    const int chunks = c / 8;
+    if (rows <= 256 && chunks > 64) {
+      tpr = 256;
+      vpt = chunks <= 256 ? 1 : chunks <= 512 ? 2 : chunks <= 1024 ? 4 : 8;
+    }
     const int teams = kBlock / tpr;
     const int64_t blocks = (rows + teams - 1) / teams;
     if (blocks > 0x7fffffff) return PTB_ERR_GRID;
@@ -551,7 +558,7 @@ int softmax_launch(const void* x, void* y, int64_t rows, int64_t cols, void* str
     softmax_rows<T, V, OutT><<<dim3(unsigned(blocks)), dim3(kBlock), 0, s>>>(xi, yo, rows, c);      \
     return launch_status();                                                                           \
   }
-    SM_CASE(64, 1) SM_CASE(64, 2) SM_CASE(64, 4) SM_CASE(256, 2) SM_CASE(256, 4) SM_CASE(256, 8)
+    SM_CASE(64, 1) SM_CASE(64, 2) SM_CASE(64, 4) SM_CASE(256, 1) SM_CASE(256, 2) SM_CASE(256, 4) SM_CASE(256, 8)
 #undef SM_CASE
   }
   if (rows > 0x7fffffff) return PTB_ERR_GRID;
