@@ -1,7 +1,8 @@
 // Single-token (decode) kernels on gfx950: sum of squares, matrix-vector products with the decode
 // layer's fused prologues / epilogue, and flash-decoding attention over a KV cache.  All of them
 // stream their big operand (the weight matrix, the K/V cache) from HBM once and are bound by HBM
-// bandwidth, so they are built for bytes in flight, not for the matrix cores.
+// bandwidth, so they are built for bytes in flight; decode attention over more than 256 keys puts
+// its dot products on the matrix cores only to keep the VALU work after each load short.
 //
 // GEMV, y[n] = sum_k xp[k] * W[k, n] with W row-major [K, N] (N contiguous), split over K:
 //   pass 1: workgroup (column block of 512, K slice of `kb` rows); the slice's xp[k] (the fused
@@ -11,7 +12,10 @@
 //           meet in LDS and the slice's fp32 partials go to the workspace [splits, N].
 //   pass 2: y[n] = bf16(sum over splits (+ r1[n] + r2[n])), one rounding.
 // Decode attention (one query token, G query heads per kv head, S cached keys, D = 128):
-//   pass 1: workgroup (key range, query rows of a kv head): teams of 256 threads each take a 64-key
+//   pass 1, more than 256 keys: one wave per (key range, kv head), 32-key steps through LDS, scores
+//           and P.V on v_mfma_f32_16x16x32_bf16 with the head's G query rows as the N side (K and V
+//           read once); an (acc, m, l) record per range (attn_decode_mfma below).
+//   pass 1, up to 256 keys: workgroup (key range, query rows of a kv head): teams of 256 threads each take a 64-key
 //           chunk per step (scores with 16 lanes per key, one 256-byte row, summed by DPP row
 //           moves; a running base-2 softmax; the next step's K and V in flight meanwhile) and meet
 //           in LDS.  A cache of at most four chunks (two for more than 3 rows a workgroup) is one
@@ -21,6 +25,7 @@
 #include <cmath>
 
 #include <mutex>
+#include <type_traits>
 
 #include "ptb_common.h"
 
@@ -390,6 +395,8 @@ constexpr int kChunk = 64;          // keys per team step
 constexpr int kTeam = 256;          // threads per 64-key chunk
 constexpr int kMaxRecords = 256;    // key ranges per kv head that the merge pass combines
 
+// The VALU form below serves caches of at most kWaveMinSeq (256) keys, which this plan covers in one
+// pass (records = 1) for every G; its range plans are the general case of the same cut.
 // How a kv head's work is cut: its G query rows go to `gsplit` workgroup rows of G / gsplit each,
 // and its keys to `records` workgroups holding `teams` teams of 256 threads, each team taking one
 // 64-key chunk per step for `steps` steps.  A cache that the teams of one workgroup cover in one
@@ -445,6 +452,76 @@ __device__ __forceinline__ void load_step(const uint16_t* __restrict__ kp, const
   }
 }
 
+// One 16-byte query vector, dims 8*(qi%16).. of query head qi/16 (the layout of the q/k-norm
+// kernel), with, for the fused q-norm + RoPE (qw given), its norm weights and the token's cos/sin.
+struct QVec {
+  u32x4 q, w, wp;
+  f32x4v cs0, cs1, sn0, sn1;
+};
+__device__ __forceinline__ QVec load_qvec(const uint16_t* __restrict__ q, int qi, const uint16_t* __restrict__ qw,
+                                          const float* __restrict__ qcos, const float* __restrict__ qsin) {
+  QVec v;
+  v.q = *reinterpret_cast<const u32x4*>(q + 8 * qi);
+  const int qc = qi & 15;
+  v.w = u32x4{0u, 0u, 0u, 0u};
+  v.wp = v.w;
+  v.cs0 = f32x4v{0.f, 0.f, 0.f, 0.f};
+  v.cs1 = v.cs0;
+  v.sn0 = v.cs0;
+  v.sn1 = v.cs0;
+  if (qw) {
+    v.w = reinterpret_cast<const u32x4*>(qw)[qc];
+    v.wp = reinterpret_cast<const u32x4*>(qw)[qc ^ 8];
+    v.cs0 = reinterpret_cast<const f32x4v*>(qcos + 8 * qc)[0];
+    v.cs1 = reinterpret_cast<const f32x4v*>(qcos + 8 * qc)[1];
+    v.sn0 = reinterpret_cast<const f32x4v*>(qsin + 8 * qc)[0];
+    v.sn1 = reinterpret_cast<const f32x4v*>(qsin + 8 * qc)[1];
+  }
+  return v;
+}
+// The vector's 8 values as fp32 (exact bf16 values).  With q-norm + RoPE: the q/k-norm kernel's
+// arithmetic, rounded to bf16 as its output is; the sum of squares meets across the 16 lanes of
+// the head (a 16-lane row), so all 16 lanes of a row call this together.
+__device__ __forceinline__ void qvec_values(const QVec& v, int qi, bool norm, float qeps, float (&qf8)[8]) {
+  const int qc = qi & 15;
+  const u32x4 qv = v.q, wv = v.w, wp = v.wp;
+  const f32x4v cs0 = v.cs0, cs1 = v.cs1, sn0 = v.sn0, sn1 = v.sn1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    qf8[2 * e] = bf16_lo(qv[e]);
+    qf8[2 * e + 1] = bf16_hi(qv[e]);
+  }
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(qf8[e], qf8[e], ss);
+    ss = row16_sum(ss);
+    float pf[8], wf[8], pw[8];
+    u32x4 pv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pv[e] = xor8_u32(qv[e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      pf[2 * e] = bf16_lo(pv[e]);
+      pf[2 * e + 1] = bf16_hi(pv[e]);
+      wf[2 * e] = bf16_lo(wv[e]);
+      wf[2 * e + 1] = bf16_hi(wv[e]);
+      pw[2 * e] = bf16_lo(wp[e]);
+      pw[2 * e + 1] = bf16_hi(wp[e]);
+    }
+    const float r = 1.0f / sqrtf(ss / float(kD) + qeps);
+    const float cs[8] = {cs0.x, cs0.y, cs0.z, cs0.w, cs1.x, cs1.y, cs1.z, cs1.w};
+    const float sn[8] = {sn0.x, sn0.y, sn0.z, sn0.w, sn1.x, sn1.y, sn1.z, sn1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = (qf8[e] * r) * wf[e];
+      const float pp = (pf[e] * r) * pw[e];
+      const float rot = qc < 8 ? -pp : pp;
+      qf8[e] = bf16_to_f32(f32_to_bf16(fmaf(a, cs[e], rot * sn[e])));
+    }
+  }
+}
+
 // Workgroup (key range, kv head) of T teams.  Team t walks chunks (range*steps + s)*T + t: scores
 // t = (q.k) * scale*log2(e) with 16 lanes a key, a running base-2 softmax (m = running max, p =
 // 2^(t-m), l = l*2^(m_old-m) + sum of fp32 p) and acc = acc*2^(m_old-m) + sum bf16(p) * v, the next
@@ -476,57 +553,11 @@ __global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t*
   // 16 bytes a lane, lanes past the G*16 vectors repeat the last one (the same value, and no
   // branch for the load to sink into)
   const int qi = min(tid, G * kD / 8 - 1);
-  const u32x4 qv = *reinterpret_cast<const u32x4*>(q + 8 * qi);
-  // fused q-norm + RoPE (qw given): lane qi holds dims 8*(qi%16).. of head qi/16, as the q/k-norm
-  // kernel lays them out; its weights and the token's cos/sin are read here too
-  const int qc = qi & 15;
-  u32x4 wv = {0u, 0u, 0u, 0u}, wp = {0u, 0u, 0u, 0u};
-  f32x4v cs0 = {0.f, 0.f, 0.f, 0.f}, cs1 = cs0, sn0 = cs0, sn1 = cs0;
-  if (qw) {
-    wv = reinterpret_cast<const u32x4*>(qw)[qc];
-    wp = reinterpret_cast<const u32x4*>(qw)[qc ^ 8];
-    cs0 = reinterpret_cast<const f32x4v*>(qcos + 8 * qc)[0];
-    cs1 = reinterpret_cast<const f32x4v*>(qcos + 8 * qc)[1];
-    sn0 = reinterpret_cast<const f32x4v*>(qsin + 8 * qc)[0];
-    sn1 = reinterpret_cast<const f32x4v*>(qsin + 8 * qc)[1];
-  }
+  const QVec qv = load_qvec(q, qi, qw, qcos, qsin);
   u32x4 kr[kChunk / 16], vr[kChunk / 16];
   load_step(kp, vp, first * kChunk, S, kj, d8, kr, vr);
   float qf8[8];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    qf8[2 * e] = bf16_lo(qv[e]);
-    qf8[2 * e + 1] = bf16_hi(qv[e]);
-  }
-  if (qw) {   // the q/k-norm kernel's arithmetic, rounded to bf16 as its output is
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf(qf8[e], qf8[e], ss);
-    ss = row16_sum(ss);
-    float pf[8], wf[8], pw[8];
-    u32x4 pv;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) pv[e] = xor8_u32(qv[e]);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      pf[2 * e] = bf16_lo(pv[e]);
-      pf[2 * e + 1] = bf16_hi(pv[e]);
-      wf[2 * e] = bf16_lo(wv[e]);
-      wf[2 * e + 1] = bf16_hi(wv[e]);
-      pw[2 * e] = bf16_lo(wp[e]);
-      pw[2 * e + 1] = bf16_hi(wp[e]);
-    }
-    const float r = 1.0f / sqrtf(ss / float(kD) + qeps);
-    const float cs[8] = {cs0.x, cs0.y, cs0.z, cs0.w, cs1.x, cs1.y, cs1.z, cs1.w};
-    const float sn[8] = {sn0.x, sn0.y, sn0.z, sn0.w, sn1.x, sn1.y, sn1.z, sn1.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float a = (qf8[e] * r) * wf[e];
-      const float pp = (pf[e] * r) * pw[e];
-      const float rot = qc < 8 ? -pp : pp;
-      qf8[e] = bf16_to_f32(f32_to_bf16(fmaf(a, cs[e], rot * sn[e])));
-    }
-  }
+  qvec_values(qv, qi, qw != nullptr, qeps, qf8);
   // lanes past the G*16 vectors hold repeats (whose norms are not their head's): they do not store
   if (tid < G * kD / 8) {
 #pragma unroll
@@ -750,6 +781,220 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
   }
 }
 
+// Decode attention on the matrix cores.  Workgroup = one wave = (key range, kv head); the range's
+// `steps` steps of 32 keys run in turn, each step's K and V tiles moving HBM -> LDS with
+// buffer_load ... lds (the next step's while this one computes; keys past S read as zero through
+// the buffer range).  All G <= 16 query rows of the kv head are the N side of
+// v_mfma_f32_16x16x32_bf16, so K and V are read once whatever G is:
+//   S^T[key][q] = K Q^T: A = K (lane: key 16t + l%16, dims 32kk + 8(l/16) .. +7, from the K tile),
+//   B = Q^T (lane: query l%16, the same dims; rows past G are zero); key tile t's accumulator leaves
+//   lane l the scores of keys 16t + 4(l/16) + i (i < 4) of query l%16.
+//   O^T[d][q] += V^T[d][key] P^T[key][q]: B = P^T straight from the score accumulators (k slot
+//   8(l/16) + j is key 4(l/16) + j for j < 4 and 16 + 4(l/16) + j - 4 for j >= 4), A = V^T from two
+//   ds_read_b64_tr_b16 of the V tile per 16 dims (a 16-lane group reads 4 keys x 16 dims).
+// Online softmax in base 2 per step, as the reference's decode kernel per key block: t = (q.k) *
+// scale*log2(e), m = running max, p = 2^(t - m), l = l*2^(m_old - m) + sum of fp32 p (each lane
+// sums its own keys; the four lane groups add up at the end), acc = acc*2^(m_old - m) + bf16(p) V.
+// One range writes o = bf16(acc / l) itself; more leave (acc, m, l) records for attn_decode_merge.
+constexpr int kWKeys = 32;                   // keys per wave step
+constexpr int kWTile = kWKeys * kD * 2;      // 8 KB: one step's K or V tile
+
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+
+__device__ __forceinline__ bf16x8 lds_b128(uint32_t addr) {
+  return *reinterpret_cast<const lds_bf16x8*>(size_t(addr));
+}
+__device__ __forceinline__ i16x4 lds_tr16(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(size_t(addr)));
+}
+
+template <int G>
+__global__ __launch_bounds__(64) void attn_decode_mfma(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc,
+                                                       const uint16_t* __restrict__ Vc, uint16_t* __restrict__ O,
+                                                       float* __restrict__ part, int S, float c, int steps,
+                                                       const uint16_t* __restrict__ qw, const float* __restrict__ qcos,
+                                                       const float* __restrict__ qsin, float qeps) {
+  static_assert(G >= 1 && G <= 16, "the query rows fit the MFMA's N side");
+  constexpr int kRec = int(record_floats(G));
+  constexpr int kQVecs = G * kD / 8;         // 16-byte query vectors
+  // two stages of (K tile, V tile), then the query rows as bf16 [16][128] (rows past G zero)
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * kWTile + 16 * kD * 2];
+  const int range = blockIdx.x, kvh = blockIdx.y, nrec = gridDim.x;
+  const int lane = threadIdx.x, l16 = lane & 15, g4 = lane >> 4;
+  const uint16_t* kp = Kc + int64_t(kvh) * S * kD;
+  const uint16_t* vp = Vc + int64_t(kvh) * S * kD;
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
+  uint8_t* const qs = smem + 4 * kWTile;
+
+  // DMA instruction i of a tile fills key rows 4i .. 4i+3: lane L writes row 4i + L/16, slot L%16,
+  // so it fetches the chunk that belongs in that slot.  K row r keeps chunk c in slot c ^ (r & 15)
+  // (a fragment read's 16 lanes take 16 rows); V row r keeps chunk c in slot c ^ (4 * (r & 3)) (a
+  // transposing read's 16 lanes take 4 rows x 4 chunks).
+  // Offsets stay in the VGPR operand (soffset 0), which the buffer range check covers.
+  uint32_t koff[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + g4;
+    koff[i] = uint32_t(r * 256 + ((l16 ^ (r & 15)) << 4));
+  }
+  const uint32_t vdma = uint32_t(g4 * 256 + ((l16 ^ (4 * g4)) << 4));
+  auto issue = [&](int s, auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    const int key0 = (range * steps + s) * kWKeys;
+    const uint32_t bytes = uint32_t(max(0, min(kWKeys, S - key0))) * uint32_t(kD * 2);
+    i32x4 rk = make_rsrc(kp + int64_t(key0) * kD, bytes);
+    i32x4 rv = make_rsrc(vp + int64_t(key0) * kD, bytes);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {   // wave-uniform values, kept in SGPRs as the instruction needs
+      rk[e] = __builtin_amdgcn_readfirstlane(rk[e]);
+      rv[e] = __builtin_amdgcn_readfirstlane(rv[e]);
+    }
+    const uint32_t st = lds0 + uint32_t(P * 2 * kWTile);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      dma16(rk, __builtin_amdgcn_readfirstlane(st + i * 1024), koff[i], 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      dma16(rv, __builtin_amdgcn_readfirstlane(st + kWTile + i * 1024), vdma + i * 1024, 0);
+  };
+  issue(0, std::integral_constant<int, 0>{});
+
+  // the query rows into LDS (vector v at byte 16 v: row v / 16, dims 8 (v % 16) ..), zero past G;
+  // the 16 lanes of a row hold one head's vectors, as qvec_values wants
+  const uint16_t* q = Q + int64_t(kvh) * G * kD;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int v = lane + 64 * u;
+    u32x4 packed = {0u, 0u, 0u, 0u};
+    if (64 * u < kQVecs) {
+      const int qi = min(v, kQVecs - 1);
+      const QVec qv = load_qvec(q, qi, qw, qcos, qsin);
+      float qf8[8];
+      qvec_values(qv, qi, qw != nullptr, qeps, qf8);
+      if (v < kQVecs) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) packed[e] = pack_bf16x2(qf8[2 * e], qf8[2 * e + 1]);
+      }
+    }
+    *reinterpret_cast<u32x4*>(qs + 16 * v) = packed;
+  }
+  // B = Q^T fragments: query l16, dims 32kk + 8 g4 .. +7 (the wave's own LDS writes are done)
+  bf16x8 qf[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    qf[kk] = *reinterpret_cast<const bf16x8*>(qs + l16 * 256 + (4 * kk + g4) * 16);
+
+  // V^T fragment reads: in-group lane 4 jj + qq supplies key 4 g4 + jj (16 more for the second
+  // read), dims 16 dt + 4 qq .. +3 = chunk 2 dt + qq / 2, byte 8 (qq & 1) within it
+  const int jj = l16 >> 2, qq = l16 & 3;
+  uint32_t vrd[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+    vrd[dt] = uint32_t((4 * g4 + jj) * 256 + (((2 * dt + (qq >> 1)) ^ (4 * jj)) << 4) + (qq & 1) * 8);
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, lsum = 0.f;
+
+  auto step = [&](int s, auto par, auto more) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    constexpr bool MORE = decltype(more)::value;
+    // the next step's tiles go into the other stage, whose reads (the previous step's) are done
+    if constexpr (MORE) issue(s + 1, std::integral_constant<int, 1 - P>{});
+    const uint32_t st = lds0 + uint32_t(P * 2 * kWTile);
+    wait_vmcnt<MORE ? 24 : 8>();   // this step's K tile has landed (its V tile may still be coming)
+    f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bf16x8 kf = lds_b128(st + (16 * t + l16) * 256 + (((4 * kk + g4) ^ l16) << 4));
+        sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[kk], sacc[t], 0, 0, 0);
+      }
+    const int key0 = (range * steps + s) * kWKeys;
+    float tv[2][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        tv[t][i] = key0 + 16 * t + 4 * g4 + i < S ? sacc[t][i] * c : -INFINITY;
+        mx = fmaxf(mx, tv[t][i]);
+      }
+    mx = pair32_max(pair16_max(mx));
+    const float mnew = fmaxf(m, mx);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(m - mref);
+    m = mnew;
+    float ps = 0.f;
+    uint32_t pb[4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(tv[t][i] - mref);
+        const float p1 = __builtin_amdgcn_exp2f(tv[t][i + 1] - mref);
+        ps += p0;
+        ps += p1;
+        pb[2 * t + i / 2] = pack_bf16x2(p0, p1);
+      }
+    lsum = __builtin_fmaf(lsum, alpha, ps);
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+    }
+    const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pb[0], pb[1], pb[2], pb[3]});
+    wait_vmcnt<MORE ? 16 : 0>();   // this step's V tile has landed
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const i16x4 lo = lds_tr16(st + kWTile + vrd[dt]);
+      const i16x4 hi = lds_tr16(st + kWTile + vrd[dt] + 16 * 256);
+      const bf16x8 vf = __builtin_bit_cast(bf16x8, i16x8(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)));
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, acc[dt], 0, 0, 0);
+    }
+  };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using More = std::true_type;
+  using Last = std::false_type;
+  int s = 0;
+  for (; s + 2 < steps; s += 2) {
+    step(s, P0{}, More{});
+    step(s + 1, P1{}, More{});
+  }
+  if (s + 1 < steps) {
+    step(s, P0{}, More{});
+    step(s + 1, P1{}, Last{});
+  } else {
+    step(s, P0{}, Last{});
+  }
+
+  // lane l holds O^T[16 dt + 4 g4 + i][l16]; the query's l is the sum over its four lane groups
+  lsum = pair32_sum(pair16_sum(lsum));
+  if (l16 < G) {
+    if (nrec == 1) {
+      uint16_t* o = O + (int64_t(kvh) * G + l16) * kD + 4 * g4;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<u32x2v*>(o + 16 * dt) =
+            u32x2v{pack_bf16x2(acc[dt][0] / lsum, acc[dt][1] / lsum), pack_bf16x2(acc[dt][2] / lsum, acc[dt][3] / lsum)};
+    } else {
+      float* rec = part + (int64_t(kvh) * nrec + range) * kRec;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(rec + l16 * kD + 16 * dt + 4 * g4) = acc[dt];
+      if (g4 == 0) {
+        rec[G * kD + l16] = m;
+        rec[G * kD + G + l16] = lsum;
+      }
+    }
+  }
+}
+
 // q-norm + RoPE fused into the prologue when qw is given (per-head weights [128], the token's
 // cos / sin [128]): q is then the projection's raw output
 struct QNorm {
@@ -764,6 +1009,28 @@ void launch_partial(const uint16_t* q, const uint16_t* k, const uint16_t* v, uin
                     int seq, float c, const DecodePlan& p, const QNorm& qn, hipStream_t s) {
   attn_decode_partial<G, T><<<dim3(unsigned(p.records), unsigned(nkv * p.gsplit)), dim3(kTeam * T), 0, s>>>(
       q, k, v, o, part, seq, c, p.steps, p.gsplit, qn.w, qn.cos, qn.sin, qn.eps);
+}
+
+// The matrix-core form's cut of a kv head: `records` ranges of `steps` 32-key steps each, at most
+// kMaxRecords ranges (the merge pass's limit).  It serves caches of more than kWaveMinSeq keys: on
+// MI355X (8 kv heads, graph replay) 512 keys 6.98 -> 6.66 us, 4096 keys 11.46 -> 10.63 us, 32768
+// keys 38.7 -> 32.4 us against the VALU form, and G = 8 at 4096 keys 15.2 -> 11.9 us.
+constexpr int64_t kWaveMinSeq = 256;
+struct WavePlan {
+  int steps, records;
+};
+WavePlan wave_plan(int64_t seq) {
+  const int64_t n = (seq + kWKeys - 1) / kWKeys;
+  const int64_t steps = (n + kMaxRecords - 1) / kMaxRecords;
+  return {int(steps), int((n + steps - 1) / steps)};
+}
+
+template <int G>
+void launch_attn_decode_mfma(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* part,
+                             int nkv, int seq, float c, const WavePlan& p, const QNorm& qn, hipStream_t s) {
+  attn_decode_mfma<G><<<dim3(unsigned(p.records), unsigned(nkv)), dim3(64), 0, s>>>(
+      q, k, v, o, part, seq, c, p.steps, qn.w, qn.cos, qn.sin, qn.eps);
+  if (p.records > 1) attn_decode_merge<G><<<dim3(unsigned(nkv), unsigned(G)), dim3(256), 0, s>>>(part, o, p.records);
 }
 
 // G: query rows per workgroup (the kv head's group / p.gsplit)
@@ -819,6 +1086,11 @@ PTB_EXPORT int ptb_gemv_silu_bf16(const void* gate_up, const void* w, const void
 
 PTB_EXPORT size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, int64_t seq) {
   if (nkv <= 0 || group <= 0 || seq <= 0 || seq > 0x7fffffff) return 0;
+  if (seq > kWaveMinSeq) {
+    const WavePlan w = wave_plan(seq);
+    if (w.records == 1) return 0;
+    return size_t(nkv * w.records * record_floats(group)) * sizeof(float);
+  }
   const DecodePlan p = decode_plan(seq, group);
   if (p.records == 1) return 0;
   return size_t(nkv * p.gsplit * p.records * record_floats(group / p.gsplit)) * sizeof(float);
@@ -843,6 +1115,18 @@ static int attn_decode_entry(const void* q, const void* k, const void* v, void* 
   auto op = static_cast<uint16_t*>(o);
   float* ws = need ? static_cast<float*>(workspace) : nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (seq > kWaveMinSeq) {
+    const WavePlan w = wave_plan(seq);
+    switch (group) {
+      case 1: launch_attn_decode_mfma<1>(qp, kp, vp, op, ws, int(nkv), int(seq), c, w, qn, s); break;
+      case 2: launch_attn_decode_mfma<2>(qp, kp, vp, op, ws, int(nkv), int(seq), c, w, qn, s); break;
+      case 3: launch_attn_decode_mfma<3>(qp, kp, vp, op, ws, int(nkv), int(seq), c, w, qn, s); break;
+      case 4: launch_attn_decode_mfma<4>(qp, kp, vp, op, ws, int(nkv), int(seq), c, w, qn, s); break;
+      case 6: launch_attn_decode_mfma<6>(qp, kp, vp, op, ws, int(nkv), int(seq), c, w, qn, s); break;
+      default: launch_attn_decode_mfma<8>(qp, kp, vp, op, ws, int(nkv), int(seq), c, w, qn, s); break;
+    }
+    return launch_status();
+  }
   const DecodePlan p = decode_plan(seq, group);
   if (nkv * p.gsplit > 65535) return PTB_ERR_GRID;
   switch (group / p.gsplit) {

@@ -97,13 +97,14 @@ def test_attention_decode_ragged(nkv, g, s):
 
 @pytest.mark.parametrize("nkv,g,s", [(2, 1, 20000), (1, 8, 20000), (1, 4, 16384), (2, 8, 64), (5, 3, 256),
                                      (3, 8, 100), (3, 8, 250), (257, 1, 300), (2, 8, 9000), (2, 6, 3000),
-                                     (300, 8, 40)])
+                                     (300, 8, 40), (4, 2, 257), (1, 2, 40000)])
 def test_attention_decode_range_plans(nkv, g, s):
-    """Ranges of two 64-key steps (313 chunks, more than the 256 ranges a head may have) with 1 and
-    8 rows a workgroup, exactly 256 one-chunk ranges, one chunk in one pass, four teams in one pass
-    (G = 3), one row a workgroup in one pass with two and four teams (G = 8), many kv heads, all 8
-    rows in one workgroup past 8192 keys, G = 6 halved to 3 rows a workgroup (thirds would go below
-    two rows), and 2400 row workgroups (300 heads x 8)."""
+    """Caches past 256 keys (the matrix-core form, 32-key steps): three steps a range (20000 keys,
+    209 ranges: a pair of steps then a last one), two steps a range (9000 keys; 16384 over exactly
+    256 ranges), one step a range (300 and 3000 keys), five steps a range (40000), and 257 keys, whose
+    last range holds one key; caches of at most 256 keys (one pass of the VALU form): one chunk, four teams
+    (G = 3), one row a workgroup with two and four teams (G = 8), and 2400 row workgroups (300 heads
+    x 8); G = 1, 2, 3, 4, 6 and 8."""
     q, k, v = randn((nkv, g, 128), 20), randn((nkv, s, 128), 21), randn((nkv, s, 128), 22)
     got = ops.attention_decode(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
     assert_close(got, oracle.attention_decode(q, k, v), RTOL, 2e-2, f"decode plan {nkv}x{g}x{s}")
