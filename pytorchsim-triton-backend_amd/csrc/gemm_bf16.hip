@@ -575,11 +575,19 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
             *reinterpret_cast<u32x2*>(stage + fr * kPitch + (jj * 32 + 8 * g + 4 * h) * 2) =
                 u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
+      // every staged row of the block read back before the first conversion: the reads' latencies
+      // overlap instead of adding up pair by pair
+      using Staged = std::conditional_t<kF32Stage, f32x4v, u32x2>;
+      Staged sv[32 / RPI];
+#pragma unroll
+      for (int t = 0; t < 32 / RPI; ++t)
+        sv[t] = *reinterpret_cast<const Staged*>(stage + (t * RPI + rl) * kPitch + c4 * 4 * kEl);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int t = 0; t < 32 / RPI; ++t) {
         u32x2 packed;
         if constexpr (kF32Stage) {
-          f32x4v v = *reinterpret_cast<const f32x4v*>(stage + (t * RPI + rl) * kPitch + c4 * 16);
+          f32x4v v = sv[t];
           if constexpr (RESID) {
             v[0] += bf16_lo(rr[t][0]);
             v[1] += bf16_hi(rr[t][0]);
@@ -588,7 +596,7 @@ __global__ __launch_bounds__(kThreads, (WM * WN >= 12 ? 1 : 2)) void gemm_bf16_k
           }
           packed = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         } else {
-          packed = *reinterpret_cast<const u32x2*>(stage + (t * RPI + rl) * kPitch + c4 * 8);
+          packed = sv[t];
         }
         __builtin_amdgcn_raw_buffer_store_b64(packed, rsrc_c, voff[t], 0, 0);
       }

@@ -286,11 +286,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         *reinterpret_cast<u32x2*>(stage + fr * kPitch + (j * 32 + 8 * g + 4 * h) * 2) =
             u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
       }
+    // every staged row of the block read back before the first store: the reads' latencies overlap
+    u32x2 v[32 / RPI];
+#pragma unroll
+    for (int t = 0; t < 32 / RPI; ++t) v[t] = *reinterpret_cast<const u32x2*>(stage + (t * RPI + rl) * kPitch + c4 * 8);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 32 / RPI; ++t) {
-      const u32x2 v = *reinterpret_cast<const u32x2*>(stage + (t * RPI + rl) * kPitch + c4 * 8);
       const uint32_t off = gcol < N ? (uint32_t(r0 + t * RPI) * uint32_t(N) + uint32_t(gcol)) * 2u : 0x80000000u;
-      __builtin_amdgcn_raw_buffer_store_b64(v, rsrc_c, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(v[t], rsrc_c, off, 0, 0);
     }
   }
 }
