@@ -1165,7 +1165,7 @@ PTB_EXPORT int ptb_attn_decode_qnorm_rope_bf16(const void* q, const void* qnorm_
 // looked up once per device (hipGetSymbolAddress, with that device current) and kept.  Every call on a
 // GPU shares that GPU's array, so calls that overlap on one GPU race; nothing in it has to start at
 // zero (each record is written before the merge pass reads it).
-constexpr size_t kScratchBytes = size_t(16) << 20;   // 16 MiB: 8 kv heads x group 8 to 131072 keys
+constexpr size_t kScratchBytes = size_t(16) << 20;   // 16 MiB: 8 kv heads x group 8 at any cache length (at most 256 records a head)
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
