@@ -22,6 +22,7 @@
 //           workgroup per row group that writes o itself; a longer one leaves an (acc, m, l) record
 //           per range in the workspace.  Short caches give each query row its own workgroups.
 //   pass 2: workgroup (row group, query row): o = sum acc_r 2^(m_r-M) / sum l_r 2^(m_r-M), M = max m_r.
+#include <algorithm>
 #include <cmath>
 
 #include <mutex>
@@ -1011,17 +1012,21 @@ void launch_partial(const uint16_t* q, const uint16_t* k, const uint16_t* v, uin
       q, k, v, o, part, seq, c, p.steps, p.gsplit, qn.w, qn.cos, qn.sin, qn.eps);
 }
 
-// The matrix-core form's cut of a kv head: `records` ranges of `steps` 32-key steps each, at most
-// kMaxRecords ranges (the merge pass's limit).  It serves caches of more than kWaveMinSeq keys: on
-// MI355X (8 kv heads, graph replay) 512 keys 6.98 -> 6.66 us, 4096 keys 11.46 -> 10.63 us, 32768
-// keys 38.7 -> 32.4 us against the VALU form, and G = 8 at 4096 keys 15.2 -> 11.9 us.
+// The matrix-core form's cut of a kv head: `records` ranges of `steps` 32-key steps each (n steps in
+// all): ceil(n / 48) steps a range below 256 steps, ceil(n / 64) from there, so a head has at most
+// 64 ranges (the merge pass takes up to kMaxRecords).  Measured on MI355X (8 kv heads, graph
+// replay), against one step a range: 4096 keys 10.63 -> 9.70 us, 8192 keys 16.0 -> 12.4 us, 16384
+// keys 20.7 -> 18.6 us, G = 8 at 4096 keys 11.9 -> 10.2 us (fewer waves each stream more steps
+// through the two stages, and the merge has fewer records).  Against the VALU form, at one step a
+// range: 512 keys 6.98 -> 6.66 us, 4096 keys 11.46 -> 10.63 us, G = 8 at 4096 keys 15.2 -> 11.9 us.
+// It serves caches of more than kWaveMinSeq keys.
 constexpr int64_t kWaveMinSeq = 256;
 struct WavePlan {
   int steps, records;
 };
 WavePlan wave_plan(int64_t seq) {
   const int64_t n = (seq + kWKeys - 1) / kWKeys;
-  const int64_t steps = (n + kMaxRecords - 1) / kMaxRecords;
+  const int64_t steps = n < 256 ? (n + 47) / 48 : (n + 63) / 64;
   return {int(steps), int((n + steps - 1) / steps)};
 }
 
@@ -1165,7 +1170,7 @@ PTB_EXPORT int ptb_attn_decode_qnorm_rope_bf16(const void* q, const void* qnorm_
 // looked up once per device (hipGetSymbolAddress, with that device current) and kept.  Every call on a
 // GPU shares that GPU's array, so calls that overlap on one GPU race; nothing in it has to start at
 // zero (each record is written before the merge pass reads it).
-constexpr size_t kScratchBytes = size_t(16) << 20;   // 16 MiB: 8 kv heads x group 8 at any cache length (at most 256 records a head)
+constexpr size_t kScratchBytes = size_t(16) << 20;   // 16 MiB: the records of up to 62 kv heads of 8 query rows at any cache length (at most 64 a head)
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {

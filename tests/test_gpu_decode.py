@@ -99,12 +99,12 @@ def test_attention_decode_ragged(nkv, g, s):
                                      (3, 8, 100), (3, 8, 250), (257, 1, 300), (2, 8, 9000), (2, 6, 3000),
                                      (300, 8, 40), (4, 2, 257), (1, 2, 40000)])
 def test_attention_decode_range_plans(nkv, g, s):
-    """Caches past 256 keys (the matrix-core form, 32-key steps): three steps a range (20000 keys,
-    209 ranges: a pair of steps then a last one), two steps a range (9000 keys; 16384 over exactly
-    256 ranges), one step a range (300 and 3000 keys), five steps a range (40000), and 257 keys, whose
-    last range holds one key; caches of at most 256 keys (one pass of the VALU form): one chunk, four teams
-    (G = 3), one row a workgroup with two and four teams (G = 8), and 2400 row workgroups (300 heads
-    x 8); G = 1, 2, 3, 4, 6 and 8."""
+    """Caches past 256 keys (the matrix-core form, 32-key steps, ceil(n/48) steps a range below 256
+    steps, ceil(n/64) from there): ten steps a range (20000 keys: pairs of steps, the last range
+    ending in a step past S), eight (16384), five (9000: pairs, then a single step), twenty (40000),
+    two (3000), one (300, and 257 keys, whose last range holds one key); caches of at most 256 keys
+    (one pass of the VALU form): one chunk, four teams (G = 3), one row a workgroup with two and
+    four teams (G = 8), and 2400 row workgroups (300 heads x 8); G = 1, 2, 3, 4, 6 and 8."""
     q, k, v = randn((nkv, g, 128), 20), randn((nkv, s, 128), 21), randn((nkv, s, 128), 22)
     got = ops.attention_decode(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
     assert_close(got, oracle.attention_decode(q, k, v), RTOL, 2e-2, f"decode plan {nkv}x{g}x{s}")
@@ -134,11 +134,11 @@ def test_attention_decode_fused_qnorm_rope(nkv, g, s):
 def test_attention_decode_workspace_reuse():
     """One caller workspace serves consecutive calls of different shapes (each call's records
     replace the last call's)."""
-    need = max(_lib.load().ptb_attn_decode_workspace_bytes(8, 4, 4096),
-               _lib.load().ptb_attn_decode_workspace_bytes(3, 2, 1000))
+    shapes = ((8, 4, 4096, 30), (3, 2, 1000, 33), (8, 4, 4096, 36), (8, 4, 1500, 39))
+    need = max(_lib.load().ptb_attn_decode_workspace_bytes(nkv, g, s) for nkv, g, s, _ in shapes)
     assert need > 0
     ws = torch.empty(need, dtype=torch.uint8, device=DEV)
-    for nkv, g, s, seed in ((8, 4, 4096, 30), (3, 2, 1000, 33), (8, 4, 4096, 36), (8, 4, 1500, 39)):
+    for nkv, g, s, seed in shapes:
         q, k, v = randn((nkv, g, 128), seed), randn((nkv, s, 128), seed + 1), randn((nkv, s, 128), seed + 2)
         got = ops.attention_decode(q.to(DEV), k.to(DEV), v.to(DEV), workspace=ws).cpu()
         assert_close(got, oracle.attention_decode(q, k, v), RTOL, 2e-2, f"decode reuse {nkv}x{g}x{s}")
