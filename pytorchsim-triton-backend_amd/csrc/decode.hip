@@ -1090,7 +1090,7 @@ PTB_EXPORT int ptb_gemv_silu_bf16(const void* gate_up, const void* w, const void
 }
 
 PTB_EXPORT size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, int64_t seq) {
-  if (nkv <= 0 || group <= 0 || seq <= 0 || seq > 0x7fffffff) return 0;
+  if (nkv <= 0 || group <= 0 || seq <= 0 || seq >= (int64_t(1) << 30)) return 0;
   if (seq > kWaveMinSeq) {
     const WavePlan w = wave_plan(seq);
     if (w.records == 1) return 0;
@@ -1111,7 +1111,9 @@ static int attn_decode_entry(const void* q, const void* k, const void* v, void* 
   if (nkv == 0) return PTB_OK;
   if (!q || !k || !v || !o) return PTB_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return PTB_ERR_ALIGN;
-  if (nkv > 65535 || seq > 0x7fffffff || nkv * seq * kD >= (int64_t(1) << 40)) return PTB_ERR_GRID;
+  // caches below 2^30 keys (256 GB of K per kv head): the kernels' key indices, ranges * steps * 32
+  // included, stay within 32 bits
+  if (nkv > 65535 || seq >= (int64_t(1) << 30) || nkv * seq * kD >= (int64_t(1) << 40)) return PTB_ERR_GRID;
   const size_t need = ptb_attn_decode_workspace_bytes(nkv, group, seq);
   if (need && (!workspace || workspace_bytes < need)) return PTB_ERR_WORKSPACE;
   if (need && !aligned16(workspace)) return PTB_ERR_ALIGN;

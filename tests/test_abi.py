@@ -105,6 +105,11 @@ def test_32bit_buffer_offset_limits_refused(lib):
     assert lib.ptb_gemm_fp8_scaled(P16, P16, P16, P16, P16, 256, 16, 1 << 24, None) == _lib.PTB_ERR_UNSUPPORTED
     # attention: one kv head's K at 4 GiB (2^24 keys x 256 bytes)
     assert lib.ptb_flash_attn_fwd_bf16(P16, P16, P16, P16, 1, 1, 1, 1 << 24, 128, 0.1, 1, None) == _lib.PTB_ERR_GRID
+    # decode attention: caches of 2^30 keys or more (the kernels' 32-bit key indices); no workspace
+    # is quoted for them
+    assert lib.ptb_attn_decode_workspace_bytes(1, 4, 1 << 30) == 0
+    assert lib.ptb_attn_decode_bf16(P16, P16, P16, P16, 1, 4, 1 << 30, 128, 0.1, P16, 1 << 20, None) == _lib.PTB_ERR_GRID
+    assert lib.ptb_attn_decode_workspace_bytes(1, 4, (1 << 30) - 1) > 0
 
 
 def test_fused_attention_refusals(lib):
