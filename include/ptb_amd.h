@@ -267,7 +267,8 @@ int ptb_gemv_silu_bf16(const void* gate_up, const void* w, const void* res_a, co
  * kv heads; query head g of kv head h is row h*group + g).  Full softmax over the seq cached keys,
  * P rounded to bf16 before P.V, fp32 row sums.  group in {1,2,3,4,6,8}; q, k, v 16-byte aligned.
  * Workspace: ptb_attn_decode_workspace_bytes(nkv, group, seq) bytes, 16-byte aligned; 0 bytes (and
- * workspace may be NULL) when seq <= 256, which is a single launch.
+ * workspace may be NULL) when seq <= 256, which is a single launch.  seq below 2^30 (else
+ * PTB_ERR_GRID).
  * Replaces: attention_decode_<HQ>x8x<S>_bf16/00__decode_kernel/_decode_kernel_triton.py:4-29 (and
  *           qwen3_8b_layer_decode_1x<S>_bf16/03__decode_kernel). */
 size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, int64_t seq);
