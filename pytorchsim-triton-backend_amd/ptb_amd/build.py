@@ -24,8 +24,9 @@ LIB = LIB_DIR / "libptb_amd.so"
 BUILD_DIR = REPO / "_build" / "ptb_amd"
 
 ARCH = "gfx950"
-# -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32 (see DESIGN notes on the
-# target); the host pass warns that it does not know the feature, which is harmless.
+# -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32, some forms of which have
+# given wrong results now and then on the MI355X boxes this was built for, with no error; the host
+# pass warns that it does not know the feature, which is harmless.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
