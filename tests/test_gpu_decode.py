@@ -97,11 +97,12 @@ def test_attention_decode_ragged(nkv, g, s):
 
 @pytest.mark.parametrize("nkv,g,s", [(2, 1, 20000), (1, 8, 20000), (1, 4, 16384), (2, 8, 64), (5, 3, 256),
                                      (3, 8, 100), (3, 8, 250), (257, 1, 300), (2, 8, 9000), (2, 6, 3000),
-                                     (300, 8, 40), (4, 2, 257), (1, 2, 40000)])
+                                     (300, 8, 40), (4, 2, 257), (1, 2, 40000), (1, 8, 131072)])
 def test_attention_decode_range_plans(nkv, g, s):
     """Caches past 256 keys (the matrix-core form, 32-key steps, ceil(n/48) steps a range below 256
     steps, ceil(n/64) from there): ten steps a range (20000 keys: pairs of steps, the last range
     ending in a step past S), eight (16384), five (9000: pairs, then a single step), twenty (40000),
+    sixty-four (131072 keys, 64 ranges),
     two (3000), one (300, and 257 keys, whose last range holds one key); caches of at most 256 keys
     (one pass of the VALU form): one chunk, four teams (G = 3), one row a workgroup with two and
     four teams (G = 8), and 2400 row workgroups (300 heads x 8); G = 1, 2, 3, 4, 6 and 8."""
