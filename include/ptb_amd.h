@@ -263,6 +263,21 @@ int ptb_gemv_rmsnorm_bf16(const void* x, const void* add, const float* ss, const
 int ptb_gemv_silu_bf16(const void* gate_up, const void* w, const void* res_a, const void* res_b, void* y,
                        int64_t k, int64_t n, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The decode layer's gate/up and down projections with the gate/up finish pass folded into the down
+ * projection's prologue (one launch fewer).  ptb_gemv_rmsnorm_parts_bf16 is ptb_gemv_rmsnorm_bf16's
+ * partial pass alone: its fp32 partials stay in `parts` (ptb_gemv_workspace_bytes(k, n) bytes, 4-byte
+ * aligned) and nothing is written to a y.  ptb_gemv_silu_parts_bf16 is ptb_gemv_silu_bf16 whose
+ * gate_up vector is formed from such partials (gate_up_parts written by ptb_gemv_rmsnorm_parts_bf16
+ * with k = gate_up_k and n = 2 * k) with the finish pass's own sums and rounding, so its y is bit for
+ * bit that of ptb_gemv_rmsnorm_bf16 followed by ptb_gemv_silu_bf16; `workspace` is its own partials'
+ * (ptb_gemv_workspace_bytes(k, n) bytes) and must not overlap gate_up_parts.
+ * Replaces: decode 06_..._5gopcdje_triton.py:17-57 and 07_..._3d4ocw7y_triton.py:17-56 together. */
+int ptb_gemv_rmsnorm_parts_bf16(const void* x, const void* add, const float* ss, const void* g, float eps,
+                                const void* w, float* parts, int64_t k, int64_t n, size_t parts_bytes, void* stream);
+int ptb_gemv_silu_parts_bf16(const float* gate_up_parts, int64_t gate_up_k, const void* w, const void* res_a,
+                             const void* res_b, void* y, int64_t k, int64_t n, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* Decode attention for one query token: q, o [nkv, group, 128]; k, v [nkv, seq, 128] (nkv = batch *
  * kv heads; query head g of kv head h is row h*group + g).  Full softmax over the seq cached keys,
  * P rounded to bf16 before P.V, fp32 row sums.  group in {1,2,3,4,6,8}; q, k, v 16-byte aligned.

@@ -65,7 +65,10 @@ __global__ __launch_bounds__(1024) void sumsq_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------------------------
 // GEMV
 
-enum GemvMode { kPlain = 0, kRms = 1, kSilu = 2 };
+// kSiluParts: kSilu whose gate_up vector is still the fp32 partials [splits, 2K] of the GEMV that
+// produces it (that GEMV's finish pass is done in this prologue, in the finish's own order and
+// rounding, so the result is bit-identical to finishing it first).
+enum GemvMode { kPlain = 0, kRms = 1, kSilu = 2, kSiluParts = 3 };
 
 constexpr int kColBlock = 512;   // columns per workgroup: 64 lanes x 8
 constexpr int kMaxKb = 512;      // rows per K slice (LDS prologue buffer)
@@ -114,15 +117,38 @@ __device__ __forceinline__ u32x4 ld_stream(const uint16_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// bf16(sum of part[.][n]) exactly as gemv_finish forms it (no residual): split group sg (the splits
+// sp = sg mod 16) summed from 0 in split order, then the 16 groups in order from 0, one rounding.
+// Sixteen loads are in flight a round.
+__device__ __forceinline__ float finish_value(const float* __restrict__ part, int splits, int N, int n) {
+  float acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+  for (int sp0 = 0; sp0 < splits; sp0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = part[int64_t(min(sp0 + j, splits - 1)) * N + n];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (sp0 + j < splits) acc[j] += v[j];
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s += acc[j];
+  return bf16_to_f32(f32_to_bf16(s));
+}
+
 template <int MODE>
 __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ add,
                                                              const float* __restrict__ ss,
                                                              const uint16_t* __restrict__ g, float eps,
                                                              const uint16_t* __restrict__ W,
-                                                             float* __restrict__ part, int K, int N, int kb) {
+                                                             float* __restrict__ part, int K, int N, int kb,
+                                                             const float* __restrict__ xparts, int xsplits) {
   __shared__ float xs[kMaxKb];
   __shared__ float red[4][kColBlock];
+  __shared__ float xu[MODE == kSiluParts ? kMaxKb : 1];   // the up half, kSiluParts
   const int n0 = blockIdx.x * kColBlock;
   const int split = blockIdx.y;
   const int k0 = split * kb;
@@ -162,7 +188,22 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial(const uint16_t* __r
     }
     r = 1.f / sqrtf(sv / float(K) + eps);
   }
-  for (int i = threadIdx.x; i < rows; i += kGemvThreads) xs[i] = prologue<MODE>(x, add, g, r, k0 + i, K);
+  if constexpr (MODE == kSiluParts) {
+    // gate (t < rows) and up (t >= rows) values of the slice, each finished from the partials
+    for (int t = threadIdx.x; t < 2 * rows; t += kGemvThreads) {
+      const bool up = t >= rows;
+      const float v = finish_value(xparts, xsplits, 2 * K, up ? K + k0 + (t - rows) : k0 + t);
+      if (up) xu[t - rows] = v;
+      else xs[t] = v;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < rows; i += kGemvThreads) {
+      const float gv = xs[i], u = xu[i];
+      xs[i] = (gv / (__builtin_amdgcn_exp2f(-gv * 1.4426950408889634f) + 1.f)) * u;
+    }
+  } else {
+    for (int i = threadIdx.x; i < rows; i += kGemvThreads) xs[i] = prologue<MODE>(x, add, g, r, k0 + i, K);
+  }
   __syncthreads();
 
   float acc[8];
@@ -238,13 +279,16 @@ __global__ __launch_bounds__(256) void gemv_finish(const float* __restrict__ par
   }
 }
 
+// y == nullptr: the partial pass only, its partials left in ws for a consumer that finishes them
+// (kSiluParts).  xparts / xsplits: kSiluParts' input partials.
 template <int MODE>
 int launch_gemv(const void* x, const void* add, const float* ss, const void* g, float eps, const void* w,
                 const void* r1, const void* r2, void* y, int64_t k, int64_t n, void* ws, size_t ws_bytes,
-                void* stream) {
+                void* stream, const float* xparts = nullptr, int xsplits = 0) {
   if (k < 0 || n < 0) return PTB_ERR_SHAPE;
   if (n == 0) return PTB_OK;
-  if (!x || !w || !y || (MODE == kRms && !g)) return PTB_ERR_NULL;
+  if ((MODE == kSiluParts ? !xparts : !x) || !w || (MODE == kRms && !g)) return PTB_ERR_NULL;
+  if (!y && MODE != kRms) return PTB_ERR_NULL;
   if (MODE == kRms && !ss && (!aligned16(x) || (add && !aligned16(add)))) return PTB_ERR_ALIGN;
   if (k == 0) return PTB_ERR_UNSUPPORTED;
   if (k > 0x7fffffff || n > 0x7fffffff || k * n >= (int64_t(1) << 40)) return PTB_ERR_SHAPE;
@@ -259,7 +303,8 @@ int launch_gemv(const void* x, const void* add, const float* ss, const void* g, 
   const dim3 grid1(unsigned((n + kColBlock - 1) / kColBlock), unsigned(sp.splits));
   gemv_partial<MODE><<<grid1, dim3(kGemvThreads), 0, s>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(add), ss, static_cast<const uint16_t*>(g), eps,
-      static_cast<const uint16_t*>(w), part, int(k), int(n), sp.kb);
+      static_cast<const uint16_t*>(w), part, int(k), int(n), sp.kb, xparts, xsplits);
+  if (!y) return launch_status();
   gemv_finish<<<dim3(unsigned((n + kFinCols - 1) / kFinCols)), dim3(256), 0, s>>>(
       part, sp.splits, int(n), static_cast<const uint16_t*>(r1), static_cast<const uint16_t*>(r2),
       static_cast<uint16_t*>(y));
@@ -1087,6 +1132,25 @@ PTB_EXPORT int ptb_gemv_silu_bf16(const void* gate_up, const void* w, const void
   if (res_b && !res_a) return PTB_ERR_NULL;
   return launch_gemv<kSilu>(gate_up, nullptr, nullptr, nullptr, 0.f, w, res_a, res_b, y, k, n, workspace,
                             workspace_bytes, stream);
+}
+
+PTB_EXPORT int ptb_gemv_rmsnorm_parts_bf16(const void* x, const void* add, const float* ss, const void* g, float eps,
+                                           const void* w, float* parts, int64_t k, int64_t n, size_t parts_bytes,
+                                           void* stream) {
+  if (!parts) return PTB_ERR_NULL;
+  return launch_gemv<kRms>(x, add, ss, g, eps, w, nullptr, nullptr, nullptr, k, n, parts, parts_bytes, stream);
+}
+
+PTB_EXPORT int ptb_gemv_silu_parts_bf16(const float* gate_up_parts, int64_t gate_up_k, const void* w, const void* res_a,
+                                        const void* res_b, void* y, int64_t k, int64_t n, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  if (res_b && !res_a) return PTB_ERR_NULL;
+  if (gate_up_k <= 0 || gate_up_k > 0x7fffffff || k <= 0 || 2 * k > 0x7fffffff) return PTB_ERR_SHAPE;
+  if (gate_up_parts && (reinterpret_cast<uintptr_t>(gate_up_parts) & 3u)) return PTB_ERR_ALIGN;
+  // the producing GEMV's split of its K = gate_up_k rows, N = 2k columns
+  const GemvSplit gs = gemv_split(gate_up_k, 2 * k);
+  return launch_gemv<kSiluParts>(nullptr, nullptr, nullptr, nullptr, 0.f, w, res_a, res_b, y, k, n, workspace,
+                                 workspace_bytes, stream, gate_up_parts, gs.splits);
 }
 
 PTB_EXPORT size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, int64_t seq) {

@@ -129,6 +129,8 @@ SIGNATURES = {
     "ptb_gemv_bf16": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
     "ptb_gemv_rmsnorm_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_f32, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
     "ptb_gemv_silu_bf16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
+    "ptb_gemv_rmsnorm_parts_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_f32, _vp, _vp, _c_i64, _c_i64, _c_size, _vp]),
+    "ptb_gemv_silu_parts_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_size, _vp]),
     "ptb_fill_zero": (_c_int, [_vp, _c_i64, _vp]),
     "ptb_cast_i64_i32": (_c_int, [_vp, _vp, _c_i64, _vp]),
     "ptb_cumsum_int": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_i64, _vp]),

@@ -393,6 +393,55 @@ def gemv_rmsnorm(x: torch.Tensor, ss: torch.Tensor, g: torch.Tensor, w: torch.Te
     return y
 
 
+def gemv_rmsnorm_parts(x: torch.Tensor, ss: torch.Tensor | None, g: torch.Tensor, w: torch.Tensor,
+                       add: torch.Tensor | None = None, eps: float = 1e-6, parts=None) -> torch.Tensor:
+    """gemv_rmsnorm's partial pass alone: returns its fp32 partials (a uint8 tensor of
+    ptb_gemv_workspace_bytes(K, N) bytes, `parts` if given), to be finished by :func:`gemv_silu_parts`."""
+    _need(x, "x", BF16)
+    if ss is not None:
+        _need(ss, "ss", F32)
+    _need(g, "g", BF16)
+    _need(w, "w", BF16, 2)
+    if add is not None:
+        _need(add, "add", BF16)
+        if add.numel() != x.numel():
+            raise ValueError("add must match x")
+    k, n = w.shape
+    if x.numel() != k or g.numel() != k:
+        raise ValueError(f"x and g must hold {k} values")
+    need = _lib.load().ptb_gemv_workspace_bytes(k, n)
+    if parts is None:
+        parts = torch.empty(max(need, 4), dtype=torch.uint8, device=x.device)
+    _lib.call("ptb_gemv_rmsnorm_parts_bf16", x.data_ptr(), add.data_ptr() if add is not None else None,
+              ss.data_ptr() if ss is not None else None, g.data_ptr(), float(eps), w.data_ptr(), parts.data_ptr(),
+              k, n, parts.numel() * parts.element_size(), _stream(x))
+    return parts
+
+
+def gemv_silu_parts(gate_up_parts: torch.Tensor, gate_up_k: int, w: torch.Tensor, res_a: torch.Tensor | None = None,
+                    res_b: torch.Tensor | None = None, out=None, workspace=None) -> torch.Tensor:
+    """:func:`gemv_silu` over the gate|up vector that :func:`gemv_rmsnorm_parts` left as partials (its
+    W was [gate_up_k, 2K]); bit for bit gemv_rmsnorm followed by gemv_silu, one launch fewer."""
+    if not isinstance(gate_up_parts, torch.Tensor) or gate_up_parts.device.type != "cuda":
+        raise ValueError("gate_up_parts must be a GPU tensor")
+    for t, name in ((res_a, "res_a"), (res_b, "res_b")):
+        if t is not None:
+            _need(t, name, BF16)
+    if res_b is not None and res_a is None:
+        raise ValueError("res_b needs res_a")
+    _need(w, "w", BF16, 2)
+    k, n, y, ws, wsb = _gemv_args(w.shape[0], w, out, gate_up_parts, workspace)
+    if gate_up_parts.numel() * gate_up_parts.element_size() < _lib.load().ptb_gemv_workspace_bytes(gate_up_k, 2 * k):
+        raise ValueError("gate_up_parts is smaller than the producing GEMV's partials")
+    for t, name in ((res_a, "res_a"), (res_b, "res_b")):
+        if t is not None and t.numel() != n:
+            raise ValueError(f"{name} must have {n} elements")
+    _lib.call("ptb_gemv_silu_parts_bf16", gate_up_parts.data_ptr(), int(gate_up_k), w.data_ptr(),
+              res_a.data_ptr() if res_a is not None else None, res_b.data_ptr() if res_b is not None else None,
+              y.data_ptr(), k, n, ws.data_ptr(), wsb, _stream(gate_up_parts))
+    return y
+
+
 def gemv_silu(gate_up: torch.Tensor, w: torch.Tensor, res_a: torch.Tensor | None = None,
               res_b: torch.Tensor | None = None, out=None, workspace=None) -> torch.Tensor:
     """y = bf16( (silu(g) * u) @ W + (res_a + res_b) ), gate_up = g | u (2K values)."""

@@ -160,6 +160,8 @@ class Qwen3DecodeLayer:
       K06 gu = ((x + a)*r2*w_post) Wgu       K07 y = (silu(g)*u) Wd + (x + a)
 
     (The bundle's decode layer reads the cache as given; it computes no k/v for the new token.)
+    Issued as 9 kernels: each GEMV is a partial pass plus a finish pass, except that K06's finish
+    runs inside K07's prologue, and attention is a partial pass plus a merge.
     Weights as from :func:`random_weights`; the GEMV and attention workspaces are allocated once."""
 
     def __init__(self, weights: dict, cfg: Qwen3Config = QWEN3_8B):
@@ -177,6 +179,7 @@ class Qwen3DecodeLayer:
                           lib.ptb_gemv_workspace_bytes(c.hidden, 2 * c.intermediate),
                           lib.ptb_gemv_workspace_bytes(c.intermediate, c.hidden))
             attn_ws = lib.ptb_attn_decode_workspace_bytes(c.kv_heads, c.heads // c.kv_heads, seq)
+            gu_parts = lib.ptb_gemv_workspace_bytes(c.hidden, 2 * c.intermediate)
 
             def e(*shape, dtype=BF16):
                 return torch.empty(*shape, dtype=dtype, device=device)
@@ -184,8 +187,9 @@ class Qwen3DecodeLayer:
             self._bufs[key] = {
                 "ss": e(1, dtype=torch.float32), "q": e(c.heads * c.head_dim),
                 "o": e(c.kv_heads, c.heads // c.kv_heads, c.head_dim), "a": e(c.hidden),
-                "ss2": e(1, dtype=torch.float32), "gu": e(2 * c.intermediate), "y": e(c.hidden),
+                "ss2": e(1, dtype=torch.float32), "y": e(c.hidden),
                 "ws": e(max(gemv_ws, 4), dtype=torch.uint8), "attn_ws": e(max(attn_ws, 4), dtype=torch.uint8),
+                "gu_parts": e(max(gu_parts, 4), dtype=torch.uint8),
             }
         return self._bufs[key]
 
@@ -203,9 +207,9 @@ class Qwen3DecodeLayer:
                              1.0 / math.sqrt(c.head_dim), out=b["o"], workspace=b["attn_ws"],
                              qnorm=(w["w_qn"], cos, sin, c.eps))                                 # K02 + K03
         ops.gemv(b["o"].view(-1), w["wo"], out=b["a"], workspace=b["ws"])                      # K04
-        ops.gemv_rmsnorm(x, None, w["w_post"], w["wgu"], add=b["a"], eps=c.eps, out=b["gu"],
-                         workspace=b["ws"])                                                    # K05 + K06
-        ops.gemv_silu(b["gu"], w["wd"], x, b["a"], out=y, workspace=b["ws"])                   # K07
+        # K05 + K06's partial pass; K06's finish runs in K07's prologue (the same sums and rounding)
+        ops.gemv_rmsnorm_parts(x, None, w["w_post"], w["wgu"], add=b["a"], eps=c.eps, parts=b["gu_parts"])
+        ops.gemv_silu_parts(b["gu_parts"], c.hidden, w["wd"], x, b["a"], out=y, workspace=b["ws"])  # K06 + K07
         return y
 
     __call__ = forward

@@ -112,6 +112,18 @@ def test_32bit_buffer_offset_limits_refused(lib):
     assert lib.ptb_attn_decode_workspace_bytes(1, 4, (1 << 30) - 1) > 0
 
 
+def test_gemv_parts_refusals(lib):
+    """The split gate/up + down pair refuses missing partials, a residual pair without its first
+    half and a producer K that cannot be, before any launch."""
+    assert lib.ptb_gemv_rmsnorm_parts_bf16(P16, None, P16, P16, 1e-6, P16, None, 64, 64, 1 << 20, None) == \
+        _lib.PTB_ERR_NULL
+    assert lib.ptb_gemv_silu_parts_bf16(None, 64, P16, None, None, P16, 64, 64, P16, 1 << 20, None) == _lib.PTB_ERR_NULL
+    assert lib.ptb_gemv_silu_parts_bf16(P16, 64, P16, None, P16, P16, 64, 64, P16, 1 << 20, None) == _lib.PTB_ERR_NULL
+    assert lib.ptb_gemv_silu_parts_bf16(P16, 0, P16, None, None, P16, 64, 64, P16, 1 << 20, None) == _lib.PTB_ERR_SHAPE
+    assert lib.ptb_gemv_silu_parts_bf16(P16, 64, P16, None, None, P16, 64, 12, P16, 1 << 20, None) == \
+        _lib.PTB_ERR_UNSUPPORTED   # n % 8 != 0
+
+
 def test_fused_attention_refusals(lib):
     # ld narrower than q|k|v; a missing q-norm weight; a row stride that breaks 16-byte rows
     assert lib.ptb_flash_attn_fwd_qkv_bf16(P16, 1000, P16, P16, P16, P16, 1e-6, P16, 1, 4, 2, 128, 128, 0.1, 1,

@@ -64,6 +64,26 @@ def test_gemv_silu_with_residual(k, n):
     close_scaled(got, oracle.gemv_silu(gu, w), f"gemv_silu no residual {k}x{n}")
 
 
+@pytest.mark.parametrize("gk,k,n", [(4096, 12288, 4096), (1000, 260, 264)])
+def test_gemv_silu_parts_is_the_two_launches(gk, k, n):
+    """The gate/up GEMV's partial pass, then the down GEMV finishing those partials in its prologue,
+    gives the bits of gemv_rmsnorm followed by gemv_silu (the decode layer's K06 + K07), with and
+    without the residuals."""
+    x, a = randn((gk,), 50), randn((gk,), 51)
+    g = randn((gk,), 52, std=0.02, mean=1.0)
+    wgu, wd = randn((gk, 2 * k), 53, std=0.02), randn((k, n), 54, std=0.02)
+    ra, rb = randn((n,), 55), randn((n,), 56)
+    xd, ad, gd, wgud, wdd, rad, rbd = (t.to(DEV) for t in (x, a, g, wgu, wd, ra, rb))
+    gu = ops.gemv_rmsnorm(xd, None, gd, wgud, add=ad, eps=1e-6)
+    parts = ops.gemv_rmsnorm_parts(xd, None, gd, wgud, add=ad, eps=1e-6)
+    for r1, r2 in ((rad, rbd), (None, None)):
+        want = ops.gemv_silu(gu, wdd, r1, r2).cpu()
+        got = ops.gemv_silu_parts(parts, gk, wdd, r1, r2).cpu()
+        assert bits_equal(got, want), f"gemv_silu_parts {gk}x{k}x{n} residual={r1 is not None}"
+    close_scaled(got, oracle.gemv_silu(oracle.gemv_rmsnorm(x, oracle.sumsq(x, a), g, wgu, add=a, eps=1e-6), w=wd),
+                 f"gemv_silu_parts vs oracle {gk}x{k}x{n}")
+
+
 def test_gemv_exact_small_integers():
     """Small-integer operands: every product and partial sum is exact in fp32, so the split-K order
     cannot matter and the result is bit-exact."""
