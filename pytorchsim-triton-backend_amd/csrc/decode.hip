@@ -15,13 +15,10 @@
 //   pass 1, more than 256 keys: one wave per (key range, kv head), 32-key steps through LDS, scores
 //           and P.V on v_mfma_f32_16x16x32_bf16 with the head's G query rows as the N side (K and V
 //           read once); an (acc, m, l) record per range (attn_decode_mfma below).
-//   pass 1, up to 256 keys: workgroup (key range, query rows of a kv head): teams of 256 threads each take a 64-key
-//           chunk per step (scores with 16 lanes per key, one 256-byte row, summed by DPP row
-//           moves; a running base-2 softmax; the next step's K and V in flight meanwhile) and meet
-//           in LDS.  A cache of at most four chunks (two for more than 3 rows a workgroup) is one
-//           workgroup per row group that writes o itself; a longer one leaves an (acc, m, l) record
-//           per range in the workspace.  Short caches give each query row its own workgroups.
-//   pass 2: workgroup (row group, query row): o = sum acc_r 2^(m_r-M) / sum l_r 2^(m_r-M), M = max m_r.
+//   up to 256 keys, one pass: a workgroup per query row, teams of 256 threads each taking one 64-key
+//           chunk (scores with 16 lanes per key, one 256-byte row, summed by DPP row moves; a
+//           base-2 softmax over the chunk), met in LDS; the workgroup writes o itself.
+//   pass 2 (more than one range): workgroup (kv head, query head): o = sum acc_r 2^(m_r-M) / sum l_r 2^(m_r-M), M = max m_r.
 #include <algorithm>
 #include <cmath>
 
@@ -441,40 +438,12 @@ constexpr int kChunk = 64;          // keys per team step
 constexpr int kTeam = 256;          // threads per 64-key chunk
 constexpr int kMaxRecords = 256;    // key ranges per kv head that the merge pass combines
 
-// The VALU form below serves caches of at most kWaveMinSeq (256) keys, which this plan covers in one
-// pass (records = 1) for every G; its range plans are the general case of the same cut.
-// How a kv head's work is cut: its G query rows go to `gsplit` workgroup rows of G / gsplit each,
-// and its keys to `records` workgroups holding `teams` teams of 256 threads, each team taking one
-// 64-key chunk per step for `steps` steps.  A cache that the teams of one workgroup cover in one
-// step is a single pass (records = 1, the teams merged in LDS): four teams (1024 threads, 128 VGPRs
-// a lane) for up to 3 query rows, two for more, which measured faster than two teams over two
-// steps.  Longer caches take one chunk per workgroup, up to kMaxRecords workgroups a head, more
-// steps beyond that.
-struct DecodePlan {
-  int gsplit;                 // workgroups sharing a kv head's query rows (G / gsplit rows each)
-  int teams, steps, records;
-};
-DecodePlan decode_plan(int64_t seq, int64_t group) {
+// The VALU form serves caches of at most kWaveMinSeq (256) keys in one pass: a workgroup per query
+// row, T teams of 256 threads taking one 64-key chunk each (T = 1, 2 or 4 for up to 1, 2 or 4
+// chunks; four teams are 1024 threads at 128 VGPRs a lane), merged in LDS.
+inline int small_teams(int64_t seq) {
   const int64_t chunks = (seq + kChunk - 1) / kChunk;
-  // Query rows per workgroup (measured on MI355X over 8 kv heads, G = 2..8): one for caches up to
-  // 1024 keys, where a workgroup's VALU work, not HBM, sets the time; two up to 8192 keys; all of
-  // them beyond, where re-reading K and V would cost HBM bandwidth.  The workgroups of one kv head
-  // read the same K and V, the second time mostly from L2 or the last-level cache.  G splits by
-  // factors of 2 and 3 (G = 3 and 6 reach one row).  A single pass of two steps measured slower
-  // than a second (merge) launch, so single passes are one step.
-  const int rows = seq <= 1024 ? 1 : seq <= 8192 ? 2 : 8;
-  int gsplit = 1;
-  for (;;) {
-    const int64_t g = group / gsplit;
-    if (g % 2 == 0 && g / 2 >= rows) gsplit *= 2;
-    else if (g % 3 == 0 && g / 3 >= rows) gsplit *= 3;
-    else break;
-  }
-  const int64_t g = group / gsplit;
-  const int most = g <= 3 ? 4 : 2;
-  if (chunks <= most) return {gsplit, chunks <= 1 ? 1 : chunks <= 2 ? 2 : 4, 1, 1};
-  const int64_t steps = (chunks + kMaxRecords - 1) / kMaxRecords;
-  return {gsplit, 1, int(steps), int((chunks + steps - 1) / steps)};
+  return chunks <= 1 ? 1 : chunks <= 2 ? 2 : 4;
 }
 
 // One record per (kv head, key range): acc[G][128], m[G], l[G], padded to 16 bytes.
@@ -568,32 +537,29 @@ __device__ __forceinline__ void qvec_values(const QVec& v, int qi, bool norm, fl
   }
 }
 
-// Workgroup (key range, kv head) of T teams.  Team t walks chunks (range*steps + s)*T + t: scores
-// t = (q.k) * scale*log2(e) with 16 lanes a key, a running base-2 softmax (m = running max, p =
-// 2^(t-m), l = l*2^(m_old-m) + sum of fp32 p) and acc = acc*2^(m_old-m) + sum bf16(p) * v, the next
-// step's K and V in flight meanwhile.  The teams then meet in LDS (weights 2^(m_t - M)); a head of
-// one range writes o = bf16(acc / l), otherwise the range's (acc, m, l) record goes to the workspace.
+// Workgroup (query row kvh of kv head kvh / group) of T teams, team t on keys 64t .. 64t+63: scores
+// t = (q.k) * scale*log2(e) with 16 lanes a key, a base-2 softmax over the chunk (m = max, p =
+// 2^(t-m), l = sum of fp32 p) and acc = sum bf16(p) * v; the teams then meet in LDS (weights
+// 2^(m_t - M)) and the workgroup writes o = bf16(acc / l).  G = 1 (one row a workgroup).
 template <int G, int T>
 __global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t* __restrict__ Q,
                                                                  const uint16_t* __restrict__ Kc,
                                                                  const uint16_t* __restrict__ Vc,
-                                                                 uint16_t* __restrict__ O, float* __restrict__ part,
-                                                                 int S, float c, int steps, int gsplit,
+                                                                 uint16_t* __restrict__ O, int S, float c, int group,
                                                                  const uint16_t* __restrict__ qw,
                                                                  const float* __restrict__ qcos,
                                                                  const float* __restrict__ qsin, float qeps) {
-  constexpr int kRec = int(record_floats(G));
   __shared__ float qs[G][kD];
   __shared__ float ts[T][G][kChunk];      // scores, then bf16-rounded p
   __shared__ float red[T][4][G][kD];
-  __shared__ float mrun[T][G], lrun[T][G], alpha[T][G], wt[T][G], mfin[G], lfin[G];
-  const int range = blockIdx.x, kvh = blockIdx.y, nrec = gridDim.x;
+  __shared__ float mrun[T][G], lrun[T][G], alpha[T][G], wt[T][G], lfin[G];
+  const int kvh = blockIdx.x;
   const int tid = threadIdx.x, team = tid / kTeam, ttid = tid % kTeam;
   const int lane = tid & 63, wave = ttid >> 6, d8 = lane & 15, kj = ttid >> 4;
   const uint16_t* q = Q + int64_t(kvh) * G * kD;                 // kvh: this workgroup's G query rows
-  const uint16_t* kp = Kc + int64_t(kvh / gsplit) * S * kD;      // of kv head kvh / gsplit
-  const uint16_t* vp = Vc + int64_t(kvh / gsplit) * S * kD;
-  const int first = range * steps * T + team;   // this team's chunk at step 0; + s*T at step s
+  const uint16_t* kp = Kc + int64_t(kvh / group) * S * kD;       // of kv head kvh / group
+  const uint16_t* vp = Vc + int64_t(kvh / group) * S * kD;
+  const int key0 = team * kChunk;                                // this team's chunk
 
   // q's load goes out before the first step's K and V, so waiting for q does not wait for them:
   // 16 bytes a lane, lanes past the G*16 vectors repeat the last one (the same value, and no
@@ -601,7 +567,7 @@ __global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t*
   const int qi = min(tid, G * kD / 8 - 1);
   const QVec qv = load_qvec(q, qi, qw, qcos, qsin);
   u32x4 kr[kChunk / 16], vr[kChunk / 16];
-  load_step(kp, vp, first * kChunk, S, kj, d8, kr, vr);
+  load_step(kp, vp, key0, S, kj, d8, kr, vr);
   float qf8[8];
   qvec_values(qv, qi, qw != nullptr, qeps, qf8);
   // lanes past the G*16 vectors hold repeats (whose norms are not their head's): they do not store
@@ -614,9 +580,7 @@ __global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t*
     lrun[team][ttid] = 0.f;
   }
   __syncthreads();
-  // one team: q in registers; several (up to 1024 threads, 128 VGPRs a lane): q read from LDS.
-  // Up to two teams: the next step's K and V load while this one computes.
-  constexpr bool kPrefetch = T <= 2;
+  // one team: q in registers; several (up to 1024 threads, 128 VGPRs a lane): q read from LDS
   float qf[T == 1 ? G : 1][8];
   if constexpr (T == 1) {
 #pragma unroll
@@ -630,20 +594,9 @@ __global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t*
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[gi][e] = 0.f;
 
-  for (int s = 0; s < steps; ++s) {
-    const int key0 = (first + s * T) * kChunk;
-    if constexpr (!kPrefetch) {
-      if (s > 0) load_step(kp, vp, key0, S, kj, d8, kr, vr);
-    }
-    u32x4 kc[kChunk / 16], vc[kChunk / 16];
-#pragma unroll
-    for (int pass = 0; pass < kChunk / 16; ++pass) {
-      kc[pass] = kr[pass];
-      vc[pass] = vr[pass];
-    }
-    if constexpr (kPrefetch) {
-      if (s + 1 < steps) load_step(kp, vp, key0 + T * kChunk, S, kj, d8, kr, vr);
-    }
+  {
+    const u32x4 (&kc)[kChunk / 16] = kr;
+    const u32x4 (&vc)[kChunk / 16] = vr;
 
 #pragma unroll
     for (int pass = 0; pass < kChunk / 16; ++pass) {
@@ -714,7 +667,6 @@ __global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t*
         for (int e = 0; e < 8; ++e) acc[gi][e] = __builtin_fmaf(p, vf[e], acc[gi][e]);
       }
     }
-    __syncthreads();   // ts and alpha are rewritten by the next step
   }
 
   // lanes l, l^16, l^32, l^48 hold the same dims; then each team's four waves meet in LDS
@@ -739,26 +691,17 @@ __global__ __launch_bounds__(kTeam * T) void attn_decode_partial(const uint16_t*
       wt[t][tid] = w;
       ll = __builtin_fmaf(lrun[t][tid], w, ll);
     }
-    mfin[tid] = mm;
     lfin[tid] = ll;
   }
   __syncthreads();
 
-  float* rec = nrec > 1 ? part + (int64_t(kvh) * nrec + range) * kRec : nullptr;
   for (int i = tid; i < G * kD; i += kTeam * T) {
     const int gi = i / kD, d = i % kD;
     float o = 0.f;
 #pragma unroll
     for (int t = 0; t < T; ++t)
       o = __builtin_fmaf(wt[t][gi], (red[t][0][gi][d] + red[t][1][gi][d]) + (red[t][2][gi][d] + red[t][3][gi][d]), o);
-    if (nrec == 1)
-      O[(int64_t(kvh) * G + gi) * kD + d] = f32_to_bf16(o / lfin[gi]);
-    else
-      rec[i] = o;
-  }
-  if (nrec > 1 && tid < G) {
-    rec[G * kD + tid] = mfin[tid];
-    rec[G * kD + G + tid] = lfin[tid];
+    O[(int64_t(kvh) * G + gi) * kD + d] = f32_to_bf16(o / lfin[gi]);
   }
 }
 
@@ -1050,13 +993,6 @@ struct QNorm {
   float eps;
 };
 
-template <int G, int T>
-void launch_partial(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* part, int nkv,
-                    int seq, float c, const DecodePlan& p, const QNorm& qn, hipStream_t s) {
-  attn_decode_partial<G, T><<<dim3(unsigned(p.records), unsigned(nkv * p.gsplit)), dim3(kTeam * T), 0, s>>>(
-      q, k, v, o, part, seq, c, p.steps, p.gsplit, qn.w, qn.cos, qn.sin, qn.eps);
-}
-
 // The matrix-core form's cut of a kv head: `records` ranges of `steps` 32-key steps each (n steps in
 // all): ceil(n / 48) steps a range below 256 steps, ceil(n / 64) from there, so a head has at most
 // 64 ranges (the merge pass takes up to kMaxRecords).  Measured on MI355X (8 kv heads, graph
@@ -1083,19 +1019,12 @@ void launch_attn_decode_mfma(const uint16_t* q, const uint16_t* k, const uint16_
   if (p.records > 1) attn_decode_merge<G><<<dim3(unsigned(nkv), unsigned(G)), dim3(256), 0, s>>>(part, o, p.records);
 }
 
-// G: query rows per workgroup (the kv head's group / p.gsplit)
-template <int G>
-void launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* part, int nkv,
-                        int seq, float c, const DecodePlan& p, const QNorm& qn, hipStream_t s) {
-  if (p.teams == 1) {
-    launch_partial<G, 1>(q, k, v, o, part, nkv, seq, c, p, qn, s);
-  } else if (p.teams == 2) {
-    launch_partial<G, 2>(q, k, v, o, part, nkv, seq, c, p, qn, s);
-  } else {
-    if constexpr (G <= 3) launch_partial<G, 4>(q, k, v, o, part, nkv, seq, c, p, qn, s);
-  }
-  if (p.records > 1)
-    attn_decode_merge<G><<<dim3(unsigned(nkv * p.gsplit), unsigned(G)), dim3(256), 0, s>>>(part, o, p.records);
+// The VALU form: one query row a workgroup, T teams (small_teams), o written in the same launch.
+template <int T>
+void launch_attn_decode_small(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int nkv, int group,
+                              int seq, float c, const QNorm& qn, hipStream_t s) {
+  attn_decode_partial<1, T><<<dim3(unsigned(nkv * group)), dim3(kTeam * T), 0, s>>>(q, k, v, o, seq, c, group, qn.w,
+                                                                                      qn.cos, qn.sin, qn.eps);
 }
 
 }  // namespace
@@ -1155,14 +1084,10 @@ PTB_EXPORT int ptb_gemv_silu_parts_bf16(const float* gate_up_parts, int64_t gate
 
 PTB_EXPORT size_t ptb_attn_decode_workspace_bytes(int64_t nkv, int64_t group, int64_t seq) {
   if (nkv <= 0 || group <= 0 || seq <= 0 || seq >= (int64_t(1) << 30)) return 0;
-  if (seq > kWaveMinSeq) {
-    const WavePlan w = wave_plan(seq);
-    if (w.records == 1) return 0;
-    return size_t(nkv * w.records * record_floats(group)) * sizeof(float);
-  }
-  const DecodePlan p = decode_plan(seq, group);
-  if (p.records == 1) return 0;
-  return size_t(nkv * p.gsplit * p.records * record_floats(group / p.gsplit)) * sizeof(float);
+  if (seq <= kWaveMinSeq) return 0;   // the VALU form's single launch
+  const WavePlan w = wave_plan(seq);
+  if (w.records == 1) return 0;
+  return size_t(nkv * w.records * record_floats(group)) * sizeof(float);
 }
 
 static int attn_decode_entry(const void* q, const void* k, const void* v, void* o, int64_t nkv, int64_t group,
@@ -1198,15 +1123,10 @@ static int attn_decode_entry(const void* q, const void* k, const void* v, void* 
     }
     return launch_status();
   }
-  const DecodePlan p = decode_plan(seq, group);
-  if (nkv * p.gsplit > 65535) return PTB_ERR_GRID;
-  switch (group / p.gsplit) {
-    case 1: launch_attn_decode<1>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
-    case 2: launch_attn_decode<2>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
-    case 3: launch_attn_decode<3>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
-    case 4: launch_attn_decode<4>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
-    case 6: launch_attn_decode<6>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
-    default: launch_attn_decode<8>(qp, kp, vp, op, ws, int(nkv), int(seq), c, p, qn, s); break;
+  switch (small_teams(seq)) {
+    case 1: launch_attn_decode_small<1>(qp, kp, vp, op, int(nkv), int(group), int(seq), c, qn, s); break;
+    case 2: launch_attn_decode_small<2>(qp, kp, vp, op, int(nkv), int(group), int(seq), c, qn, s); break;
+    default: launch_attn_decode_small<4>(qp, kp, vp, op, int(nkv), int(group), int(seq), c, qn, s); break;
   }
   return launch_status();
 }
