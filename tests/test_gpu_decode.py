@@ -124,8 +124,8 @@ def test_attention_decode_range_plans(nkv, g, s):
     ending in a step past S), eight (16384), five (9000: pairs, then a single step), twenty (40000),
     sixty-four (131072 keys, 64 ranges),
     two (3000), one (300, and 257 keys, whose last range holds one key); caches of at most 256 keys
-    (one pass of the VALU form): one chunk, four teams (G = 3), one row a workgroup with two and
-    four teams (G = 8), and 2400 row workgroups (300 heads x 8); G = 1, 2, 3, 4, 6 and 8."""
+    (one pass of the VALU form, a workgroup per query row): one team (64 and 40 keys), two (100)
+    and four (250 and 256 keys), and 2400 row workgroups (300 heads x 8); G = 1, 2, 3, 4, 6 and 8."""
     q, k, v = randn((nkv, g, 128), 20), randn((nkv, s, 128), 21), randn((nkv, s, 128), 22)
     got = ops.attention_decode(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
     assert_close(got, oracle.attention_decode(q, k, v), RTOL, 2e-2, f"decode plan {nkv}x{g}x{s}")
